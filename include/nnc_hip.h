@@ -1,0 +1,102 @@
+/*
+ * nnc_hip.h - lifecycle, memory and measurement entry points of
+ * libnnc_hip.so, the gfx950 (MI355X) implementation of the nnc operator ABI
+ * declared in nnc_ops.h.
+ *
+ * The reference has no device: generated tensors.c points every Tensor into a
+ * static host pool (codegen/x86_emitters/tensors.py:589-600, 826-868) and
+ * constants_loader.c fread()s weights into static arrays
+ * (x86_emitters/constants_loader.py:196-291). The HIP target keeps the memory
+ * plan (cost_aware offsets) but places it in ONE hipMalloc'd HBM arena:
+ *
+ *     nnc_hip_init(0);
+ *     nnc_hip_arena_reserve(NNC_MEMORY_SIZE);   // one allocation
+ *     nnc_hip_bind(&tensor_x, OFFSET_x);        // per tensor, at load time
+ *     nnc_hip_upload(&tensor_w, host_bytes);    // constants, inputs
+ *     nnc_run();                                // enqueues nnc_* kernels
+ *     nnc_hip_download(&tensor_output, host);   // waits, copies back
+ *
+ * All calls are made from one host thread at a time per device (the O0-O2
+ * generated code is serial, c_emitter.py:832-847). Return codes: 0 = success,
+ * otherwise an NNC_HIP_E* value, also kept for nnc_hip_last_error().
+ */
+#ifndef NNC_HIP_H
+#define NNC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include "nnc_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    NNC_HIP_OK = 0,
+    NNC_HIP_EINVAL = 1,   /* bad argument (NULL tensor, bad rank, shape) */
+    NNC_HIP_ENOMEM = 2,   /* device allocation failed / arena too small  */
+    NNC_HIP_EDEVICE = 3,  /* a HIP runtime call failed                   */
+    NNC_HIP_EUNSUPP = 4,  /* argument combination not implemented        */
+    NNC_HIP_ESTATE = 5    /* called before nnc_hip_init                  */
+};
+
+/* Select the device, create the library stream (default priority) and the
+ * per-device workspace. Idempotent for the same device. */
+int nnc_hip_init(int device);
+/* Wait for all work, free the arena, workspace and stream. */
+void nnc_hip_shutdown(void);
+
+/* ---- the HBM arena ----------------------------------------------------- */
+/* Reserve the arena with one hipMalloc (256-byte aligned base). Calling it
+ * again with a larger size replaces the arena (previous bindings dangle). */
+int nnc_hip_arena_reserve(size_t bytes);
+void* nnc_hip_arena_base(void);
+size_t nnc_hip_arena_size(void);
+/* t->data = arena + offset; fails if [offset, offset + t->nbytes) is outside
+ * the arena or offset is not 16-byte aligned. */
+int nnc_hip_bind(Tensor* t, size_t offset);
+
+/* ---- explicit allocations (tests and callers without an arena) --------- */
+void* nnc_hip_malloc(size_t bytes);
+void nnc_hip_free(void* ptr);
+
+/* ---- host <-> device (synchronous with respect to the library stream) -- */
+int nnc_hip_upload(Tensor* t, const void* host_src);    /* t->nbytes bytes */
+int nnc_hip_download(const Tensor* t, void* host_dst);  /* t->nbytes bytes */
+int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int nnc_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+
+/* ---- synchronisation and errors ---------------------------------------- */
+int nnc_hip_sync(void);             /* waits for the library stream */
+void* nnc_hip_stream(void);         /* the hipStream_t, for callers that
+                                       order their own work after ours */
+int nnc_hip_last_error(void);       /* last non-zero code since reset */
+const char* nnc_hip_last_error_message(void);
+void nnc_hip_clear_error(void);
+
+/* ---- per-kernel timing --------------------------------------------------
+ * While enabled, every kernel launch is bracketed by hipEvents recorded on
+ * the library stream; durations accumulate per kernel name. Reading the
+ * table synchronises. Used by bench.py for the roofline figures. */
+void nnc_hip_profile_enable(int on);
+void nnc_hip_profile_reset(void);
+int nnc_hip_profile_count(void);
+/* Entry i: copies the kernel name (NUL-terminated, truncated to cap), the
+ * number of launches and the summed milliseconds. Returns 0 on success. */
+int nnc_hip_profile_entry(int i, char* name, int cap, int64_t* launches,
+                          double* total_ms);
+
+/* ---- launch capture ------------------------------------------------------
+ * Record every kernel the following nnc_* calls enqueue into a hipGraph and
+ * replay it with one launch. Between begin and end nothing executes. The
+ * graph keeps the device pointers of the captured calls. */
+int nnc_hip_graph_begin(void);
+int nnc_hip_graph_end(void);
+int nnc_hip_graph_launch(void);
+void nnc_hip_graph_destroy(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NNC_HIP_H */

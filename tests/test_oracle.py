@@ -1,0 +1,269 @@
+"""Pin the CPU oracle (oracle/nnc_oracle.c).
+
+1. Bit-for-bit against the golden vectors, which the reference runtime itself
+   produced (tests/golden/make_golden.py).
+2. Bit-for-bit against the reference runtime on fresh random cases, where
+   oracle/_ref is built.
+3. Against closed forms that a plausible restatement mistake (dropped term,
+   swapped index, transposed operand, wrong pad side) would break.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import caserun
+from conftest import GOLDEN
+
+F32 = np.float32
+
+
+@pytest.mark.parametrize("case", GOLDEN, ids=[c["name"] for c in GOLDEN])
+def test_oracle_matches_reference_golden(case, oracle_lib, abi):
+    got = caserun.run_case(oracle_lib, case, abi)
+    for key, exp in case["expected"].items():
+        assert caserun.same_bits(got[key], exp), f"{case['name']}:{key} differs from reference"
+
+
+# ---------------------------------------------------------------------------
+# fresh random cases, oracle vs reference (bit-exact)
+# ---------------------------------------------------------------------------
+def _conv_case(rng, op, n, ci, h, w, co, kh, kw, sh, sw, ph, pw, bias=True):
+    ho = (h + 2 * ph - kh) // sh + 1
+    wo = (w + 2 * pw - kw) // sw + 1
+    t = {"x": rng.standard_normal((n, ci, h, w)).astype(F32),
+         "w": rng.standard_normal((co, ci, kh, kw)).astype(F32),
+         "out": np.zeros((n, co, ho, wo), F32)}
+    args = [("t", "x"), ("t", "w")]
+    if bias:
+        t["b"] = rng.standard_normal((co,)).astype(F32)
+        args.append(("t", "b"))
+    else:
+        args.append(("null",))
+    args += [("t", "out"), ("i", kh), ("i", kw), ("i", sh), ("i", sw), ("i", ph), ("i", pw)]
+    return {"name": "rand", "op": op, "tensors": t, "args": args, "outputs": ["out"]}
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_oracle_conv_random_vs_reference(seed, oracle_lib, ref_lib, abi):
+    rng = np.random.default_rng(1000 + seed)
+    kh = int(rng.integers(1, 6))
+    kw = int(rng.integers(1, 6))
+    sh, sw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+    ph, pw = int(rng.integers(0, kh)), int(rng.integers(0, kw))
+    c = _conv_case(rng, ["nnc_conv", "nnc_conv_relu", "nnc_conv_sigmoid"][seed % 3],
+                   int(rng.integers(1, 3)), int(rng.integers(1, 5)), int(rng.integers(kh, 12)),
+                   int(rng.integers(kw, 12)), int(rng.integers(1, 6)), kh, kw, sh, sw, ph, pw,
+                   bias=bool(seed % 2))
+    a = caserun.run_case(oracle_lib, c, abi)["out"]
+    b = caserun.run_case(ref_lib, c, abi)["out"]
+    assert caserun.same_bits(a, b)
+
+
+@pytest.mark.parametrize("shape", [(56, 56), (28, 28), (7, 7), (3, 3), (2, 9)])
+def test_oracle_conv3x3_fast_paths_vs_reference(shape, oracle_lib, ref_lib, abi):
+    """The reference 3x3 s1/s2 paths use SSE2 interiors and border fallbacks;
+    the oracle's single loop must agree with every one of them."""
+    rng = np.random.default_rng(sum(shape))
+    for op, s in (("nnc_conv", 1), ("nnc_conv", 2), ("nnc_conv_relu", 1)):
+        c = _conv_case(rng, op, 1, 3, shape[0], shape[1], 4, 3, 3, s, s, 1, 1)
+        assert caserun.same_bits(caserun.run_case(oracle_lib, c, abi)["out"],
+                                 caserun.run_case(ref_lib, c, abi)["out"])
+    c = _conv_case(rng, "nnc_conv7x7_s2", 1, 3, shape[0] + 6, shape[1] + 6, 2, 7, 7, 2, 2, 3, 3)
+    c["args"] = c["args"][:4]
+    assert caserun.same_bits(caserun.run_case(oracle_lib, c, abi)["out"],
+                             caserun.run_case(ref_lib, c, abi)["out"])
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_oracle_matmul_gemm_random_vs_reference(seed, oracle_lib, ref_lib, abi):
+    rng = np.random.default_rng(2000 + seed)
+    M, K, N = (int(v) for v in rng.integers(1, 40, 3))
+    mm = {"name": "mm", "op": "nnc_matmul",
+          "tensors": {"a": rng.standard_normal((M, K)).astype(F32),
+                      "b": rng.standard_normal((K, N)).astype(F32), "out": np.zeros((M, N), F32)},
+          "args": [("t", "a"), ("t", "b"), ("t", "out")], "outputs": ["out"]}
+    assert caserun.same_bits(caserun.run_case(oracle_lib, mm, abi)["out"],
+                             caserun.run_case(ref_lib, mm, abi)["out"])
+    ta, tb = seed % 2, seed // 2
+    g = {"name": "g", "op": "nnc_gemm",
+         "tensors": {"a": rng.standard_normal((K, M) if ta else (M, K)).astype(F32),
+                     "b": rng.standard_normal((N, K) if tb else (K, N)).astype(F32),
+                     "c": rng.standard_normal((M, N)).astype(F32), "out": np.zeros((M, N), F32)},
+         "args": [("t", "a"), ("t", "b"), ("t", "c"), ("t", "out"), ("f", 0.75), ("f", -1.5),
+                  ("i", ta), ("i", tb)], "outputs": ["out"]}
+    assert caserun.same_bits(caserun.run_case(oracle_lib, g, abi)["out"],
+                             caserun.run_case(ref_lib, g, abi)["out"])
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_oracle_rowwise_random_vs_reference(seed, oracle_lib, ref_lib, abi):
+    rng = np.random.default_rng(3000 + seed)
+    shape = tuple(int(v) for v in rng.integers(1, 9, 3))
+    axis = int(rng.integers(-3, 3))
+    x = (rng.standard_normal(shape) * 4).astype(F32)
+    red_shape = list(shape)
+    red_shape[axis] = 1
+    for op, t, args in [
+        ("nnc_softmax", {"x": x, "out": np.zeros_like(x)}, [("t", "x"), ("t", "out"), ("i", axis)]),
+        ("nnc_reducesum", {"x": x, "out": np.zeros(red_shape, F32)},
+         [("t", "x"), ("t", "out"), ("i", axis), ("i", 1)]),
+        ("nnc_reducemean", {"x": x, "out": np.zeros(red_shape, F32)},
+         [("t", "x"), ("t", "out"), ("i", axis), ("i", 0)]),
+        ("nnc_layernorm", {"x": x, "g": rng.standard_normal(shape[axis]).astype(F32),
+                           "b": rng.standard_normal(shape[axis]).astype(F32), "out": np.zeros_like(x)},
+         [("t", "x"), ("t", "g"), ("t", "b"), ("t", "out"), ("i", axis), ("f", 1e-5)]),
+    ]:
+        c = {"name": op, "op": op, "tensors": t, "args": args, "outputs": ["out"]}
+        assert caserun.same_bits(caserun.run_case(oracle_lib, c, abi)["out"],
+                                 caserun.run_case(ref_lib, c, abi)["out"]), op
+
+
+# ---------------------------------------------------------------------------
+# closed forms (no reference needed)
+# ---------------------------------------------------------------------------
+def _np_conv_f64(x, w, b, sh, sw, ph, pw, ho, wo):
+    """float64 direct convolution with top/left padding; fp32 products are exact
+    in float64, so rounding the float64 sum once reproduces a float64
+    accumulator up to summation order (within 1 ulp for these sizes)."""
+    n, ci, h, ww = x.shape
+    co, _, kh, kw = w.shape
+    pad = np.zeros((n, ci, max(h + 2 * ph, (ho - 1) * sh + kh) + kh, max(ww + 2 * pw, (wo - 1) * sw + kw) + kw))
+    pad[:, :, ph:ph + h, pw:pw + ww] = x
+    out = np.zeros((n, co, ho, wo))
+    for r in range(kh):
+        for c in range(kw):
+            patch = pad[:, :, r:r + (ho - 1) * sh + 1:sh, c:c + (wo - 1) * sw + 1:sw]
+            out += np.einsum("nchw,oc->nohw", patch, w[:, :, r, c].astype(np.float64))
+    if b is not None:
+        out += b.astype(np.float64)[None, :, None, None]
+    return out
+
+
+@pytest.mark.parametrize("spec", [(3, 3, 1, 1, 1, 1), (3, 3, 2, 2, 1, 1), (1, 1, 2, 2, 0, 0),
+                                  (7, 7, 2, 2, 3, 3), (5, 5, 1, 1, 2, 2), (3, 5, 2, 1, 1, 2)])
+def test_oracle_conv_closed_form(spec, oracle_lib, abi):
+    kh, kw, sh, sw, ph, pw = spec
+    rng = np.random.default_rng(kh * 100 + kw)
+    c = _conv_case(rng, "nnc_conv", 2, 3, 11, 10, 5, kh, kw, sh, sw, ph, pw)
+    got = caserun.run_case(oracle_lib, c, abi)["out"]
+    t = c["tensors"]
+    ref = _np_conv_f64(t["x"], t["w"], t["b"], sh, sw, ph, pw, got.shape[2], got.shape[3])
+    np.testing.assert_allclose(got, ref.astype(F32), rtol=2e-7, atol=1e-6)
+
+
+def test_oracle_conv_pad_only_top_left(oracle_lib, abi):
+    """Output extent decides the bottom/right padding (c_emitter.py:1051-1058):
+    an output one row shorter than 'same' must equal the same-pad result
+    cropped, not a shifted window."""
+    rng = np.random.default_rng(5)
+    c = _conv_case(rng, "nnc_conv", 1, 2, 6, 6, 3, 3, 3, 1, 1, 1, 1)
+    full = caserun.run_case(oracle_lib, c, abi)["out"]
+    c2 = dict(c)
+    c2["tensors"] = dict(c["tensors"], out=np.zeros((1, 3, 5, 5), F32))
+    crop = caserun.run_case(oracle_lib, c2, abi)["out"]
+    assert caserun.same_bits(crop, full[:, :, :5, :5].copy())
+
+
+def test_oracle_gemm_closed_form(oracle_lib, abi):
+    rng = np.random.default_rng(9)
+    for ta in (0, 1):
+        for tb in (0, 1):
+            M, K, N = 7, 13, 5
+            a = rng.uniform(-1, 1, (K, M) if ta else (M, K)).astype(F32)
+            b = rng.uniform(-1, 1, (N, K) if tb else (K, N)).astype(F32)
+            cvec = rng.uniform(-1, 1, (N,)).astype(F32)
+            c = {"name": "g", "op": "nnc_gemm",
+                 "tensors": {"a": a, "b": b, "c": cvec, "out": np.zeros((M, N), F32)},
+                 "args": [("t", "a"), ("t", "b"), ("t", "c"), ("t", "out"), ("f", 2.0), ("f", 0.5),
+                          ("i", ta), ("i", tb)], "outputs": ["out"]}
+            got = caserun.run_case(oracle_lib, c, abi)["out"]
+            A = (a.T if ta else a).astype(np.float64)
+            B = (b.T if tb else b).astype(np.float64)
+            ref = (2.0 * (A @ B) + 0.5 * cvec.astype(np.float64)).astype(F32)
+            np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_oracle_matmul_batched_reproduces_reference_stepping(oracle_lib, abi):
+    """The reference advances A and B by their batch COUNT per batch
+    (ops.c:1687-1704); batch 0 is a true product, later batches are shifted
+    windows. The oracle must show exactly that."""
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal((3, 4, 5)).astype(F32)
+    b = rng.standard_normal((3, 5, 6)).astype(F32)
+    c = {"name": "bm", "op": "nnc_matmul",
+         "tensors": {"a": a, "b": b, "out": np.zeros((3, 4, 6), F32)},
+         "args": [("t", "a"), ("t", "b"), ("t", "out")], "outputs": ["out"]}
+    got = caserun.run_case(oracle_lib, c, abi)["out"]
+    np.testing.assert_allclose(got[0], a[0] @ b[0], rtol=1e-5, atol=1e-5)
+    fa, fb = a.ravel(), b.ravel()
+    a1 = fa[3:3 + 20].reshape(4, 5)
+    b1 = fb[3:3 + 30].reshape(5, 6)
+    np.testing.assert_allclose(got[1], a1 @ b1, rtol=1e-5, atol=1e-5)
+
+
+def test_oracle_softmax_and_layernorm_invariants(oracle_lib, abi):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((16, 100)) * 5).astype(F32)
+    c = {"name": "s", "op": "nnc_softmax", "tensors": {"x": x, "out": np.zeros_like(x)},
+         "args": [("t", "x"), ("t", "out"), ("i", -1)], "outputs": ["out"]}
+    p = caserun.run_case(oracle_lib, c, abi)["out"].astype(np.float64)
+    np.testing.assert_allclose(p.sum(1), 1.0, atol=1e-5)
+    e = np.exp(x.astype(np.float64) - x.max(1, keepdims=True))
+    np.testing.assert_allclose(p, e / e.sum(1, keepdims=True), rtol=1e-5, atol=1e-7)
+    g = rng.standard_normal(100).astype(F32)
+    bb = rng.standard_normal(100).astype(F32)
+    c = {"name": "l", "op": "nnc_layernorm",
+         "tensors": {"x": x, "g": g, "b": bb, "out": np.zeros_like(x)},
+         "args": [("t", "x"), ("t", "g"), ("t", "b"), ("t", "out"), ("i", -1), ("f", 1e-5)],
+         "outputs": ["out"]}
+    y = caserun.run_case(oracle_lib, c, abi)["out"].astype(np.float64)
+    xd = x.astype(np.float64)
+    ref = (xd - xd.mean(1, keepdims=True)) / np.sqrt(xd.var(1, keepdims=True) + 1e-5) * g + bb
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_oracle_pools_and_copies_closed_form(oracle_lib, abi):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 3, 9, 8)).astype(F32)
+    c = {"name": "mp", "op": "nnc_maxpool2d",
+         "tensors": {"x": x, "out": np.zeros((2, 3, 5, 4), F32)},
+         "args": [("t", "x"), ("t", "out"), ("i", 3), ("i", 3), ("i", 2), ("i", 2), ("i", 1), ("i", 1)],
+         "outputs": ["out"]}
+    got = caserun.run_case(oracle_lib, c, abi)["out"]
+    pad = np.full((2, 3, 12, 11), -np.inf, F32)
+    pad[:, :, 1:10, 1:9] = x
+    ref = np.stack([np.stack([pad[:, :, 2 * i:2 * i + 3, 2 * j:2 * j + 3].max((2, 3)) for j in range(4)], -1)
+                    for i in range(5)], -2)
+    assert caserun.same_bits(got, ref.astype(F32))
+    c = {"name": "ap", "op": "nnc_avgpool2d",
+         "tensors": {"x": x, "out": np.zeros((2, 3, 1, 1), F32)},
+         "args": [("t", "x"), ("t", "out"), ("i", 9), ("i", 8), ("i", 9), ("i", 8), ("i", 0), ("i", 0)],
+         "outputs": ["out"]}
+    got = caserun.run_case(oracle_lib, c, abi)["out"]
+    np.testing.assert_allclose(got[..., 0, 0], x.astype(np.float64).mean((2, 3)), rtol=1e-5, atol=1e-6)
+    perm = (0, 2, 3, 1)
+    c = {"name": "tr", "op": "nnc_transpose",
+         "tensors": {"x": x, "out": np.zeros(tuple(x.shape[p] for p in perm), F32)},
+         "args": [("t", "x"), ("t", "out"), ("i64", list(perm)), ("i", 4)], "outputs": ["out"]}
+    assert caserun.same_bits(caserun.run_case(oracle_lib, c, abi)["out"], np.transpose(x, perm).copy())
+    parts = [rng.standard_normal((2, k, 3)).astype(F32) for k in (1, 4, 2)]
+    t = {f"p{i}": p for i, p in enumerate(parts)}
+    t["out"] = np.zeros((2, 7, 3), F32)
+    c = {"name": "cc", "op": "nnc_concat", "tensors": t,
+         "args": [("tl", ["p0", "p1", "p2"]), ("t", "out"), ("i", 3), ("i", 1)], "outputs": ["out"]}
+    assert caserun.same_bits(caserun.run_case(oracle_lib, c, abi)["out"], np.concatenate(parts, 1))
+
+
+def test_oracle_binary_flat_modulo_rule(oracle_lib, abi):
+    a = np.arange(8, dtype=F32).reshape(2, 4)
+    b = np.array([10.0, 20.0], F32)
+    c = {"name": "fm", "op": "nnc_add", "tensors": {"a": a, "b": b, "out": np.zeros_like(a)},
+         "args": [("t", "a"), ("t", "b"), ("t", "out")], "outputs": ["out"]}
+    got = caserun.run_case(oracle_lib, c, abi)["out"].ravel()
+    assert got.tolist() == [10, 21, 12, 23, 14, 25, 16, 27]  # b[i % 2], not numpy's rule
+    c["tensors"] = {"a": np.arange(3, dtype=F32), "b": np.arange(5, dtype=F32),
+                    "out": np.full(8, -1.0, F32)}
+    got = caserun.run_case(oracle_lib, c, abi)["out"]
+    assert got.tolist() == [0, 2, 4, -1, -1, -1, -1, -1]  # only min(3,5,8) written
