@@ -156,11 +156,12 @@ void nnc_add_relu(Tensor* a, Tensor* b, Tensor* out);    /* s > 0 ? s : 0 */
 void nnc_add_sigmoid(Tensor* a, Tensor* b, Tensor* out);
 
 /* ---- MatMul + Relu -------------------------------------------------------
- * The reference code generator emits this call for the matmul_relu fusion
- * pattern (c_emitter.py:1143-1171, fusion_patterns.py:145-153) but no
- * reference runtime defines it, so such models fail to link there. Defined
- * here as relu(nnc_matmul(a, b)) so the fused O3 output links. */
-void nnc_matmul_relu(Tensor* a, Tensor* b, Tensor* output);
+ * The reference code generator emits this call, with the argument list
+ * (a, b, bias or NULL, output), for the matmul_relu fusion pattern
+ * (c_emitter.py:1143-1171, fusion_patterns.py:145-153), but no reference
+ * runtime defines it, so such models fail to link there. Defined here as
+ * relu(nnc_matmul(a, b) + bias), bias being [N] (per column) or [M, N]. */
+void nnc_matmul_relu(Tensor* a, Tensor* b, Tensor* bias, Tensor* output);
 
 #ifdef __cplusplus
 }

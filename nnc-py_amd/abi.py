@@ -90,7 +90,7 @@ SIGNATURES: dict[str, list] = {
     "nnc_unsqueeze": [TP, TP, c_int],
     "nnc_tile": [TP, TP, I64P, c_int],
     "nnc_matmul": [TP, TP, TP],
-    "nnc_matmul_relu": [TP, TP, TP],
+    "nnc_matmul_relu": [TP, TP, TP, TP],
     "nnc_gemm": [TP, TP, TP, TP, c_float, c_float, c_int, c_int],
     "nnc_gemm_nt": [TP, TP, TP, TP, c_float, c_float],
     "nnc_reducemean": [TP, TP, c_int, c_int],

@@ -1,0 +1,103 @@
+// Internal header of libnnc_hip.so: device context, error reporting, launch
+// wrapper with optional per-kernel timing, small tensor helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "nnc_hip.h"
+#include "nnc_ops.h"
+
+namespace nnc {
+
+// ---------------------------------------------------------------------------
+// device context (one per process; the generated code drives one device)
+// ---------------------------------------------------------------------------
+struct Context {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    char* arena = nullptr;
+    size_t arena_bytes = 0;
+    // split-K partials and other per-call scratch; grown outside capture only
+    float* workspace = nullptr;
+    size_t workspace_bytes = 0;
+    bool capturing = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    bool profiling = false;
+    int cu_count = 256;
+};
+
+Context& ctx();
+
+// Returns false (and records NNC_HIP_ESTATE) if nnc_hip_init has not run.
+bool ready(const char* who);
+
+// Record an error code + message (printed once to stderr, kept for
+// nnc_hip_last_error()).
+void fail(int code, const char* who, const char* fmt, ...);
+
+// Check a HIP runtime call; on failure record NNC_HIP_EDEVICE.
+bool hip_ok(hipError_t e, const char* who, const char* what);
+
+// Ensure the workspace holds at least `bytes`; returns nullptr if it cannot
+// (inside graph capture the workspace cannot grow).
+float* workspace(size_t bytes);
+size_t workspace_capacity();
+
+// ---------------------------------------------------------------------------
+// kernel launch with optional hipEvent timing (keyed by kernel name)
+// ---------------------------------------------------------------------------
+struct TimedScope {
+    const char* name;
+    hipEvent_t start = nullptr, stop = nullptr;
+    explicit TimedScope(const char* n);
+    ~TimedScope();
+};
+
+template <typename Kernel, typename... Args>
+inline void launch(const char* name, Kernel kernel, dim3 grid, dim3 block, size_t lds,
+                   Args... args) {
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) return;
+    TimedScope scope(name);
+    hipLaunchKernelGGL(kernel, grid, block, lds, ctx().stream, args...);
+    hip_ok(hipGetLastError(), name, "launch");
+}
+
+// Copy `bytes` bytes device-to-device on the library stream with a kernel
+// (16-byte vector path when aligned; no memset/memcpy nodes under capture).
+// src == dst is a no-op. Defined in movement.hip.
+void device_copy(const char* name, const void* src, void* dst, size_t bytes);
+
+// ---------------------------------------------------------------------------
+// tensor helpers (host side)
+// ---------------------------------------------------------------------------
+inline int64_t numel(const Tensor* t) {
+    int64_t n = 1;
+    for (int d = 0; d < t->ndim; ++d) n *= t->shape[d];
+    return n;
+}
+
+inline int64_t prod(const int64_t* s, int lo, int hi) {
+    int64_t p = 1;
+    for (int d = lo; d < hi; ++d) p *= s[d];
+    return p;
+}
+
+inline bool has_data(const Tensor* t) { return t && t->data && (t->shape || t->ndim == 0); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Grid size for a grid-stride element-wise kernel over n items with `per`
+// items per thread.
+inline unsigned grid_for(int64_t n, int per, int block = 256) {
+    int64_t g = ceil_div(ceil_div(n, per), block);
+    const int64_t cap = (int64_t)ctx().cu_count * 16;
+    if (g > cap) g = cap;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+}  // namespace nnc

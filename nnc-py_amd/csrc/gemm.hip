@@ -1,0 +1,542 @@
+// Gemm, Gemm_nt and MatMul of the nnc ABI (runtime/x86/ops.c:1607-1886).
+//
+// Dense products run on the fp32 MFMA tile engine (mfma_tile.h) with one of
+// four operand layouts per side (k-contiguous or x-contiguous, 16-byte or
+// scalar loads), optional batching (grid.y) and split-K. Products with one
+// output row or column are HBM-bound and use dedicated kernels:
+//   gemv_xc_k  out[j] = sum_k a[k] * B[k][j]   (B row-major; float4 columns,
+//              K split across workgroups, deterministic partial reduction)
+//   dot_k      out[i][j] = sum_k A[i][k] * B[j][k]  (both k-contiguous; one
+//              wave per output, shuffle reduction)
+//
+// The reference accumulates Gemm in fp64 and MatMul with a Kahan fp32 sum;
+// here every product accumulates in fp32 (two-level for MFMA tiles), within
+// the 1e-4 absolute / 1e-3 relative bar.
+//
+// DIVERGES: batched MatMul steps A by M*K and B by K*N per batch (numpy /
+// ONNX semantics). The reference steps by the batch count (ops.c:1687-1704),
+// which is only correct for a single batch.
+#include "mfma_tile.h"
+
+namespace nnc {
+
+struct GemmArgs {
+    const float* A;
+    const float* B;
+    const float* C;
+    float* out;
+    float* ws;
+    int M, N, K;
+    int64_t lda, ldb, sa, sb, so;
+    float alpha, beta;
+    int c_mode;  // 0 none, 1 C[j], 2 C[i*N + j]
+    int relu;
+    int tiles_m, tiles_n, splits, k_per_split;
+};
+
+__device__ __forceinline__ float gemm_finish(const GemmArgs& g, int i, int j, float v) {
+    float o = g.alpha * v;
+    if (g.c_mode == 1) o += g.beta * g.C[j];
+    else if (g.c_mode == 2) o += g.beta * g.C[(int64_t)i * g.N + j];
+    if (g.relu) o = o > 0.0f ? o : 0.0f;
+    return o;
+}
+
+// Loader kinds: element (x, k) at base[x*ld + k] (K*) or base[k*ld + x] (X*)
+enum LoadKind { kKC4 = 0, kKC = 1, kXC4 = 2, kXC = 3 };
+
+template <int KIND, int X, int BK, int LD>
+struct PickLoader;
+template <int X, int BK, int LD>
+struct PickLoader<kKC4, X, BK, LD> {
+    typedef KContigLoader4<X, BK, LD> type;
+    static __device__ int64_t offset(int x0, int64_t ld) { return (int64_t)x0 * ld; }
+};
+template <int X, int BK, int LD>
+struct PickLoader<kKC, X, BK, LD> {
+    typedef KContigLoader<X, BK, LD> type;
+    static __device__ int64_t offset(int x0, int64_t ld) { return (int64_t)x0 * ld; }
+};
+template <int X, int BK, int LD>
+struct PickLoader<kXC4, X, BK, LD> {
+    typedef XContigLoader4<X, BK, LD> type;
+    static __device__ int64_t offset(int x0, int64_t) { return x0; }
+};
+template <int X, int BK, int LD>
+struct PickLoader<kXC, X, BK, LD> {
+    typedef XContigLoader<X, BK, LD> type;
+    static __device__ int64_t offset(int x0, int64_t) { return x0; }
+};
+
+template <class T, int AK, int BKIND>
+__global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g) {
+    __shared__ float lds[T::LDS_FLOATS];
+    float* As = lds;
+    float* Bs = lds + T::BK * T::LDA;
+    const int total = g.tiles_m * g.tiles_n * g.splits;
+    const int lin = xcd_remap(blockIdx.x, total);
+    const int mt = lin % g.tiles_m;
+    const int rest = lin / g.tiles_m;
+    const int nt = rest % g.tiles_n;
+    const int s = rest / g.tiles_n;
+    const int batch = blockIdx.y;
+    const int i0 = mt * T::BM, j0 = nt * T::BN;
+    const int kb = s * g.k_per_split;
+    const int ke = min(g.K, kb + g.k_per_split);
+
+    typedef PickLoader<AK, T::BM, T::BK, T::LDA> PA;
+    typedef PickLoader<BKIND, T::BN, T::BK, T::LDB> PB;
+    typename PA::type la;
+    typename PB::type lb;
+    la.init(g.A + batch * g.sa + PA::offset(i0, g.lda), g.lda, g.M - i0, g.K);
+    lb.init(g.B + batch * g.sb + PB::offset(j0, g.ldb), g.ldb, g.N - j0, g.K);
+
+    floatx16 sum[T::TM][T::TN];
+    mfma_mainloop<T>(la, lb, kb, ke, As, Bs, sum);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wi = (wave / T::WN) * T::WAVE_M;
+    const int wj = (wave % T::WN) * T::WAVE_N;
+#pragma unroll
+    for (int tn = 0; tn < T::TN; ++tn) {
+        const int j = j0 + wj + tn * 32 + (lane & 31);
+        if (j >= g.N) continue;
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = i0 + wi + tm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (i >= g.M) continue;
+                const float v = sum[tm][tn][r];
+                if (g.ws)
+                    g.ws[(((int64_t)batch * g.splits + s) * g.M + i) * g.N + j] = v;
+                else
+                    g.out[batch * g.so + (int64_t)i * g.N + j] = gemm_finish(g, i, j, v);
+            }
+    }
+}
+
+__global__ void __launch_bounds__(256) gemm_splitk_reduce_k(GemmArgs g, int batches) {
+    const int64_t mn = (int64_t)g.M * g.N;
+    const int64_t total = mn * batches;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        const int64_t b = e / mn;
+        const int64_t ij = e - b * mn;
+        float v = 0.f;
+        for (int s = 0; s < g.splits; ++s) v += g.ws[(b * g.splits + s) * mn + ij];
+        const int i = (int)(ij / g.N), j = (int)(ij - (int64_t)i * g.N);
+        g.out[b * g.so + ij] = gemm_finish(g, i, j, v);
+    }
+}
+
+// out[j] partials: thread owns 4 consecutive columns (VEC) or 1.
+template <bool VEC>
+__global__ void __launch_bounds__(256) gemv_xc_k(const float* a, int64_t a_stride, const float* B,
+                                                 int64_t ldb, float* ws, int N, int K, int k_per) {
+    const int s = blockIdx.y;
+    const int kb = s * k_per, ke = min(K, kb + k_per);
+    if (VEC) {
+        const int j = (blockIdx.x * 256 + threadIdx.x) * 4;
+        if (j >= N) return;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j + 3 < N) {
+            for (int k = kb; k < ke; ++k) {
+                const float av = a[k * a_stride];
+                const float4 bv = *reinterpret_cast<const float4*>(B + (int64_t)k * ldb + j);
+                acc.x += av * bv.x;
+                acc.y += av * bv.y;
+                acc.z += av * bv.z;
+                acc.w += av * bv.w;
+            }
+            *reinterpret_cast<float4*>(ws + (int64_t)s * N + j) = acc;
+        } else {
+            for (int k = kb; k < ke; ++k) {
+                const float av = a[k * a_stride];
+                const float* row = B + (int64_t)k * ldb + j;
+                acc.x += av * row[0];
+                if (j + 1 < N) acc.y += av * row[1];
+                if (j + 2 < N) acc.z += av * row[2];
+            }
+            float* dst = ws + (int64_t)s * N + j;
+            dst[0] = acc.x;
+            if (j + 1 < N) dst[1] = acc.y;
+            if (j + 2 < N) dst[2] = acc.z;
+        }
+    } else {
+        const int j = blockIdx.x * 256 + threadIdx.x;
+        if (j >= N) return;
+        float acc = 0.f;
+        for (int k = kb; k < ke; ++k) acc += a[k * a_stride] * B[(int64_t)k * ldb + j];
+        ws[(int64_t)s * N + j] = acc;
+    }
+}
+
+__global__ void __launch_bounds__(256) gemv_reduce_k(GemmArgs g) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= g.N) return;
+    float v = 0.f;
+    for (int s = 0; s < g.splits; ++s) v += g.ws[(int64_t)s * g.N + j];
+    g.out[j] = gemm_finish(g, 0, j, v);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// one wave per output (i, j): sum_k A[i*lda + k] * B[j*ldb + k]
+template <bool VEC>
+__global__ void __launch_bounds__(256) dot_k(GemmArgs g) {
+    const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (w >= (int64_t)g.M * g.N) return;
+    const int i = (int)(w / g.N), j = (int)(w - (int64_t)(w / g.N) * g.N);
+    const float* a = g.A + (int64_t)i * g.lda;
+    const float* b = g.B + (int64_t)j * g.ldb;
+    float acc = 0.f;
+    if (VEC) {
+        const int K4 = g.K / 4;
+        for (int q = lane; q < K4; q += 64) {
+            const float4 x = reinterpret_cast<const float4*>(a)[q];
+            const float4 y = reinterpret_cast<const float4*>(b)[q];
+            acc += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+        }
+        for (int k = K4 * 4 + lane; k < g.K; k += 64) acc += a[k] * b[k];
+    } else {
+        for (int k = lane; k < g.K; k += 64) acc += a[k] * b[k];
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) g.out[(int64_t)i * g.N + j] = gemm_finish(g, i, j, acc);
+}
+
+typedef Tile<128, 128, 32, 2, 2> GemmT128;
+typedef Tile<64, 64, 32, 2, 2> GemmT64;
+
+template <class T, int AK, int BKIND>
+static void launch_mfma(GemmArgs& g, int batches, const char* name) {
+    g.tiles_m = (int)ceil_div(g.M, T::BM);
+    g.tiles_n = (int)ceil_div(g.N, T::BN);
+    const int tiles = g.tiles_m * g.tiles_n * batches;
+    const int target = 2 * ctx().cu_count;
+    int splits = 1;
+    if (tiles < target) {
+        const int max_by_k = (int)(g.K / (4 * T::BK));
+        splits = (int)ceil_div(target, tiles);
+        if (splits > max_by_k) splits = max_by_k;
+        if (splits > 32) splits = 32;
+        if (splits < 1) splits = 1;
+    }
+    g.ws = nullptr;
+    if (splits > 1) {
+        size_t need = (size_t)splits * batches * g.M * g.N * sizeof(float);
+        float* ws = workspace(need);
+        while (!ws && splits > 1) {
+            --splits;
+            need = (size_t)splits * batches * g.M * g.N * sizeof(float);
+            ws = need <= workspace_capacity() ? workspace(need) : nullptr;
+        }
+        g.ws = splits > 1 ? ws : nullptr;
+    }
+    g.k_per_split = (int)(ceil_div(ceil_div(g.K, splits), T::BK) * T::BK);
+    g.splits = (int)ceil_div(g.K, g.k_per_split);
+    if (g.splits < 1) g.splits = 1;
+    if (g.splits == 1) g.ws = nullptr;
+    launch(name, gemm_mfma_k<T, AK, BKIND>, dim3(g.tiles_m * g.tiles_n * g.splits, batches),
+           dim3(256), 0, g);
+    if (g.ws)
+        launch("gemm_splitk_reduce", gemm_splitk_reduce_k, dim3(grid_for((int64_t)g.M * g.N * batches, 1)),
+               dim3(256), 0, g, batches);
+}
+
+template <int AK, int BKIND>
+static void launch_mfma_small(GemmArgs& g, int batches, const char* name) {
+    launch_mfma<GemmT64, AK, BKIND>(g, batches, name);
+}
+
+template <int AK>
+static void dispatch_b_small(GemmArgs& g, int bkind, int batches, const char* name) {
+    switch (bkind) {
+        case kKC4: return launch_mfma_small<AK, kKC4>(g, batches, name);
+        case kKC: return launch_mfma_small<AK, kKC>(g, batches, name);
+        case kXC4: return launch_mfma_small<AK, kXC4>(g, batches, name);
+        default: return launch_mfma_small<AK, kXC>(g, batches, name);
+    }
+}
+
+// Describe operands as: A element (i, k) = A[i*lda + k] if a_kc else A[k*lda + i];
+// B element (k, j) = B[j*ldb + k] if b_kc else B[k*ldb + j].
+struct GemmProblem {
+    const float* A;
+    const float* B;
+    const float* C;
+    float* out;
+    int M, N, K, batches;
+    int64_t lda, ldb, sa, sb, so;
+    bool a_kc, b_kc;
+    float alpha, beta;
+    int c_mode, relu;
+};
+
+static void gemm_run(const GemmProblem& p, const char* name) {
+    if (p.M <= 0 || p.N <= 0 || p.batches <= 0) return;
+    GemmArgs g{};
+    g.A = p.A;
+    g.B = p.B;
+    g.C = p.C;
+    g.out = p.out;
+    g.M = p.M;
+    g.N = p.N;
+    g.K = p.K;
+    g.lda = p.lda;
+    g.ldb = p.ldb;
+    g.sa = p.sa;
+    g.sb = p.sb;
+    g.so = p.so;
+    g.alpha = p.alpha;
+    g.beta = p.beta;
+    g.c_mode = p.c_mode;
+    g.relu = p.relu;
+    g.splits = 1;
+    if (p.K <= 0) {
+        // empty contraction: out = beta*C (alpha*0)
+        GemmArgs z = g;
+        z.K = 0;
+        z.ws = nullptr;
+        // reuse the dot kernel with K = 0
+        launch(name, dot_k<false>, dim3((unsigned)ceil_div((int64_t)p.M * p.N, 4)), dim3(256), 0, z);
+        return;
+    }
+    if (p.batches == 1 && p.M == 1 && !p.b_kc) {
+        // one output row, B row-major: stream B once
+        const int64_t a_stride = p.a_kc ? 1 : p.lda;
+        const bool vec = aligned16(p.B) && p.ldb % 4 == 0 && p.N % 4 == 0;
+        const int cols_per_block = vec ? 1024 : 256;
+        const int col_blocks = (int)ceil_div(p.N, cols_per_block);
+        int splits = (int)ceil_div(4 * ctx().cu_count, col_blocks);
+        const int max_by_k = (int)ceil_div(p.K, 16);
+        if (splits > max_by_k) splits = max_by_k;
+        if (splits < 1) splits = 1;
+        float* ws = workspace((size_t)splits * p.N * sizeof(float));
+        if (!ws) return fail(NNC_HIP_ENOMEM, name, "workspace");
+        const int k_per = (int)ceil_div(p.K, splits);
+        splits = (int)ceil_div(p.K, k_per);
+        g.ws = ws;
+        g.splits = splits;
+        if (vec)
+            launch(name, gemv_xc_k<true>, dim3(col_blocks, splits), dim3(256), 0, p.A, a_stride, p.B,
+                   p.ldb, ws, p.N, p.K, k_per);
+        else
+            launch(name, gemv_xc_k<false>, dim3(col_blocks, splits), dim3(256), 0, p.A, a_stride,
+                   p.B, p.ldb, ws, p.N, p.K, k_per);
+        launch("gemv_reduce", gemv_reduce_k, dim3((unsigned)ceil_div(p.N, 256)), dim3(256), 0, g);
+        return;
+    }
+    if (p.batches == 1 && p.a_kc && p.b_kc && (p.M == 1 || p.N == 1 || (int64_t)p.M * p.N <= 64)) {
+        const bool vec = aligned16(p.A) && aligned16(p.B) && p.lda % 4 == 0 && p.ldb % 4 == 0;
+        const dim3 grid((unsigned)ceil_div((int64_t)p.M * p.N, 4));
+        if (vec) launch(name, dot_k<true>, grid, dim3(256), 0, g);
+        else launch(name, dot_k<false>, grid, dim3(256), 0, g);
+        return;
+    }
+    // MFMA tiles. 16-byte loads need 4-float alignment of every row/batch start.
+    const bool a_al = aligned16(p.A) && p.lda % 4 == 0 && p.sa % 4 == 0;
+    const bool b_al = aligned16(p.B) && p.ldb % 4 == 0 && p.sb % 4 == 0;
+    const int akind = p.a_kc ? ((a_al && p.K % 4 == 0) ? kKC4 : kKC) : (a_al ? kXC4 : kXC);
+    const int bkind = p.b_kc ? ((b_al && p.K % 4 == 0) ? kKC4 : kKC) : (b_al ? kXC4 : kXC);
+    const bool big = (int64_t)p.M * p.N * p.batches >= (int64_t)128 * 128 * 2 * ctx().cu_count / 4 &&
+                     p.M >= 128 && p.N >= 128;
+    if (big && (akind == kKC4 || akind == kXC4) && (bkind == kKC4 || bkind == kXC4)) {
+        if (akind == kKC4 && bkind == kKC4) return launch_mfma<GemmT128, kKC4, kKC4>(g, p.batches, name);
+        if (akind == kKC4 && bkind == kXC4) return launch_mfma<GemmT128, kKC4, kXC4>(g, p.batches, name);
+        if (akind == kXC4 && bkind == kKC4) return launch_mfma<GemmT128, kXC4, kKC4>(g, p.batches, name);
+        return launch_mfma<GemmT128, kXC4, kXC4>(g, p.batches, name);
+    }
+    switch (akind) {
+        case kKC4: return dispatch_b_small<kKC4>(g, bkind, p.batches, name);
+        case kKC: return dispatch_b_small<kKC>(g, bkind, p.batches, name);
+        case kXC4: return dispatch_b_small<kXC4>(g, bkind, p.batches, name);
+        default: return dispatch_b_small<kXC>(g, bkind, p.batches, name);
+    }
+}
+
+static bool args_ok(const char* name, Tensor* a, Tensor* b, Tensor* out) {
+    if (!ready(name)) return false;
+    if (!has_data(a) || !has_data(b) || !has_data(out)) {
+        fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
+        return false;
+    }
+    return true;
+}
+
+static void matmul_impl(Tensor* a, Tensor* b, Tensor* bias, Tensor* out, int relu, const char* name) {
+    if (!args_ok(name, a, b, out)) return;
+    GemmProblem p{};
+    p.A = (const float*)a->data;
+    p.B = (const float*)b->data;
+    p.out = (float*)out->data;
+    p.alpha = 1.f;
+    p.beta = 1.f;
+    p.relu = relu;
+    p.batches = 1;
+    const int an = a->ndim, bn = b->ndim, on = out->ndim;
+    if (an == 2 && bn == 2) {
+        p.M = (int)a->shape[0];
+        p.K = (int)a->shape[1];
+        p.N = (int)b->shape[1];
+        if (b->shape[0] != p.K) return fail(NNC_HIP_EINVAL, name, "inner dimensions differ");
+        p.lda = p.K;
+        p.ldb = p.N;
+        p.a_kc = true;
+        p.b_kc = false;
+    } else if (an == 1 && bn == 2) {
+        p.M = 1;
+        p.K = (int)a->shape[0];
+        p.N = (int)b->shape[1];
+        if (b->shape[0] != p.K) return fail(NNC_HIP_EINVAL, name, "inner dimensions differ");
+        p.lda = p.K;
+        p.ldb = p.N;
+        p.a_kc = true;
+        p.b_kc = false;
+    } else if (an == 2 && bn == 1) {
+        p.M = (int)a->shape[0];
+        p.K = (int)a->shape[1];
+        p.N = 1;
+        if (b->shape[0] != p.K) return fail(NNC_HIP_EINVAL, name, "inner dimensions differ");
+        p.lda = p.K;
+        p.ldb = p.K;  // the vector as one k-contiguous column
+        p.a_kc = true;
+        p.b_kc = true;
+    } else if (an >= 2 && bn >= 2) {
+        p.M = (int)out->shape[on - 2];
+        p.N = (int)out->shape[on - 1];
+        p.K = (int)a->shape[an - 1];
+        if (a->shape[an - 2] != p.M || b->shape[bn - 2] != p.K || b->shape[bn - 1] != p.N)
+            return fail(NNC_HIP_EINVAL, name, "matrix dimensions do not match the output");
+        const int64_t batches = prod(out->shape, 0, on - 2);
+        const int64_t abat = prod(a->shape, 0, an - 2), bbat = prod(b->shape, 0, bn - 2);
+        if ((abat != batches && abat != 1) || (bbat != batches && bbat != 1))
+            return fail(NNC_HIP_EUNSUPP, name, "batch broadcast other than full or none");
+        if (batches >= 65536) return fail(NNC_HIP_EUNSUPP, name, "more than 65535 batches");
+        p.batches = (int)batches;
+        p.lda = p.K;
+        p.ldb = p.N;
+        p.sa = abat == 1 ? 0 : (int64_t)p.M * p.K;
+        p.sb = bbat == 1 ? 0 : (int64_t)p.K * p.N;
+        p.so = (int64_t)p.M * p.N;
+        p.a_kc = true;
+        p.b_kc = false;
+    } else {
+        return;  // the reference computes nothing for other ranks
+    }
+    if (bias && bias->data) {
+        const int64_t bn = numel(bias);
+        p.C = (const float*)bias->data;
+        if (bn == p.N) p.c_mode = 1;
+        else if (bn == (int64_t)p.M * p.N) p.c_mode = 2;
+        else return fail(NNC_HIP_EINVAL, name, "bias must have N or M*N elements");
+    }
+    gemm_run(p, name);
+}
+
+}  // namespace nnc
+
+using namespace nnc;
+
+extern "C" {
+
+void nnc_matmul(Tensor* a, Tensor* b, Tensor* out) { matmul_impl(a, b, nullptr, out, 0, "nnc_matmul"); }
+
+// Emitted by the reference code generator as (a, b, bias or NULL, out)
+// (c_emitter.py:1143-1171); relu(a @ b + bias).
+void nnc_matmul_relu(Tensor* a, Tensor* b, Tensor* bias, Tensor* out) {
+    matmul_impl(a, b, bias, out, 1, "nnc_matmul_relu");
+}
+
+// ops.c:1732-1841: dimension logic of the reference, including its 1-D cases.
+void nnc_gemm(Tensor* a, Tensor* b, Tensor* c, Tensor* out, float alpha, float beta, int ta, int tb) {
+    const char* name = "nnc_gemm";
+    if (!args_ok(name, a, b, out)) return;
+    GemmProblem p{};
+    p.A = (const float*)a->data;
+    p.B = (const float*)b->data;
+    p.out = (float*)out->data;
+    p.alpha = alpha;
+    p.beta = beta;
+    p.batches = 1;
+    if (a->ndim == 2 && b->ndim == 2) {
+        p.M = (int)(ta ? a->shape[1] : a->shape[0]);
+        p.K = (int)(ta ? a->shape[0] : a->shape[1]);
+        p.N = (int)(tb ? b->shape[0] : b->shape[1]);
+    } else if (a->ndim == 1 && b->ndim == 2) {
+        p.M = 1;
+        p.K = (int)a->shape[0];
+        p.N = (int)b->shape[1];
+        ta = 0;
+    } else if (a->ndim == 2 && b->ndim == 1) {
+        p.M = (int)a->shape[0];
+        p.K = (int)a->shape[1];
+        p.N = 1;
+        tb = 0;
+    } else {
+        // the reference's flatten fallback reads B outside its buffer
+        return fail(NNC_HIP_EUNSUPP, name, "operand ranks %d x %d", a->ndim, b->ndim);
+    }
+    if (numel(a) < (int64_t)p.M * p.K || numel(b) < (int64_t)p.K * p.N)
+        return fail(NNC_HIP_EINVAL, name, "operand smaller than M*K or K*N");
+    p.a_kc = !ta;
+    p.lda = ta ? p.M : p.K;
+    p.b_kc = tb != 0;
+    p.ldb = tb ? p.K : p.N;
+    if (c && c->data) {
+        p.C = (const float*)c->data;
+        p.c_mode = c->ndim == 1 ? 1 : 2;
+        if (numel(c) < (p.c_mode == 1 ? p.N : (int64_t)p.M * p.N))
+            return fail(NNC_HIP_EINVAL, name, "C smaller than the output");
+    }
+    if (numel(out) < (int64_t)p.M * p.N) return fail(NNC_HIP_EINVAL, name, "output too small");
+    gemm_run(p, name);
+}
+
+// ops.c:1843-1886: B stored [N, K].
+void nnc_gemm_nt(Tensor* a, Tensor* b, Tensor* c, Tensor* out, float alpha, float beta) {
+    const char* name = "nnc_gemm_nt";
+    if (!args_ok(name, a, b, out)) return;
+    GemmProblem p{};
+    p.A = (const float*)a->data;
+    p.B = (const float*)b->data;
+    p.out = (float*)out->data;
+    p.alpha = alpha;
+    p.beta = beta;
+    p.batches = 1;
+    if (a->ndim == 2 && b->ndim == 2) {
+        p.M = (int)a->shape[0];
+        p.K = (int)a->shape[1];
+        p.N = (int)b->shape[0];
+    } else if (a->ndim == 1 && b->ndim == 2) {
+        p.M = 1;
+        p.K = (int)a->shape[0];
+        p.N = (int)b->shape[0];
+    } else {
+        p.M = 1;
+        p.K = (int)numel(a);
+        p.N = b->ndim == 2 ? (int)b->shape[0] : (int)numel(b);
+    }
+    if (numel(b) < (int64_t)p.N * p.K) return fail(NNC_HIP_EINVAL, name, "B smaller than N*K");
+    p.a_kc = true;
+    p.lda = p.K;
+    p.b_kc = true;
+    p.ldb = p.K;
+    if (c && c->data) {
+        p.C = (const float*)c->data;
+        p.c_mode = c->ndim == 1 ? 1 : 2;
+        if (numel(c) < (p.c_mode == 1 ? p.N : (int64_t)p.M * p.N))
+            return fail(NNC_HIP_EINVAL, name, "C smaller than the output");
+    }
+    if (numel(out) < (int64_t)p.M * p.N) return fail(NNC_HIP_EINVAL, name, "output too small");
+    gemm_run(p, name);
+}
+
+}  // extern "C"

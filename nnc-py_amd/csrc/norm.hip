@@ -1,0 +1,367 @@
+// Softmax, LayerNorm and single-axis ReduceMean/ReduceSum of the nnc ABI
+// (runtime/x86/ops.c:260-310, 2095-2171, 1892-1989).
+//
+// All three view the input as [outer][len][inner] around one axis.
+//
+// inner == 1 (the reduced / normalised elements are contiguous): one wave64
+// per row. Rows of up to 4096 floats are read once with 16-byte loads into
+// registers; max / sums are combined across the wave with xor shuffles, and
+// the row is written once: one HBM read + one HBM write per element. Longer
+// rows loop over global memory (re-reads come from L2).
+//
+// inner > 1 (strided axis): one thread per (outer, inner) column, lanes along
+// inner so every load coalesces; the column is walked in the reference's
+// order. For ReduceMean/Sum that walk is the reference's own Kahan sum, so the
+// strided reduction is bit-exact with it.
+//
+// Arithmetic follows the reference's formulas: softmax = exp(x - max) / sum
+// with max by strict '>' from -inf; layernorm y = g[i] * ((x - mean) / std) +
+// b[i], std = sqrtf(var + eps), var the mean of squared deviations. Parallel
+// sums change the summation order, so these are tolerance parity
+// (1e-4 abs / 1e-3 rel), except the strided reduction.
+#include <math.h>
+
+#include "common.h"
+
+namespace nnc {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// softmax
+// ---------------------------------------------------------------------------
+// PER float4 per lane: rows up to 256*PER floats, dim % 4 == 0, aligned.
+template <int PER>
+__global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, float* out, int64_t rows,
+                                                         int dim) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wstride = (int64_t)gridDim.x * 4;
+    const int d4 = dim / 4;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += wstride) {
+        const float4* x = reinterpret_cast<const float4*>(in + row * dim);
+        float4 v[PER];
+        float m = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int idx = lane + 64 * q;
+            v[q] = idx < d4 ? x[idx] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            if (idx < d4) {
+                if (v[q].x > m) m = v[q].x;
+                if (v[q].y > m) m = v[q].y;
+                if (v[q].z > m) m = v[q].z;
+                if (v[q].w > m) m = v[q].w;
+            }
+        }
+        m = wave_max(m);
+        float s = 0.f;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            if (lane + 64 * q < d4) {
+                v[q].x = expf(v[q].x - m);
+                v[q].y = expf(v[q].y - m);
+                v[q].z = expf(v[q].z - m);
+                v[q].w = expf(v[q].w - m);
+                s += (v[q].x + v[q].y) + (v[q].z + v[q].w);
+            }
+        }
+        s = wave_sum(s);
+        float4* y = reinterpret_cast<float4*>(out + row * dim);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int idx = lane + 64 * q;
+            if (idx < d4) y[idx] = make_float4(v[q].x / s, v[q].y / s, v[q].z / s, v[q].w / s);
+        }
+    }
+}
+
+// any contiguous row: three passes over global memory
+__global__ void __launch_bounds__(256) softmax_rows_k(const float* in, float* out, int64_t rows,
+                                                      int dim) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wstride = (int64_t)gridDim.x * 4;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += wstride) {
+        const float* x = in + row * dim;
+        float m = -INFINITY;
+        for (int i = lane; i < dim; i += 64)
+            if (x[i] > m) m = x[i];
+        m = wave_max(m);
+        float s = 0.f;
+        for (int i = lane; i < dim; i += 64) s += expf(x[i] - m);
+        s = wave_sum(s);
+        float* y = out + row * dim;
+        for (int i = lane; i < dim; i += 64) y[i] = expf(x[i] - m) / s;
+    }
+}
+
+// strided axis: thread per (outer, inner)
+__global__ void __launch_bounds__(256) softmax_cols_k(const float* in, float* out, int64_t outer,
+                                                      int dim, int64_t inner) {
+    const int64_t total = outer * inner;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        const int64_t o = e / inner, q = e - o * inner;
+        const float* x = in + o * dim * inner + q;
+        float* y = out + o * dim * inner + q;
+        float m = -INFINITY;
+        for (int s = 0; s < dim; ++s)
+            if (x[s * inner] > m) m = x[s * inner];
+        float den = 0.f;
+        for (int s = 0; s < dim; ++s) den += expf(x[s * inner] - m);
+        for (int s = 0; s < dim; ++s) y[s * inner] = expf(x[s * inner] - m) / den;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// layernorm over a contiguous span of D*inner floats per outer row
+// ---------------------------------------------------------------------------
+template <int PER>
+__global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, const float* g,
+                                                           const float* b, float* out, int64_t rows,
+                                                           int span, int inner, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wstride = (int64_t)gridDim.x * 4;
+    const int s4 = span / 4;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += wstride) {
+        const float4* x = reinterpret_cast<const float4*>(in + row * span);
+        float4 v[PER];
+        float acc = 0.f;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int idx = lane + 64 * q;
+            v[q] = idx < s4 ? x[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+            acc += (v[q].x + v[q].y) + (v[q].z + v[q].w);
+        }
+        const float mean = wave_sum(acc) / (float)span;
+        float sq = 0.f;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            if (lane + 64 * q < s4) {
+                const float dx = v[q].x - mean, dy = v[q].y - mean;
+                const float dz = v[q].z - mean, dw = v[q].w - mean;
+                sq += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+            }
+        }
+        const float var = wave_sum(sq) / (float)span;
+        const float sd = sqrtf(var + eps);
+        float4* y = reinterpret_cast<float4*>(out + row * span);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int idx = lane + 64 * q;
+            if (idx < s4) {
+                const int e = idx * 4;
+                float r[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int i = (e + c) / inner;
+                    const float gi = g ? g[i] : 1.0f, bi = b ? b[i] : 0.0f;
+                    r[c] = gi * ((r[c] - mean) / sd) + bi;
+                }
+                y[idx] = make_float4(r[0], r[1], r[2], r[3]);
+            }
+        }
+    }
+}
+
+// any span: one workgroup per row, three passes
+__global__ void __launch_bounds__(256) layernorm_rows_k(const float* in, const float* g,
+                                                        const float* b, float* out, int64_t rows,
+                                                        int64_t span, int64_t inner, float eps) {
+    __shared__ float part[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const float* x = in + row * span;
+        float acc = 0.f;
+        for (int64_t e = threadIdx.x; e < span; e += 256) acc += x[e];
+        acc = wave_sum(acc);
+        if (lane == 0) part[wave] = acc;
+        __syncthreads();
+        const float mean = ((part[0] + part[1]) + (part[2] + part[3])) / (float)span;
+        __syncthreads();
+        float sq = 0.f;
+        for (int64_t e = threadIdx.x; e < span; e += 256) {
+            const float d = x[e] - mean;
+            sq += d * d;
+        }
+        sq = wave_sum(sq);
+        if (lane == 0) part[wave] = sq;
+        __syncthreads();
+        const float var = ((part[0] + part[1]) + (part[2] + part[3])) / (float)span;
+        __syncthreads();
+        const float sd = sqrtf(var + eps);
+        float* y = out + row * span;
+        for (int64_t e = threadIdx.x; e < span; e += 256) {
+            const int64_t i = e / inner;
+            const float gi = g ? g[i] : 1.0f, bi = b ? b[i] : 0.0f;
+            y[e] = gi * ((x[e] - mean) / sd) + bi;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// single-axis reductions
+// ---------------------------------------------------------------------------
+// contiguous rows: wave per row, Kahan per lane, shuffle tree across lanes
+template <bool MEAN>
+__global__ void __launch_bounds__(256) reduce_rows_k(const float* in, float* out, int64_t rows,
+                                                     int64_t len) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wstride = (int64_t)gridDim.x * 4;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += wstride) {
+        const float* x = in + row * len;
+        float s = 0.f, c = 0.f;
+        for (int64_t i = lane; i < len; i += 64) {
+            const float y = x[i] - c;
+            const float t = s + y;
+            c = (t - s) - y;
+            s = t;
+        }
+        s = wave_sum(s);
+        if (lane == 0) out[row] = MEAN ? s / (float)len : s;
+    }
+}
+
+// strided axis: thread per (outer, inner), the reference's sequential Kahan sum
+template <bool MEAN>
+__global__ void __launch_bounds__(256) reduce_cols_k(const float* in, float* out, int64_t outer,
+                                                     int64_t len, int64_t inner) {
+    const int64_t total = outer * inner;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        const int64_t o = e / inner, q = e - o * inner;
+        const float* x = in + o * len * inner + q;
+        float s = 0.f, c = 0.f;
+        for (int64_t r = 0; r < len; ++r) {
+            const float y = x[r * inner] - c;
+            const float t = s + y;
+            c = (t - s) - y;
+            s = t;
+        }
+        out[e] = MEAN ? s / (float)len : s;
+    }
+}
+
+static bool split_axis(const char* name, Tensor* in, int& axis, int64_t& outer, int64_t& len,
+                       int64_t& inner) {
+    const int nd = in->ndim;
+    if (axis < 0) axis += nd;
+    if (axis < 0 || axis >= nd) {
+        fail(NNC_HIP_EINVAL, name, "axis out of range");
+        return false;
+    }
+    outer = prod(in->shape, 0, axis);
+    len = in->shape[axis];
+    inner = prod(in->shape, axis + 1, nd);
+    return true;
+}
+
+template <int PER>
+static void softmax_v4(const float* x, float* y, int64_t rows, int dim, const char* name) {
+    launch(name, softmax_rows_v4_k<PER>, dim3(grid_for(rows, 4, 1) * 1), dim3(256), 0, x, y, rows, dim);
+}
+
+template <int PER>
+static void layernorm_v4(const float* x, const float* g, const float* b, float* y, int64_t rows,
+                         int span, int inner, float eps, const char* name) {
+    launch(name, layernorm_rows_v4_k<PER>, dim3(grid_for(rows, 4, 1)), dim3(256), 0, x, g, b, y, rows,
+           span, inner, eps);
+}
+
+}  // namespace nnc
+
+using namespace nnc;
+
+extern "C" {
+
+void nnc_softmax(Tensor* in, Tensor* out, int axis) {
+    const char* name = "nnc_softmax";
+    if (!ready(name)) return;
+    if (!has_data(in) || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
+    int64_t outer, len, inner;
+    if (!split_axis(name, in, axis, outer, len, inner)) return;
+    if (outer * len * inner == 0) return;
+    const float* x = (const float*)in->data;
+    float* y = (float*)out->data;
+    if (len >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "axis too long");
+    if (inner == 1) {
+        const int dim = (int)len;
+        const bool v4 = dim % 4 == 0 && aligned16(x) && aligned16(y);
+        if (v4 && dim <= 256) return softmax_v4<1>(x, y, outer, dim, name);
+        if (v4 && dim <= 512) return softmax_v4<2>(x, y, outer, dim, name);
+        if (v4 && dim <= 1024) return softmax_v4<4>(x, y, outer, dim, name);
+        if (v4 && dim <= 2048) return softmax_v4<8>(x, y, outer, dim, name);
+        if (v4 && dim <= 4096) return softmax_v4<16>(x, y, outer, dim, name);
+        launch(name, softmax_rows_k, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, dim);
+        return;
+    }
+    launch(name, softmax_cols_k, dim3(grid_for(outer * inner, 1)), dim3(256), 0, x, y, outer, (int)len,
+           inner);
+}
+
+void nnc_layernorm(Tensor* in, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps) {
+    const char* name = "nnc_layernorm";
+    if (!ready(name)) return;
+    if (!has_data(in) || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
+    int64_t outer, len, inner;
+    if (!split_axis(name, in, axis, outer, len, inner)) return;
+    const int64_t span = len * inner;
+    if (outer * span == 0) return;
+    const float* x = (const float*)in->data;
+    const float* g = (scale && scale->data) ? (const float*)scale->data : nullptr;
+    const float* b = (bias && bias->data) ? (const float*)bias->data : nullptr;
+    if ((g && numel(scale) < len) || (b && numel(bias) < len))
+        return fail(NNC_HIP_EINVAL, name, "scale/bias shorter than the axis");
+    float* y = (float*)out->data;
+    const bool v4 = span % 4 == 0 && span < (1 << 30) && aligned16(x) && aligned16(y);
+    const int sp = (int)span, inn = (int)inner;
+    if (v4 && span <= 256) return layernorm_v4<1>(x, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 512) return layernorm_v4<2>(x, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 1024) return layernorm_v4<4>(x, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 2048) return layernorm_v4<8>(x, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 4096) return layernorm_v4<16>(x, g, b, y, outer, sp, inn, eps, name);
+    unsigned grid = (unsigned)(outer < 65536 ? outer : 65536);
+    launch(name, layernorm_rows_k, dim3(grid), dim3(256), 0, x, g, b, y, outer, span, inner, eps);
+}
+
+static void reduce_entry(const char* name, Tensor* in, Tensor* out, int axis, bool mean) {
+    if (!ready(name)) return;
+    if (!has_data(in) || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
+    int64_t outer, len, inner;
+    if (!split_axis(name, in, axis, outer, len, inner)) return;
+    if (numel(out) < outer * inner) return fail(NNC_HIP_EINVAL, name, "output smaller than the reduction");
+    if (outer * inner == 0) return;
+    const float* x = (const float*)in->data;
+    float* y = (float*)out->data;
+    if (inner == 1) {
+        if (mean) launch(name, reduce_rows_k<true>, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, len);
+        else launch(name, reduce_rows_k<false>, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, len);
+        return;
+    }
+    const dim3 g(grid_for(outer * inner, 1));
+    if (mean) launch(name, reduce_cols_k<true>, g, dim3(256), 0, x, y, outer, len, inner);
+    else launch(name, reduce_cols_k<false>, g, dim3(256), 0, x, y, outer, len, inner);
+}
+
+void nnc_reducemean(Tensor* in, Tensor* out, int axis, int keepdims) {
+    (void)keepdims;
+    reduce_entry("nnc_reducemean", in, out, axis, true);
+}
+
+void nnc_reducesum(Tensor* in, Tensor* out, int axis, int keepdims) {
+    (void)keepdims;
+    reduce_entry("nnc_reducesum", in, out, axis, false);
+}
+
+}  // extern "C"

@@ -1,0 +1,356 @@
+// Lifecycle, HBM arena, host<->device copies, errors, timing table and launch
+// capture of libnnc_hip.so (declared in include/nnc_hip.h).
+//
+// The reference runtime owns no state: generated tensors.c places tensors in
+// a static host pool (codegen/x86_emitters/tensors.py:589-600). Here the pool
+// becomes one hipMalloc'd arena and this file owns the device, the stream and
+// a grow-only workspace for split-K partials.
+#include <stdarg.h>
+#include <string.h>
+
+#include <atomic>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace nnc {
+
+static Context g_ctx;
+static std::atomic<int> g_last_error{0};
+static char g_last_msg[512] = "";
+
+Context& ctx() { return g_ctx; }
+
+void fail(int code, const char* who, const char* fmt, ...) {
+    char body[384];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(body, sizeof body, fmt, ap);
+    va_end(ap);
+    snprintf(g_last_msg, sizeof g_last_msg, "%s: %s", who, body);
+    g_last_error.store(code);
+    fprintf(stderr, "%s\n", g_last_msg);
+    fflush(stderr);
+}
+
+bool hip_ok(hipError_t e, const char* who, const char* what) {
+    if (e == hipSuccess) return true;
+    fail(NNC_HIP_EDEVICE, who, "%s failed: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+bool ready(const char* who) {
+    if (g_ctx.stream) return true;
+    fail(NNC_HIP_ESTATE, who, "nnc_hip_init() has not been called");
+    return false;
+}
+
+// Default workspace: enough for split-K over the ResNet-18 / GEMM-sweep
+// shapes without growing; grows (outside capture) when a call needs more.
+static const size_t kDefaultWorkspace = 64u << 20;
+
+float* workspace(size_t bytes) {
+    if (bytes <= g_ctx.workspace_bytes) return g_ctx.workspace;
+    if (g_ctx.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(g_ctx.stream), "workspace", "hipStreamSynchronize"))
+        return nullptr;
+    if (g_ctx.workspace) (void)hipFree(g_ctx.workspace);
+    g_ctx.workspace = nullptr;
+    g_ctx.workspace_bytes = 0;
+    size_t want = bytes < kDefaultWorkspace ? kDefaultWorkspace : bytes;
+    void* p = nullptr;
+    if (!hip_ok(hipMalloc(&p, want), "workspace", "hipMalloc")) return nullptr;
+    g_ctx.workspace = static_cast<float*>(p);
+    g_ctx.workspace_bytes = want;
+    return g_ctx.workspace;
+}
+
+size_t workspace_capacity() { return g_ctx.workspace_bytes; }
+
+// ---------------------------------------------------------------------------
+// per-kernel timing
+// ---------------------------------------------------------------------------
+struct Pending {
+    std::string name;
+    hipEvent_t start, stop;
+};
+struct Stat {
+    std::string name;
+    int64_t launches = 0;
+    double ms = 0.0;
+};
+static std::vector<Pending> g_pending;
+static std::vector<hipEvent_t> g_event_pool;
+static std::vector<Stat> g_stats;
+
+static hipEvent_t take_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    (void)hipEventCreate(&e);
+    return e;
+}
+
+TimedScope::TimedScope(const char* n) : name(n) {
+    if (!g_ctx.profiling || g_ctx.capturing) return;
+    start = take_event();
+    stop = take_event();
+    (void)hipEventRecord(start, g_ctx.stream);
+}
+
+TimedScope::~TimedScope() {
+    if (!start) return;
+    (void)hipEventRecord(stop, g_ctx.stream);
+    g_pending.push_back({name, start, stop});
+}
+
+static void resolve_pending() {
+    if (g_pending.empty()) return;
+    (void)hipStreamSynchronize(g_ctx.stream);
+    for (auto& p : g_pending) {
+        float ms = 0.f;
+        (void)hipEventElapsedTime(&ms, p.start, p.stop);
+        Stat* s = nullptr;
+        for (auto& st : g_stats)
+            if (st.name == p.name) { s = &st; break; }
+        if (!s) {
+            g_stats.push_back(Stat{p.name, 0, 0.0});
+            s = &g_stats.back();
+        }
+        s->launches += 1;
+        s->ms += ms;
+        g_event_pool.push_back(p.start);
+        g_event_pool.push_back(p.stop);
+    }
+    g_pending.clear();
+}
+
+}  // namespace nnc
+
+using namespace nnc;
+
+extern "C" {
+
+int nnc_hip_init(int device) {
+    Context& c = g_ctx;
+    if (c.stream && c.device == device) return NNC_HIP_OK;
+    if (c.stream) nnc_hip_shutdown();
+    int count = 0;
+    if (!hip_ok(hipGetDeviceCount(&count), "nnc_hip_init", "hipGetDeviceCount"))
+        return NNC_HIP_EDEVICE;
+    if (device < 0 || device >= count) {
+        fail(NNC_HIP_EINVAL, "nnc_hip_init", "device %d out of range (%d devices)", device, count);
+        return NNC_HIP_EINVAL;
+    }
+    if (!hip_ok(hipSetDevice(device), "nnc_hip_init", "hipSetDevice")) return NNC_HIP_EDEVICE;
+    hipDeviceProp_t prop;
+    if (hip_ok(hipGetDeviceProperties(&prop, device), "nnc_hip_init", "hipGetDeviceProperties"))
+        c.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    if (!hip_ok(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking), "nnc_hip_init",
+                "hipStreamCreate"))
+        return NNC_HIP_EDEVICE;
+    c.device = device;
+    if (!workspace(kDefaultWorkspace)) return NNC_HIP_ENOMEM;
+    return NNC_HIP_OK;
+}
+
+void nnc_hip_shutdown(void) {
+    Context& c = g_ctx;
+    if (!c.stream) return;
+    (void)hipStreamSynchronize(c.stream);
+    nnc_hip_graph_destroy();
+    for (auto& p : g_pending) {
+        (void)hipEventDestroy(p.start);
+        (void)hipEventDestroy(p.stop);
+    }
+    g_pending.clear();
+    for (auto e : g_event_pool) (void)hipEventDestroy(e);
+    g_event_pool.clear();
+    if (c.arena) (void)hipFree(c.arena);
+    if (c.workspace) (void)hipFree(c.workspace);
+    (void)hipStreamDestroy(c.stream);
+    g_ctx = Context{};
+}
+
+int nnc_hip_arena_reserve(size_t bytes) {
+    if (!ready("nnc_hip_arena_reserve")) return NNC_HIP_ESTATE;
+    Context& c = g_ctx;
+    if (c.arena && bytes <= c.arena_bytes) return NNC_HIP_OK;
+    (void)hipStreamSynchronize(c.stream);
+    if (c.arena) (void)hipFree(c.arena);
+    c.arena = nullptr;
+    c.arena_bytes = 0;
+    void* p = nullptr;
+    if (!hip_ok(hipMalloc(&p, bytes ? bytes : 256), "nnc_hip_arena_reserve", "hipMalloc"))
+        return NNC_HIP_ENOMEM;
+    c.arena = static_cast<char*>(p);
+    c.arena_bytes = bytes;
+    return NNC_HIP_OK;
+}
+
+void* nnc_hip_arena_base(void) { return g_ctx.arena; }
+size_t nnc_hip_arena_size(void) { return g_ctx.arena_bytes; }
+
+int nnc_hip_bind(Tensor* t, size_t offset) {
+    if (!t) {
+        fail(NNC_HIP_EINVAL, "nnc_hip_bind", "NULL tensor");
+        return NNC_HIP_EINVAL;
+    }
+    if (!g_ctx.arena) {
+        fail(NNC_HIP_ESTATE, "nnc_hip_bind", "no arena reserved");
+        return NNC_HIP_ESTATE;
+    }
+    if ((offset & 15u) != 0 || offset + (size_t)t->nbytes > g_ctx.arena_bytes) {
+        fail(NNC_HIP_EINVAL, "nnc_hip_bind", "offset %zu + %lld bytes outside arena of %zu (or misaligned)",
+             offset, (long long)t->nbytes, g_ctx.arena_bytes);
+        return NNC_HIP_EINVAL;
+    }
+    t->data = g_ctx.arena + offset;
+    return NNC_HIP_OK;
+}
+
+void* nnc_hip_malloc(size_t bytes) {
+    if (!ready("nnc_hip_malloc")) return nullptr;
+    void* p = nullptr;
+    if (!hip_ok(hipMalloc(&p, bytes ? bytes : 16), "nnc_hip_malloc", "hipMalloc")) return nullptr;
+    return p;
+}
+
+void nnc_hip_free(void* ptr) {
+    if (!ptr || !g_ctx.stream) return;
+    (void)hipStreamSynchronize(g_ctx.stream);
+    (void)hipFree(ptr);
+}
+
+int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (!ready("nnc_hip_memcpy_h2d")) return NNC_HIP_ESTATE;
+    if (!bytes) return NNC_HIP_OK;
+    if (!hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx.stream),
+                "nnc_hip_memcpy_h2d", "hipMemcpyAsync") ||
+        !hip_ok(hipStreamSynchronize(g_ctx.stream), "nnc_hip_memcpy_h2d", "hipStreamSynchronize"))
+        return NNC_HIP_EDEVICE;
+    return NNC_HIP_OK;
+}
+
+int nnc_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (!ready("nnc_hip_memcpy_d2h")) return NNC_HIP_ESTATE;
+    if (!bytes) return NNC_HIP_OK;
+    if (!hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.stream),
+                "nnc_hip_memcpy_d2h", "hipMemcpyAsync") ||
+        !hip_ok(hipStreamSynchronize(g_ctx.stream), "nnc_hip_memcpy_d2h", "hipStreamSynchronize"))
+        return NNC_HIP_EDEVICE;
+    return NNC_HIP_OK;
+}
+
+int nnc_hip_upload(Tensor* t, const void* host_src) {
+    if (!t || !t->data || !host_src) {
+        fail(NNC_HIP_EINVAL, "nnc_hip_upload", "NULL tensor, data or source");
+        return NNC_HIP_EINVAL;
+    }
+    return nnc_hip_memcpy_h2d(t->data, host_src, (size_t)t->nbytes);
+}
+
+int nnc_hip_download(const Tensor* t, void* host_dst) {
+    if (!t || !t->data || !host_dst) {
+        fail(NNC_HIP_EINVAL, "nnc_hip_download", "NULL tensor, data or destination");
+        return NNC_HIP_EINVAL;
+    }
+    return nnc_hip_memcpy_d2h(host_dst, t->data, (size_t)t->nbytes);
+}
+
+int nnc_hip_sync(void) {
+    if (!ready("nnc_hip_sync")) return NNC_HIP_ESTATE;
+    return hip_ok(hipStreamSynchronize(g_ctx.stream), "nnc_hip_sync", "hipStreamSynchronize")
+               ? NNC_HIP_OK
+               : NNC_HIP_EDEVICE;
+}
+
+void* nnc_hip_stream(void) { return g_ctx.stream; }
+
+int nnc_hip_last_error(void) { return g_last_error.load(); }
+const char* nnc_hip_last_error_message(void) { return g_last_msg; }
+void nnc_hip_clear_error(void) {
+    g_last_error.store(0);
+    g_last_msg[0] = '\0';
+}
+
+void nnc_hip_profile_enable(int on) {
+    if (!on) resolve_pending();
+    g_ctx.profiling = on != 0;
+}
+
+void nnc_hip_profile_reset(void) {
+    resolve_pending();
+    g_stats.clear();
+}
+
+int nnc_hip_profile_count(void) {
+    resolve_pending();
+    return (int)g_stats.size();
+}
+
+int nnc_hip_profile_entry(int i, char* name, int cap, int64_t* launches, double* total_ms) {
+    resolve_pending();
+    if (i < 0 || i >= (int)g_stats.size()) return NNC_HIP_EINVAL;
+    if (name && cap > 0) {
+        strncpy(name, g_stats[i].name.c_str(), (size_t)cap - 1);
+        name[cap - 1] = '\0';
+    }
+    if (launches) *launches = g_stats[i].launches;
+    if (total_ms) *total_ms = g_stats[i].ms;
+    return NNC_HIP_OK;
+}
+
+int nnc_hip_graph_begin(void) {
+    if (!ready("nnc_hip_graph_begin")) return NNC_HIP_ESTATE;
+    nnc_hip_graph_destroy();
+    resolve_pending();
+    if (!hip_ok(hipStreamBeginCapture(g_ctx.stream, hipStreamCaptureModeRelaxed),
+                "nnc_hip_graph_begin", "hipStreamBeginCapture"))
+        return NNC_HIP_EDEVICE;
+    g_ctx.capturing = true;
+    return NNC_HIP_OK;
+}
+
+int nnc_hip_graph_end(void) {
+    if (!ready("nnc_hip_graph_end")) return NNC_HIP_ESTATE;
+    if (!g_ctx.capturing) {
+        fail(NNC_HIP_ESTATE, "nnc_hip_graph_end", "no capture in progress");
+        return NNC_HIP_ESTATE;
+    }
+    g_ctx.capturing = false;
+    hipGraph_t g = nullptr;
+    if (!hip_ok(hipStreamEndCapture(g_ctx.stream, &g), "nnc_hip_graph_end", "hipStreamEndCapture"))
+        return NNC_HIP_EDEVICE;
+    g_ctx.graph = g;
+    if (!hip_ok(hipGraphInstantiate(&g_ctx.graph_exec, g, nullptr, nullptr, 0), "nnc_hip_graph_end",
+                "hipGraphInstantiate"))
+        return NNC_HIP_EDEVICE;
+    return NNC_HIP_OK;
+}
+
+int nnc_hip_graph_launch(void) {
+    if (!ready("nnc_hip_graph_launch")) return NNC_HIP_ESTATE;
+    if (!g_ctx.graph_exec) {
+        fail(NNC_HIP_ESTATE, "nnc_hip_graph_launch", "no captured graph");
+        return NNC_HIP_ESTATE;
+    }
+    TimedScope scope("graph");
+    return hip_ok(hipGraphLaunch(g_ctx.graph_exec, g_ctx.stream), "nnc_hip_graph_launch",
+                  "hipGraphLaunch")
+               ? NNC_HIP_OK
+               : NNC_HIP_EDEVICE;
+}
+
+void nnc_hip_graph_destroy(void) {
+    if (g_ctx.graph_exec) (void)hipGraphExecDestroy(g_ctx.graph_exec);
+    if (g_ctx.graph) (void)hipGraphDestroy(g_ctx.graph);
+    g_ctx.graph_exec = nullptr;
+    g_ctx.graph = nullptr;
+}
+
+}  // extern "C"

@@ -484,9 +484,17 @@ void nnc_matmul(Tensor* a, Tensor* b, Tensor* out) {
     }
 }
 
-/* composition relu(matmul) for the emitted-but-undefined reference call */
-void nnc_matmul_relu(Tensor* a, Tensor* b, Tensor* out) {
+/* relu(matmul + bias) for the emitted-but-undefined reference call
+ * (c_emitter.py:1143-1171 passes a, b, bias-or-NULL, out); the bias is added
+ * per column ([N]) or element-wise ([M, N]) before the Relu. */
+void nnc_matmul_relu(Tensor* a, Tensor* b, Tensor* bias, Tensor* out) {
     nnc_matmul(a, b, out);
+    if (bias && bias->data) {
+        const int64_t n = numel(out), bn = numel(bias);
+        float* z = (float*)out->data;
+        const float* bb = (const float*)bias->data;
+        for (int64_t i = 0; i < n; ++i) z[i] += bb[i % bn];
+    }
     nnc_relu(out, out);
 }
 

@@ -70,6 +70,25 @@ def ref_lib(abi):
     return abi.bind(ctypes.CDLL(str(path)))
 
 
+@pytest.fixture(scope="session")
+def hip(pkg):
+    """libnnc_hip.so initialised on device 0 (GPU tests only). No fallback:
+    a missing library fails the test."""
+    from nnc_py_amd import runtime
+    lib = runtime.init(0)
+    yield lib
+    runtime.sync()
+
+
+@pytest.fixture
+def dmem(hip):
+    from nnc_py_amd import runtime
+    runtime.clear_error()
+    mem = runtime.DeviceMem()
+    yield mem
+    mem.release()
+
+
 def load_golden():
     manifest = json.loads((TESTS / "golden" / "manifest.json").read_text())
     arrays = np.load(TESTS / "golden" / "golden.npz")

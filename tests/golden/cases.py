@@ -440,7 +440,7 @@ def matmul_cases():
     a = rng.uniform(-1, 1, (20, 40)).astype(F32)
     b = rng.uniform(-1, 1, (40, 30)).astype(F32)
     out.append(case("nnc_matmul_relu_2d", "nnc_matmul_relu", {"a": a, "b": b, "out": np.zeros((20, 30), F32)},
-                    [("t", "a"), ("t", "b"), ("t", "out")], ["out"], "fp"))
+                    [("t", "a"), ("t", "b"), ("null",), ("t", "out")], ["out"], "fp"))
     # gemm variants: trans flags, bias shapes, alpha/beta
     gspecs = [
         ("nn_bN", 33, 47, 29, 0, 0, "N", 1.0, 1.0),

@@ -1,0 +1,55 @@
+"""The C-ABI libraries load and export what include/*.h declares (CPU only:
+no HIP call is made, the library is only dlopen'ed)."""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+INCLUDE = ROOT / "include"
+
+
+def test_signature_table_matches_header(abi):
+    declared = set(abi.declared_symbols(INCLUDE / "nnc_ops.h"))
+    assert declared == set(abi.SIGNATURES), declared ^ set(abi.SIGNATURES)
+
+
+def test_reference_abi_is_covered(abi):
+    """Every entry point of the reference ABI (runtime/include/nnc_ops.h) is in
+    our header; the only addition is the emitted-but-undefined matmul_relu."""
+    ref_names = {n for n in abi.SIGNATURES if n not in abi.NOT_IN_REFERENCE}
+    assert len(ref_names) == 55
+
+
+def test_hip_library_exports_every_declared_symbol(abi, pkg):
+    from nnc_py_amd import runtime
+    if not runtime.LIB_PATH.exists():
+        pytest.fail("libnnc_hip.so is not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(runtime.LIB_PATH))
+    missing = []
+    for header in sorted(INCLUDE.glob("*.h")):
+        for name in abi.declared_symbols(header):
+            if not hasattr(lib, name):
+                missing.append(f"{header.name}:{name}")
+    assert not missing, missing
+
+
+def test_hip_header_declares_the_runtime_table(abi, pkg):
+    from nnc_py_amd import runtime
+    declared = set(abi.declared_symbols(INCLUDE / "nnc_hip.h"))
+    assert declared == set(runtime._HIP_SIGNATURES), declared ^ set(runtime._HIP_SIGNATURES)
+
+
+def test_oracle_exports_every_op(abi, oracle_lib):
+    for name in abi.SIGNATURES:
+        assert hasattr(oracle_lib, name), name
+
+
+def test_product_does_not_link_the_oracle(pkg):
+    """libnnc_hip.so must not depend on or embed the CPU oracle."""
+    from nnc_py_amd import runtime
+    data = runtime.LIB_PATH.read_bytes()
+    assert b"liboracle" not in data and b"libref_ops" not in data
