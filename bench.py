@@ -1,0 +1,229 @@
+#!/usr/bin/env python3
+"""ResNet-18 fp32 inference throughput on one MI355X through libnnc_hip.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one nnc_run() of ResNet-18 (BatchNorm folded) over a batch of 32
+synthetic 3x224x224 images: the O3 program (conv+relu and add+relu fused,
+specialised conv entry points, constant FC weight in [N, K]) lowered to nnc_*
+calls, its activations and weights in one HBM arena, replayed as one
+hipGraph per step. Inputs are resident in HBM before timing starts.
+
+Printed as one JSON line (rank 0): images/s at batch 32 (value), batch 1 as
+an extra figure, the roofline of the dominant kernel measured live from the
+library's per-launch hipEvent table, a per-kernel table, and the reference
+CPU runtime timed on this host as a baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "ResNet-18 fp32 images/s (b1,b32) on 1 GPU; per-op % HBM/MFMA roofline"
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_FP32_MFMA_TF = 157.3  # MI355X dense fp32 matrix
+
+
+def load_package():
+    if "nnc_py_amd" in sys.modules:
+        return sys.modules["nnc_py_amd"]
+    pkg = ROOT / "nnc-py_amd"
+    spec = importlib.util.spec_from_file_location("nnc_py_amd", pkg / "__init__.py",
+                                                  submodule_search_locations=[str(pkg)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["nnc_py_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed_steps(ex, steps: int, warmup: int, graph: bool, runtime) -> float:
+    """Seconds for `steps` nnc_run() after `warmup`; synchronised both sides."""
+    for _ in range(warmup):
+        ex.run()
+    runtime.sync()
+    if graph:
+        ex.capture()
+        ex.replay()
+        runtime.sync()
+    step = ex.replay if graph else ex.run
+    runtime.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    runtime.sync()
+    return time.perf_counter() - t0
+
+
+def kernel_table(ex, runtime, steps: int) -> list[dict]:
+    """Per-kernel averages over `steps` directly launched nnc_run() calls."""
+    runtime.profile_reset()
+    runtime.profile_enable(True)
+    for _ in range(steps):
+        ex.run()
+    runtime.sync()
+    table = runtime.profile_table()
+    runtime.profile_enable(False)
+    rows = []
+    for r in table:
+        avg_ms = r["ms"] / r["launches"]
+        if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma")):
+            bound, unit, peak = "mfma", "TFLOP/s", PEAK_FP32_MFMA_TF
+            achieved = r["flops"] / (r["ms"] * 1e-3) / 1e12
+        else:
+            bound, unit, peak = "hbm", "GB/s", PEAK_HBM_GBS
+            achieved = r["bytes"] / (r["ms"] * 1e-3) / 1e9 if r["ms"] > 0 else 0.0
+        rows.append({"kernel": r["name"], "launches_per_step": r["launches"] / steps,
+                     "avg_us": round(avg_ms * 1e3, 2), "ms_per_step": round(r["ms"] / steps, 4),
+                     "bound": bound, "achieved": round(achieved, 2), "unit": unit,
+                     "frac": round(achieved / peak, 4),
+                     "work_per_launch": (r["flops"] if bound == "mfma" else r["bytes"]) / r["launches"]})
+    rows.sort(key=lambda x: -x["ms_per_step"])
+    return rows
+
+
+def cpu_baseline(pkg, iters: int) -> dict | None:
+    """ResNet-18 batch 1 through a CPU implementation of the same ABI: the
+    reference runtime (runtime/x86/ops.c compiled by oracle/Makefile into
+    oracle/_ref/) when present, else the oracle restatement; one thread."""
+    from nnc_py_amd.compiler import Executor, build_program, zoo
+    from nnc_py_amd import abi
+    ref = ROOT / "oracle" / "_ref" / "libref_ops.so"
+    port = ROOT / "oracle" / "liboracle.so"
+    if ref.exists():
+        path, kind = ref, "reference"
+    elif port.exists():
+        path, kind = port, "port"
+    else:
+        return None
+    lib = abi.bind(ctypes.CDLL(str(path)))
+    prog = build_program(zoo.resnet18(batch=1, seed=1), opt_level=3)
+    ex = Executor(prog, device=False, lib=lib)
+    ex.set_input("input", np.random.default_rng(0).standard_normal((1, 3, 224, 224)).astype(np.float32))
+    ex.run()  # warmup
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        ex.run()
+    dt = (time.perf_counter() - t0) / iters
+    cpu = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(1.0 / dt, 4), "unit": "images/s", "cores": 1, "kind": kind,
+            "sample": (f"ResNet-18 fp32 batch 1, same O3 call sequence, 1 warmup + {iters} timed "
+                       f"nnc_run() ({dt:.2f} s each), {path.relative_to(ROOT)} gcc -O2, 1 thread; "
+                       f"host {cpu}, nproc {os.cpu_count()}")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--no-graph", action="store_true", help="launch each nnc_* call instead of a hipGraph")
+    ap.add_argument("--profile-steps", type=int, default=5)
+    ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--no-b1", action="store_true", help="measure batch 32 only (profiling runs)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build runs the nnc program on a single MI355X "
+              f"(--gpus {args.gpus}, WORLD_SIZE {world} requested); multi-GPU batch sharding is "
+              f"described in DESIGN.md and not launched.", file=sys.stderr)
+        return 2
+
+    pkg = load_package()
+    from nnc_py_amd import runtime
+    from nnc_py_amd.compiler import Executor, build_program, zoo
+    runtime.init(0)
+    graph = not args.no_graph
+    results = {}
+    tables = {}
+    runs = [(args.batch, args.steps)] + ([] if args.no_b1 else [(1, max(args.steps, 50))])
+    for batch, steps in runs:
+        log(f"building ResNet-18 batch {batch}")
+        prog = build_program(zoo.resnet18(batch=batch, seed=1), opt_level=3)
+        ex = Executor(prog, device=True)
+        x = np.random.default_rng(0).standard_normal((batch, 3, 224, 224)).astype(np.float32)
+        ex.set_input("input", x)
+        log(f"batch {batch}: {args.warmup} warmup + {steps} timed steps (graph={graph})")
+        dt = timed_steps(ex, steps, args.warmup, graph, runtime)
+        out = ex.get("output")
+        if not np.isfinite(out).all():
+            log("non-finite output")
+            return 1
+        results[batch] = {"images_per_s": batch * steps / dt, "ms_per_step": dt / steps * 1e3, "steps": steps}
+        log(f"batch {batch}: {results[batch]['ms_per_step']:.3f} ms/step, "
+            f"{results[batch]['images_per_s']:.1f} images/s")
+        if batch == args.batch:
+            tables[batch] = kernel_table(ex, runtime, args.profile_steps)
+        ex.close()
+
+    table = tables[args.batch]
+    dom = table[0]
+    peak = PEAK_FP32_MFMA_TF if dom["bound"] == "mfma" else PEAK_HBM_GBS
+    roofline = {"kernel": dom["kernel"], "bound": dom["bound"], "achieved": dom["achieved"],
+                "peak": peak, "unit": dom["unit"], "frac": round(dom["achieved"] / peak, 4),
+                "traffic": None, "avg_launch_us": dom["avg_us"],
+                "work_per_launch": dom["work_per_launch"]}
+    gpu_ms = sum(r["ms_per_step"] for r in table)
+    conv_ms = sum(r["ms_per_step"] for r in table if r["bound"] == "mfma")
+    conv_flops = zoo.resnet18_flops(args.batch)
+
+    cpu = None
+    if not args.skip_cpu:
+        log(f"CPU baseline: ResNet-18 batch 1, {args.cpu_iters} timed runs")
+        cpu = cpu_baseline(pkg, args.cpu_iters)
+
+    b = results[args.batch]
+    line = {
+        "metric": METRIC,
+        "value": round(b["images_per_s"], 2),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": b["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(b["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x ~ N(0,1) seed 0; He-normal conv/FC weights, biases N(0, 0.01^2), seed 1",
+        "config": {"workload": "ResNet-18 fp32 (BN folded), batch 32, 3x224x224, O3 nnc program, one hipGraph per step",
+                   "batch": args.batch, "opt_level": 3, "graph": graph},
+        "b1": ({"images_per_s": round(results[1]["images_per_s"], 2),
+                "ms_per_step": round(results[1]["ms_per_step"], 4)} if 1 in results else None),
+        "roofline": roofline,
+        "mfma_frac_all_conv": round(conv_flops / (conv_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TF, 4) if conv_ms else None,
+        "kernel_ms_per_step": round(gpu_ms, 4),
+        "per_kernel": [{k: r[k] for k in ("kernel", "launches_per_step", "avg_us", "bound", "achieved", "unit", "frac")}
+                       for r in table],
+        "cpu_baseline": cpu,
+        "host": platform.node(),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

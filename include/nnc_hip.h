@@ -85,6 +85,10 @@ int nnc_hip_profile_count(void);
  * number of launches and the summed milliseconds. Returns 0 on success. */
 int nnc_hip_profile_entry(int i, char* name, int cap, int64_t* launches,
                           double* total_ms);
+/* Entry i: algorithmic work summed over its launches - flops for the matrix
+ * kernels, bytes every launch must move through HBM at least once for the
+ * bandwidth-bound kernels (0 where not applicable). */
+int nnc_hip_profile_work(int i, double* flops, double* bytes);
 
 /* ---- launch capture ------------------------------------------------------
  * Record every kernel the following nnc_* calls enqueue into a hipGraph and

@@ -1,0 +1,170 @@
+"""Build and run a lowered program in-process.
+
+build_program() runs the pass pipeline of an optimisation level, plans the
+arena and lowers every node to an nnc_* call - the same program the code
+generator writes out as model.c/tensors.c. Executor binds it to one
+implementation of the ABI and runs nnc_run()'s call sequence through ctypes:
+
+  Executor(prog, device=True)   libnnc_hip.so, one device allocation holding
+                                the whole arena (activations + constants)
+  Executor(prog, lib=cpu_lib)   a host implementation of the same ABI on a
+                                host buffer with the same layout (used by the
+                                tests to compare whole networks)
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from .. import abi
+from .ir import Graph, Node
+from .lower import Call, lower
+from .passes import (MemoryPlan, check_plan, eliminate_dead_code, eliminate_identity, fuse_patterns,
+                     plan_memory, prepack_lowering)
+
+
+@dataclass
+class Program:
+    graph: Graph
+    order: list[Node]
+    plan: MemoryPlan
+    calls: list[Call]
+    opt_level: int
+
+
+def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None = None,
+                  max_memory: int | None = None) -> Program:
+    """Pass pipeline per optimisation level (passes/base.py:67-161 of the
+    reference), arena plan, lowering. Mutates `graph`."""
+    if opt_level >= 1:
+        eliminate_identity(graph)
+        eliminate_dead_code(graph)
+    if opt_level >= 3:
+        fuse_patterns(graph)
+        prepack_lowering(graph)
+    order = graph.topological_sort()
+    strategy = memory_strategy or ("basic" if opt_level == 0 else "cost_aware")
+    plan = plan_memory(graph, order, strategy, max_memory)
+    check_plan(graph, order, plan)
+    return Program(graph, order, plan, lower(graph, order), opt_level)
+
+
+class Executor:
+    def __init__(self, prog: Program, device: bool = True, lib: ctypes.CDLL | None = None):
+        self.prog = prog
+        self.device = device
+        g, plan = prog.graph, prog.plan
+        if device:
+            from .. import runtime
+            self.rt = runtime
+            self.lib = lib or runtime.load()
+            self.base = self.lib.nnc_hip_malloc(plan.total_bytes)
+            if not self.base:
+                raise runtime.HipError(f"cannot allocate a {plan.total_bytes}-byte arena")
+        else:
+            if lib is None:
+                raise ValueError("a host executor needs an ABI library")
+            self.lib = lib
+            self._host = np.zeros(plan.total_bytes + 256, np.uint8)
+            addr = self._host.ctypes.data
+            self.base = addr + (-addr % 256)
+        self._keep = []
+        self.tensors: dict[str, abi.Tensor] = {}
+        for name, off in plan.offsets.items():
+            t = g.tensors[name]
+            ten, sh = abi.make_tensor(self.base + off, abi.NUMPY_TO_NNC[t.dtype], t.shape, t.nbytes)
+            self._keep.append(sh)
+            self.tensors[name] = ten
+        for name, t in g.constants.items():
+            self._write(name, t.data)
+        self._calls = [(getattr(self.lib, c.op), self._args(c)) for c in prog.calls]
+
+    # -- memory --------------------------------------------------------------
+    def _addr(self, name: str) -> int:
+        return self.base + self.prog.plan.offsets[name]
+
+    def _write(self, name: str, arr: np.ndarray) -> None:
+        t = self.prog.graph.tensors[name]
+        a = np.ascontiguousarray(arr, dtype=t.dtype)
+        assert a.nbytes == t.nbytes, (name, a.shape, t.shape)
+        if self.device:
+            self.rt.check(self.lib.nnc_hip_memcpy_h2d(self._addr(name), a.ctypes.data, a.nbytes), "upload")
+        else:
+            ctypes.memmove(self._addr(name), a.ctypes.data, a.nbytes)
+
+    def _read(self, name: str) -> np.ndarray:
+        t = self.prog.graph.tensors[name]
+        out = np.empty(t.shape, t.dtype)
+        if self.device:
+            self.rt.check(self.lib.nnc_hip_memcpy_d2h(out.ctypes.data, self._addr(name), t.nbytes), "download")
+        else:
+            ctypes.memmove(out.ctypes.data, self._addr(name), t.nbytes)
+        return out
+
+    def set_input(self, name: str, arr: np.ndarray) -> None:
+        self._write(name, arr)
+
+    def get(self, name: str) -> np.ndarray:
+        if self.device:
+            self.rt.sync()
+        return self._read(name)
+
+    # -- calls ---------------------------------------------------------------
+    def _args(self, call: Call) -> tuple:
+        out = []
+        for spec in call.args:
+            kind = spec[0]
+            if kind == "t":
+                out.append(ctypes.pointer(self.tensors[spec[1]]))
+            elif kind == "tv":
+                t = self.prog.graph.tensors[spec[1]]
+                ten, sh = abi.make_tensor(self._addr(spec[1]), abi.NUMPY_TO_NNC[t.dtype], spec[2], t.nbytes)
+                self._keep += [ten, sh]
+                out.append(ctypes.pointer(ten))
+            elif kind == "null" or kind == "i64null":
+                out.append(None)
+            elif kind == "i":
+                out.append(int(spec[1]))
+            elif kind == "f":
+                out.append(float(spec[1]))
+            elif kind == "tl":
+                arr = (abi.TP * len(spec[1]))(*[ctypes.pointer(self.tensors[n]) for n in spec[1]])
+                self._keep.append(arr)
+                out.append(ctypes.cast(arr, abi.TPP))
+            elif kind == "i64":
+                arr = (ctypes.c_int64 * max(1, len(spec[1])))(*[int(v) for v in spec[1]])
+                self._keep.append(arr)
+                out.append(ctypes.cast(arr, abi.I64P))
+            else:
+                raise ValueError(f"unknown argument kind {kind!r}")
+        return tuple(out)
+
+    def run(self) -> None:
+        """One nnc_run(): every call in order (asynchronous on the device)."""
+        for fn, args in self._calls:
+            fn(*args)
+
+    def capture(self) -> None:
+        """Record run() into a hipGraph (device only); replay() launches it."""
+        self.rt.check(self.lib.nnc_hip_graph_begin(), "nnc_hip_graph_begin")
+        try:
+            self.run()
+        finally:
+            self.rt.check(self.lib.nnc_hip_graph_end(), "nnc_hip_graph_end")
+
+    def replay(self) -> None:
+        self.rt.check(self.lib.nnc_hip_graph_launch(), "nnc_hip_graph_launch")
+
+    def close(self) -> None:
+        if self.device and self.base:
+            self.lib.nnc_hip_free(self.base)
+            self.base = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

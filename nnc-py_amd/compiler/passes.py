@@ -1,0 +1,304 @@
+"""Graph passes of the MI355X pipeline.
+
+Same pass sequence and semantics as the reference's default pipelines
+(passes/base.py:67-161) for the parts that decide what the device executes:
+
+  O0   liveness -> memory plan
+  O1   identity elimination -> dead-code elimination -> liveness -> plan
+  O2   as O1 (the reference's spill re-plan targets its x86 fast/slow pools;
+       on the GPU the whole plan lives in HBM, see MemoryPlan)
+  O3   O1 + pattern fusion (conv_relu, conv_sigmoid, add_relu, add_sigmoid,
+       matmul_relu; pattern/fusion_patterns.py:105-153) + prepack lowering
+       (conv kernel kind, constant Gemm B transposed to [N, K];
+       passes/prepack_lowering.py:48-118)
+
+The memory plan places every non-constant tensor at an offset of one HBM
+arena, reusing the space of tensors whose last use has passed, and lets the
+element-wise ops write over an input that dies at that node, like the
+reference's cost_aware strategy (passes/strategies/cost_aware_allocator.py:
+39-48, 412-436). Constants get their own region of the same arena.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .ir import Graph, Node
+
+ALIGN = 256  # arena offsets; 16-byte vector loads need 16, 256 keeps rows cache-line aligned
+
+# ops that may write over a same-sized input that dies at the node
+# (cost_aware_allocator.py:39-48)
+INPLACE_OPS = {"Relu", "Sigmoid", "Tanh", "Add", "Sub", "Mul", "Div", "Clip",
+               "FusedAddRelu", "FusedAddSigmoid"}
+
+
+# ---------------------------------------------------------------------------
+# cleanup
+# ---------------------------------------------------------------------------
+def eliminate_identity(g: Graph) -> int:
+    """Bypass Identity nodes (passes/identity_elimination.py:13): consumers read
+    the Identity's input. An Identity producing a graph output is kept."""
+    removed = 0
+    for node in list(g.nodes):
+        if node.op_type != "Identity" or node.outputs[0] in g.outputs:
+            continue
+        src, dst = node.inputs[0], node.outputs[0]
+        for c in g.nodes:
+            c.inputs = [src if i == dst else i for i in c.inputs]
+        g.nodes.remove(node)
+        g.tensors.pop(dst, None)
+        removed += 1
+    return removed
+
+
+def eliminate_dead_code(g: Graph) -> int:
+    """Drop nodes none of whose outputs reach a graph output
+    (passes/dead_code_elimination.py:13), then unreferenced tensors."""
+    live = set(g.outputs)
+    keep = []
+    for node in reversed(g.topological_sort()):
+        if any(o in live for o in node.outputs):
+            keep.append(node)
+            live.update(i for i in node.inputs if i)
+    removed = len(g.nodes) - len(keep)
+    kept = set(id(n) for n in keep)
+    g.nodes = [n for n in g.nodes if id(n) in kept]
+    used = set(g.inputs) | set(g.outputs)
+    for n in g.nodes:
+        used.update(n.inputs)
+        used.update(n.outputs)
+    for name in list(g.tensors):
+        if name not in used:
+            del g.tensors[name]
+    return removed
+
+
+# ---------------------------------------------------------------------------
+# pattern fusion (O3)
+# ---------------------------------------------------------------------------
+_PATTERNS = [  # (producer, consumer, fused op), in priority order
+    ("Conv", "Relu", "FusedConvRelu"),
+    ("Conv", "Sigmoid", "FusedConvSigmoid"),
+    ("Add", "Relu", "FusedAddRelu"),
+    ("Add", "Sigmoid", "FusedAddSigmoid"),
+    ("MatMul", "Relu", "FusedMatMulRelu"),
+]
+
+
+def fuse_patterns(g: Graph) -> int:
+    """producer().only_used_by(consumer()) -> one fused node carrying the
+    producer's inputs/attrs and the consumer's output."""
+    fused = 0
+    for prod_op, cons_op, fused_op in _PATTERNS:
+        for node in list(g.nodes):
+            if node.op_type != prod_op or node.outputs[0] in g.outputs:
+                continue
+            users = g.consumers(node.outputs[0])
+            if len(users) != 1 or users[0].op_type != cons_op:
+                continue
+            user = users[0]
+            mid = node.outputs[0]
+            node.op_type = fused_op
+            node.outputs = list(user.outputs)
+            node.metadata["fused_from"] = [node.name, user.name]
+            g.nodes.remove(user)
+            g.tensors.pop(mid, None)
+            fused += 1
+    return fused
+
+
+def prepack_lowering(g: Graph) -> None:
+    """Conv kernel kind and constant Gemm B packing
+    (passes/prepack_lowering.py:48-118)."""
+    for node in g.nodes:
+        if node.op_type in ("Conv", "FusedConvRelu", "FusedConvSigmoid"):
+            kh, kw = node.attrs.get("kernel_shape", [1, 1])
+            sh, sw = node.attrs.get("strides", [1, 1])
+            pads = node.attrs.get("pads", [0, 0, 0, 0])
+            ph, pw = pads[0], pads[1]
+            kind = "generic"
+            if kh == 1 and kw == 1:
+                kind = "pointwise_1x1"
+            elif (kh, kw, sh, sw, ph, pw) == (3, 3, 1, 1, 1, 1):
+                kind = "spatial_3x3"
+            elif (kh, kw, sh, sw, ph, pw) == (7, 7, 2, 2, 3, 3):
+                kind = "stem_7x7_s2"
+            node.metadata.setdefault("lowering", {})["kernel_kind"] = kind
+        elif node.op_type == "Gemm" and len(node.inputs) >= 2:
+            low = node.metadata.setdefault("lowering", {})
+            wname = node.inputs[1]
+            w = g.tensors[wname]
+            if int(node.attrs.get("transA", 0)) != 0:
+                continue
+            if int(node.attrs.get("transB", 0)) == 1:
+                if w.is_constant:
+                    low["weight_pack"] = "rhs_transposed_constant"
+                continue
+            if w.is_constant and w.data.ndim == 2 and len(g.consumers(wname)) == 1:
+                w.data = np.ascontiguousarray(w.data.T)
+                w.shape = tuple(w.data.shape)
+                node.attrs["transB"] = 1
+                low["weight_pack"] = "rhs_transposed_constant"
+
+
+# ---------------------------------------------------------------------------
+# liveness and the arena plan
+# ---------------------------------------------------------------------------
+@dataclass
+class Liveness:
+    start: int
+    end: int
+    is_input: bool = False
+    is_output: bool = False
+
+
+def liveness(g: Graph, order: list[Node]) -> dict[str, Liveness]:
+    """[first definition, last use] per non-constant tensor over `order`
+    (passes/liveness.py:23-132). Graph inputs are live from step 0, graph
+    outputs to the end."""
+    live: dict[str, Liveness] = {}
+    last = len(order)
+    for name in g.inputs:
+        live[name] = Liveness(0, 0, is_input=True)
+    for idx, node in enumerate(order):
+        for o in node.outputs:
+            if o and not g.tensors[o].is_constant:
+                live.setdefault(o, Liveness(idx, idx))
+        for i in node.inputs:
+            if i in live:
+                live[i].end = max(live[i].end, idx)
+    for name in g.outputs:
+        if name in live:
+            live[name].end = last
+            live[name].is_output = True
+    for name in g.inputs:  # inputs stay resident across repeated runs
+        live[name].end = last
+    return live
+
+
+@dataclass
+class MemoryPlan:
+    """Offsets of every tensor in one arena: [activations | constants]."""
+    offsets: dict[str, int] = field(default_factory=dict)
+    activation_bytes: int = 0
+    constant_offset: int = 0
+    total_bytes: int = 0
+    inplace: dict[str, str] = field(default_factory=dict)  # output -> reused input
+
+
+def _align(x: int) -> int:
+    return (x + ALIGN - 1) // ALIGN * ALIGN
+
+
+def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
+                max_memory: int | None = None) -> MemoryPlan:
+    """Greedy offset assignment over the execution order.
+
+    basic:       every activation gets its own region (no reuse).
+    cost_aware:  freed regions are reused best-fit; element-wise nodes write
+                 over a same-sized input that dies there.
+    Raises ValueError when the activations exceed max_memory (the reference
+    raises the same way when the budget is below the peak node demand,
+    cost_aware_allocator.py:88-102)."""
+    live = liveness(g, order)
+    sizes = {n: _align(g.tensors[n].nbytes) for n in live}
+    plan = MemoryPlan()
+    free: list[tuple[int, int]] = []  # (offset, size)
+    top = 0
+
+    def take(size: int) -> int:
+        nonlocal top
+        if strategy == "cost_aware":
+            best = None
+            for k, (off, sz) in enumerate(free):
+                if sz >= size and (best is None or sz < free[best][1]):
+                    best = k
+            if best is not None:
+                off, sz = free.pop(best)
+                if sz > size:
+                    free.append((off + size, sz - size))
+                return off
+        off = top
+        top += size
+        return off
+
+    def release(off: int, size: int) -> None:
+        if strategy != "cost_aware":
+            return
+        free.append((off, size))
+        free.sort()
+        merged = []
+        for o, s in free:
+            if merged and merged[-1][0] + merged[-1][1] == o:
+                merged[-1] = (merged[-1][0], merged[-1][1] + s)
+            else:
+                merged.append((o, s))
+        free[:] = merged
+        # a free block ending at the top shrinks the pool
+        nonlocal top
+        if free and free[-1][0] + free[-1][1] == top:
+            top = free.pop()[0]
+
+    for name in g.inputs:
+        plan.offsets[name] = take(sizes[name])
+    for idx, node in enumerate(order):
+        reused = set()
+        for o in node.outputs:
+            if not o or o not in live or o in plan.offsets:
+                continue
+            slot = None
+            if strategy == "cost_aware" and node.op_type in INPLACE_OPS:
+                for i in node.inputs:
+                    li = live.get(i)
+                    if (li and li.end == idx and not li.is_output and not li.is_input
+                            and i in plan.offsets and i not in reused and sizes[i] == sizes[o]):
+                        slot = plan.offsets[i]
+                        reused.add(i)
+                        plan.inplace[o] = i
+                        break
+            plan.offsets[o] = slot if slot is not None else take(sizes[o])
+        # graph inputs stay resident so nnc_run() can be repeated on them
+        for i in set(node.inputs):
+            li = live.get(i)
+            if li and li.end == idx and not li.is_output and not li.is_input and i not in reused:
+                release(plan.offsets[i], sizes[i])
+        # outputs nobody reads die immediately
+        for o in node.outputs:
+            lo = live.get(o)
+            if lo and lo.end == idx and not lo.is_output and o not in node.inputs:
+                release(plan.offsets[o], sizes[o])
+    plan.activation_bytes = _align(max([top] + [plan.offsets[n] + sizes[n] for n in plan.offsets]))
+    if max_memory is not None and plan.activation_bytes > max_memory:
+        raise ValueError(f"max_memory ({max_memory}) < peak activation footprint "
+                         f"({plan.activation_bytes}) of the arena plan")
+    off = plan.activation_bytes
+    plan.constant_offset = off
+    for name, t in g.constants.items():
+        plan.offsets[name] = off
+        off += _align(t.nbytes)
+    plan.total_bytes = _align(off)
+    return plan
+
+
+def check_plan(g: Graph, order: list[Node], plan: MemoryPlan) -> None:
+    """Invariants: simultaneously live tensors never overlap (except an
+    in-place output and the input it replaces), every offset aligned, every
+    tensor inside the arena."""
+    live = liveness(g, order)
+    names = list(live)
+    for n in plan.offsets:
+        assert plan.offsets[n] % ALIGN == 0, n
+        assert plan.offsets[n] + g.tensors[n].nbytes <= plan.total_bytes, n
+    for a_i, a in enumerate(names):
+        la, oa, sa = live[a], plan.offsets[a], g.tensors[a].nbytes
+        for b in names[a_i + 1:]:
+            lb, ob, sb = live[b], plan.offsets[b], g.tensors[b].nbytes
+            overlap_t = la.start <= lb.end and lb.start <= la.end
+            overlap_m = oa < ob + sb and ob < oa + sa
+            if overlap_t and overlap_m:
+                pair = plan.inplace.get(a) == b or plan.inplace.get(b) == a
+                if not pair:
+                    raise AssertionError(f"{a} and {b} overlap in time and memory")

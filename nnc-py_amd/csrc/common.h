@@ -49,8 +49,14 @@ size_t workspace_capacity();
 // ---------------------------------------------------------------------------
 // kernel launch with optional hipEvent timing (keyed by kernel name)
 // ---------------------------------------------------------------------------
+// Algorithmic work of the next launch: flops for matrix kernels, bytes that
+// must cross HBM at least once for bandwidth kernels. Recorded with the
+// launch's time in the timing table (roofline figures). Cleared by launch().
+void set_work(double flops, double bytes);
+
 struct TimedScope {
     const char* name;
+    double flops = 0.0, bytes = 0.0;
     hipEvent_t start = nullptr, stop = nullptr;
     explicit TimedScope(const char* n);
     ~TimedScope();

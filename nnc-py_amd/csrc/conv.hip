@@ -177,9 +177,16 @@ typedef Tile<128, 128, 32, 2, 2> ConvT128;  // Co >= 128: 2x2 blocks per wave
 typedef Tile<64, 128, 32, 1, 4> ConvT64;    // Co == 64: 2x1 blocks per wave
 typedef Tile<64, 64, 32, 2, 2> ConvTSmall;  // small problems: 1 block per wave
 
+// Timing-table key of one kernel instance: conv_igemm_<BM>x<BN>_k<kh>x<kw>_<v4|s1>
 template <class T, int KH, int KW>
-static void launch_conv_t(const ConvArgs& a, bool avec, const char* name) {
+static void launch_conv_t(const ConvArgs& a, bool avec, const char*) {
     const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(256);
+    char name[64];
+    if (KH > 0)
+        snprintf(name, sizeof name, "conv_igemm_%dx%d_k%dx%d_%s", T::BM, T::BN, KH, KW, avec ? "v4" : "s1");
+    else
+        snprintf(name, sizeof name, "conv_igemm_%dx%d_kany_%s", T::BM, T::BN, avec ? "v4" : "s1");
+    set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
     if (avec)
         launch(name, conv_igemm_k<T, KH, KW, true>, grid, block, 0, a);
     else
@@ -226,6 +233,7 @@ static void launch_conv_k(ConvArgs& a, bool avec, const char* name) {
         launch_conv_t<T, 0, 0>(a, avec, name);
     if (a.ws) {
         const int64_t total = (int64_t)a.Co * a.Npix;
+        set_work(0.0, 4.0 * (double)total * (a.splits + 1));
         launch("conv_splitk_reduce", conv_splitk_reduce_k, dim3(grid_for(total, 1)), dim3(256), 0,
                (const float*)a.ws, a.bias, a.out, a.splits, a.Co, a.Npix, a.Ho * a.Wo, a.act);
     }

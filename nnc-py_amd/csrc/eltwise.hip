@@ -146,6 +146,7 @@ static void binary_entry(const char* name, Tensor* a, Tensor* b, Tensor* out) {
     const float* y = static_cast<const float*>(b->data);
     float* z = static_cast<float*>(out->data);
     const bool a_direct = an >= cnt, b_direct = bn >= cnt;
+    set_work(0.0, 4.0 * ((double)(an < cnt ? an : cnt) + (double)(bn < cnt ? bn : cnt) + (double)cnt));
     if (a_direct && b_direct)
         launch_binary<OP, kDirect, kDirect>(name, x, y, z, cnt, an, bn);
     else if (a_direct && bn == 1)
@@ -215,6 +216,7 @@ static void unary_entry(const char* name, Tensor* in, Tensor* out, float lo = 0.
     }
     const float* x = static_cast<const float*>(in->data);
     float* z = static_cast<float*>(out->data);
+    set_work(0.0, 8.0 * (double)n);
     uint32_t done = 0;
     if (aligned16(x) && aligned16(z) && n >= 4) {
         const uint32_t n4 = (uint32_t)(n / 4);

@@ -244,11 +244,18 @@ static void launch_mfma(GemmArgs& g, int batches, const char* name) {
     g.splits = (int)ceil_div(g.K, g.k_per_split);
     if (g.splits < 1) g.splits = 1;
     if (g.splits == 1) g.ws = nullptr;
-    launch(name, gemm_mfma_k<T, AK, BKIND>, dim3(g.tiles_m * g.tiles_n * g.splits, batches),
+    static const char* kinds[4] = {"k4", "k1", "x4", "x1"};
+    char kname[64];
+    snprintf(kname, sizeof kname, "gemm_mfma_%dx%d_%s%s", T::BM, T::BN, kinds[AK], kinds[BKIND]);
+    set_work(2.0 * g.M * (double)g.N * g.K * batches, 0.0);
+    launch(kname, gemm_mfma_k<T, AK, BKIND>, dim3(g.tiles_m * g.tiles_n * g.splits, batches),
            dim3(256), 0, g);
-    if (g.ws)
+    (void)name;
+    if (g.ws) {
+        set_work(0.0, 4.0 * (double)g.M * g.N * batches * (g.splits + 1));
         launch("gemm_splitk_reduce", gemm_splitk_reduce_k, dim3(grid_for((int64_t)g.M * g.N * batches, 1)),
                dim3(256), 0, g, batches);
+    }
 }
 
 template <int AK, int BKIND>
@@ -325,20 +332,23 @@ static void gemm_run(const GemmProblem& p, const char* name) {
         splits = (int)ceil_div(p.K, k_per);
         g.ws = ws;
         g.splits = splits;
+        set_work(2.0 * p.K * (double)p.N, 4.0 * ((double)p.K * p.N + p.K + (double)p.N * splits));
         if (vec)
-            launch(name, gemv_xc_k<true>, dim3(col_blocks, splits), dim3(256), 0, p.A, a_stride, p.B,
+            launch("gemv_xc_v4", gemv_xc_k<true>, dim3(col_blocks, splits), dim3(256), 0, p.A, a_stride, p.B,
                    p.ldb, ws, p.N, p.K, k_per);
         else
-            launch(name, gemv_xc_k<false>, dim3(col_blocks, splits), dim3(256), 0, p.A, a_stride,
+            launch("gemv_xc_s1", gemv_xc_k<false>, dim3(col_blocks, splits), dim3(256), 0, p.A, a_stride,
                    p.B, p.ldb, ws, p.N, p.K, k_per);
+        set_work(0.0, 4.0 * (double)p.N * (splits + 1));
         launch("gemv_reduce", gemv_reduce_k, dim3((unsigned)ceil_div(p.N, 256)), dim3(256), 0, g);
         return;
     }
     if (p.batches == 1 && p.a_kc && p.b_kc && (p.M == 1 || p.N == 1 || (int64_t)p.M * p.N <= 64)) {
         const bool vec = aligned16(p.A) && aligned16(p.B) && p.lda % 4 == 0 && p.ldb % 4 == 0;
         const dim3 grid((unsigned)ceil_div((int64_t)p.M * p.N, 4));
-        if (vec) launch(name, dot_k<true>, grid, dim3(256), 0, g);
-        else launch(name, dot_k<false>, grid, dim3(256), 0, g);
+        set_work(2.0 * p.M * (double)p.N * p.K, 4.0 * ((double)p.M * p.K + (double)p.N * p.K + (double)p.M * p.N));
+        if (vec) launch("dot_rows_v4", dot_k<true>, grid, dim3(256), 0, g);
+        else launch("dot_rows_s1", dot_k<false>, grid, dim3(256), 0, g);
         return;
     }
     // MFMA tiles. 16-byte loads need 4-float alignment of every row/batch start.

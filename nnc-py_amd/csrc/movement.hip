@@ -25,6 +25,7 @@ __global__ void __launch_bounds__(256) copy1_k(const uint8_t* src, uint8_t* dst,
 
 void device_copy(const char* name, const void* src, void* dst, size_t bytes) {
     if (src == dst || bytes == 0) return;
+    set_work(0.0, 2.0 * (double)bytes);
     const uint8_t* s = static_cast<const uint8_t*>(src);
     uint8_t* d = static_cast<uint8_t*>(dst);
     size_t done = 0;
@@ -101,6 +102,7 @@ template <typename E>
 static void slab_copy(const char* name, const void* src, int64_t src_row, void* dst, int64_t dst_row,
                       int64_t outer, int64_t slab) {
     if (outer * slab == 0) return;
+    set_work(0.0, 2.0 * (double)(outer * slab) * sizeof(E));
     // 16-byte granules when every row start stays aligned
     const int64_t per16 = 16 / (int64_t)sizeof(E);
     if (aligned16(src) && aligned16(dst) && slab % per16 == 0 && src_row % per16 == 0 &&
@@ -301,6 +303,7 @@ void nnc_transpose(Tensor* in, Tensor* out, int64_t* perm, int ndim) {
             return fail(NNC_HIP_EINVAL, name, "permutation does not match the shapes");
     const int64_t total = numel(out);
     if (total == 0) return;
+    set_work(0.0, 8.0 * (double)total);
     // [B..][R][C] -> [B..][C][R]: leading axes kept, last two swapped
     bool swap_last = ndim >= 2 && pm[ndim - 1] == ndim - 2 && pm[ndim - 2] == ndim - 1;
     for (int d = 0; d < ndim - 2 && swap_last; ++d) swap_last = pm[d] == d;

@@ -295,6 +295,7 @@ void nnc_softmax(Tensor* in, Tensor* out, int axis) {
     const float* x = (const float*)in->data;
     float* y = (float*)out->data;
     if (len >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "axis too long");
+    set_work(0.0, 8.0 * (double)(outer * len * inner));
     if (inner == 1) {
         const int dim = (int)len;
         const bool v4 = dim % 4 == 0 && aligned16(x) && aligned16(y);
@@ -324,6 +325,7 @@ void nnc_layernorm(Tensor* in, Tensor* scale, Tensor* bias, Tensor* out, int axi
     if ((g && numel(scale) < len) || (b && numel(bias) < len))
         return fail(NNC_HIP_EINVAL, name, "scale/bias shorter than the axis");
     float* y = (float*)out->data;
+    set_work(0.0, 8.0 * (double)(outer * span) + (g ? 4.0 * len : 0.0) + (b ? 4.0 * len : 0.0));
     const bool v4 = span % 4 == 0 && span < (1 << 30) && aligned16(x) && aligned16(y);
     const int sp = (int)span, inn = (int)inner;
     if (v4 && span <= 256) return layernorm_v4<1>(x, g, b, y, outer, sp, inn, eps, name);
@@ -344,6 +346,7 @@ static void reduce_entry(const char* name, Tensor* in, Tensor* out, int axis, bo
     if (outer * inner == 0) return;
     const float* x = (const float*)in->data;
     float* y = (float*)out->data;
+    set_work(0.0, 4.0 * (double)(outer * len * inner + outer * inner));
     if (inner == 1) {
         if (mean) launch(name, reduce_rows_k<true>, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, len);
         else launch(name, reduce_rows_k<false>, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, len);

@@ -94,6 +94,7 @@ static void pool_entry(const char* name, Tensor* in, Tensor* out, int kh, int kw
         launch(name, fill_value_k, dim3(grid_for(numel(out), 1)), dim3(256), 0, a.out, numel(out),
                -3.402823e38f);
     }
+    set_work(0.0, 4.0 * ((double)numel(in) + (double)nc * a.Ho * a.Wo));
     launch(name, pool2d_k<MAX>, dim3(grid_for(nc * a.Ho * a.Wo, 1)), dim3(256), 0, a);
 }
 

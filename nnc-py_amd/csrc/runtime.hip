@@ -73,13 +73,20 @@ size_t workspace_capacity() { return g_ctx.workspace_bytes; }
 // ---------------------------------------------------------------------------
 struct Pending {
     std::string name;
+    double flops, bytes;
     hipEvent_t start, stop;
 };
 struct Stat {
     std::string name;
     int64_t launches = 0;
-    double ms = 0.0;
+    double ms = 0.0, flops = 0.0, bytes = 0.0;
 };
+static double g_next_flops = 0.0, g_next_bytes = 0.0;
+
+void set_work(double flops, double bytes) {
+    g_next_flops = flops;
+    g_next_bytes = bytes;
+}
 static std::vector<Pending> g_pending;
 static std::vector<hipEvent_t> g_event_pool;
 static std::vector<Stat> g_stats;
@@ -95,7 +102,8 @@ static hipEvent_t take_event() {
     return e;
 }
 
-TimedScope::TimedScope(const char* n) : name(n) {
+TimedScope::TimedScope(const char* n) : name(n), flops(g_next_flops), bytes(g_next_bytes) {
+    g_next_flops = g_next_bytes = 0.0;
     if (!g_ctx.profiling || g_ctx.capturing) return;
     start = take_event();
     stop = take_event();
@@ -105,7 +113,7 @@ TimedScope::TimedScope(const char* n) : name(n) {
 TimedScope::~TimedScope() {
     if (!start) return;
     (void)hipEventRecord(stop, g_ctx.stream);
-    g_pending.push_back({name, start, stop});
+    g_pending.push_back({name, flops, bytes, start, stop});
 }
 
 static void resolve_pending() {
@@ -118,11 +126,13 @@ static void resolve_pending() {
         for (auto& st : g_stats)
             if (st.name == p.name) { s = &st; break; }
         if (!s) {
-            g_stats.push_back(Stat{p.name, 0, 0.0});
+            g_stats.push_back(Stat{p.name, 0, 0.0, 0.0, 0.0});
             s = &g_stats.back();
         }
         s->launches += 1;
         s->ms += ms;
+        s->flops += p.flops;
+        s->bytes += p.bytes;
         g_event_pool.push_back(p.start);
         g_event_pool.push_back(p.stop);
     }
@@ -302,6 +312,14 @@ int nnc_hip_profile_entry(int i, char* name, int cap, int64_t* launches, double*
     }
     if (launches) *launches = g_stats[i].launches;
     if (total_ms) *total_ms = g_stats[i].ms;
+    return NNC_HIP_OK;
+}
+
+int nnc_hip_profile_work(int i, double* flops, double* bytes) {
+    resolve_pending();
+    if (i < 0 || i >= (int)g_stats.size()) return NNC_HIP_EINVAL;
+    if (flops) *flops = g_stats[i].flops;
+    if (bytes) *bytes = g_stats[i].bytes;
     return NNC_HIP_OK;
 }
 

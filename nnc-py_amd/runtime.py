@@ -48,6 +48,8 @@ _HIP_SIGNATURES = {
     "nnc_hip_profile_entry": ([ctypes.c_int, ctypes.c_char_p, ctypes.c_int,
                                ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_double)],
                               ctypes.c_int),
+    "nnc_hip_profile_work": ([ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
+                             ctypes.c_int),
     "nnc_hip_graph_begin": ([], ctypes.c_int),
     "nnc_hip_graph_end": ([], ctypes.c_int),
     "nnc_hip_graph_launch": ([], ctypes.c_int),
@@ -186,15 +188,20 @@ def profile_reset() -> None:
     load().nnc_hip_profile_reset()
 
 
-def profile_table() -> list[tuple[str, int, float]]:
-    """[(kernel name, launches, total ms)] accumulated since the last reset."""
+def profile_table() -> list[dict]:
+    """Per kernel name since the last reset: launches, total ms, and the
+    algorithmic flops / bytes of those launches."""
     lib = load()
     out = []
     name = ctypes.create_string_buffer(128)
     for i in range(lib.nnc_hip_profile_count()):
         launches = ctypes.c_int64()
         ms = ctypes.c_double()
+        flops = ctypes.c_double()
+        nbytes = ctypes.c_double()
         check(lib.nnc_hip_profile_entry(i, name, 128, ctypes.byref(launches), ctypes.byref(ms)),
               "nnc_hip_profile_entry")
-        out.append((name.value.decode(), launches.value, ms.value))
+        check(lib.nnc_hip_profile_work(i, ctypes.byref(flops), ctypes.byref(nbytes)), "nnc_hip_profile_work")
+        out.append({"name": name.value.decode(), "launches": launches.value, "ms": ms.value,
+                    "flops": flops.value, "bytes": nbytes.value})
     return out

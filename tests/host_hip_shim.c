@@ -1,0 +1,55 @@
+/*
+ * TEST INFRASTRUCTURE ONLY: a host-memory stand-in for the lifecycle half of
+ * include/nnc_hip.h, so that code generated for the mi355x target can be
+ * linked with the CPU oracle (oracle/liboracle.so) and its nnc_run() checked
+ * on a machine without a GPU. The arena is a host allocation; copies are
+ * memcpy; graph capture reports "unsupported" so generated code takes its
+ * node-by-node path. Never linked into the product.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "nnc_hip.h"
+
+static char* arena = NULL;
+static size_t arena_size = 0;
+
+int nnc_hip_init(int device) { (void)device; return 0; }
+void nnc_hip_shutdown(void) { free(arena); arena = NULL; arena_size = 0; }
+int nnc_hip_arena_reserve(size_t bytes) {
+    if (arena && bytes <= arena_size) return 0;
+    free(arena);
+    arena = aligned_alloc(256, (bytes + 255) / 256 * 256);
+    arena_size = arena ? bytes : 0;
+    return arena ? 0 : NNC_HIP_ENOMEM;
+}
+void* nnc_hip_arena_base(void) { return arena; }
+size_t nnc_hip_arena_size(void) { return arena_size; }
+int nnc_hip_bind(Tensor* t, size_t offset) {
+    if (!arena || offset + (size_t)t->nbytes > arena_size) return NNC_HIP_EINVAL;
+    t->data = arena + offset;
+    return 0;
+}
+void* nnc_hip_malloc(size_t bytes) { return malloc(bytes); }
+void nnc_hip_free(void* p) { free(p); }
+int nnc_hip_upload(Tensor* t, const void* src) { memcpy(t->data, src, (size_t)t->nbytes); return 0; }
+int nnc_hip_download(const Tensor* t, void* dst) { memcpy(dst, t->data, (size_t)t->nbytes); return 0; }
+int nnc_hip_memcpy_h2d(void* d, const void* s, size_t n) { memcpy(d, s, n); return 0; }
+int nnc_hip_memcpy_d2h(void* d, const void* s, size_t n) { memcpy(d, s, n); return 0; }
+int nnc_hip_sync(void) { return 0; }
+void* nnc_hip_stream(void) { return NULL; }
+int nnc_hip_last_error(void) { return 0; }
+const char* nnc_hip_last_error_message(void) { return "host shim"; }
+void nnc_hip_clear_error(void) {}
+void nnc_hip_profile_enable(int on) { (void)on; }
+void nnc_hip_profile_reset(void) {}
+int nnc_hip_profile_count(void) { return 0; }
+int nnc_hip_profile_entry(int i, char* n, int c, int64_t* l, double* m) {
+    (void)i; (void)n; (void)c; (void)l; (void)m;
+    return NNC_HIP_EINVAL;
+}
+int nnc_hip_profile_work(int i, double* f, double* b) { (void)i; (void)f; (void)b; return NNC_HIP_EINVAL; }
+int nnc_hip_graph_begin(void) { return NNC_HIP_EUNSUPP; }
+int nnc_hip_graph_end(void) { return NNC_HIP_EUNSUPP; }
+int nnc_hip_graph_launch(void) { return NNC_HIP_EUNSUPP; }
+void nnc_hip_graph_destroy(void) {}
