@@ -9,17 +9,16 @@
 //   B[k][j] = input[n][ci][oh*sh - ph + r][ow*sw - pw + c], 0 outside
 // The B tile is gathered straight from the NCHW input (no im2col buffer);
 // consecutive lanes take consecutive pixels, so the gathers coalesce along
-// the input rows. D's 32x32 MFMA layout puts consecutive pixels in
-// consecutive lanes, so the NCHW stores coalesce too. Bias and the fused
-// activation are applied in the epilogue.
+// input rows. D's 32x32 MFMA layout puts consecutive pixels in consecutive
+// lanes, so the NCHW stores coalesce too. Bias and the fused activation are
+// applied in the epilogue (or in the stream-K fixup for shared tiles).
 //
 // Padding follows the reference: only the top/left pads are arguments, the
 // bottom/right extent comes from the output shape (c_emitter.py:1051-1058).
 //
-// When Co x pixels gives too few workgroups to fill the 256 CUs (the 14x14
-// and 7x7 stages), K is split over workgroups; each writes an fp32 partial
-// tile to the workspace and a second kernel sums the partials in a fixed
-// order and applies bias + activation (deterministic, no atomics).
+// Accumulation: one fp32 MFMA chain per workgroup segment (K <= 4608 at
+// ResNet-18 scale stays inside 1e-4 abs / 1e-3 rel of the reference's fp64
+// sum); shared tiles add their segments in fixed workgroup order.
 #include <math.h>
 
 #include "mfma_tile.h"
@@ -39,22 +38,23 @@ struct ConvArgs {
     const float* w;
     const float* bias;
     float* out;
-    float* ws;  // split-K partials [split][Co][Npix] or null
+    float* ws;  // stream-K partial tiles
     int N, Ci, H, W, Co, Ho, Wo, kh, kw, sh, sw, ph, pw;
-    int K, Npix;
-    int tiles_m, tiles_n, splits, k_per_split, act;
+    int K, Npix, act;
+    int tiles_m, tiles_n;
 };
 
-// B operand: gathers input taps for X consecutive output pixels.
-// KH/KW > 0 fix the kernel size at compile time (cheap k -> (ci, r, c)).
+// B operand: gathers input taps for X consecutive output pixels. KH/KW > 0
+// fix the kernel size at compile time (k -> (ci, r, c) by constant division).
+// Buffer loads over the whole input tensor (byte offsets < 2^31, checked on
+// the host); out-of-image taps get an out-of-range offset and read 0.
 template <int X, int BK, int LD, int KH, int KW>
 struct ConvGather {
     static constexpr int KROWS = 256 / X;
     static constexpr int PER = X * BK / 256;
     static_assert(256 % X == 0 && BK % KROWS == 0, "gather shape");
-    const float* img;
-    int h0, w0, H, W, K, kw_rt, khw_rt;
-    int64_t HW;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int img, h0, w0, H, W, K, kw_rt, khw_rt, HW;
     bool valid;
     int xx, kk;
     float v[PER];
@@ -74,11 +74,12 @@ struct ConvGather {
         w0 = ow * a.sw - a.pw;
         H = a.H;
         W = a.W;
-        HW = (int64_t)a.H * a.W;
+        HW = a.H * a.W;
         K = a.K;
         kw_rt = a.kw;
         khw_rt = a.kh * a.kw;
-        img = a.in + (int64_t)n * a.Ci * HW;
+        img = n * a.Ci * HW;
+        rsrc = make_rsrc(a.in);
     }
     __device__ void load(int k0) {
         const int khw = KH > 0 ? KH * KW : khw_rt;
@@ -91,10 +92,8 @@ struct ConvGather {
             const int r = t / kwid;
             const int c = t - r * kwid;
             const int h = h0 + r, w = w0 + c;
-            float val = 0.f;
-            if (valid && k < K && (unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W)
-                val = img[ci * HW + (int64_t)h * W + w];
-            v[p] = val;
+            const bool ok = valid && k < K && (unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W;
+            v[p] = load_f32(rsrc, ok ? (uint32_t)(img + ci * HW + h * W + w) * 4u : kOutOfRange);
         }
     }
     __device__ void store(float* S) const {
@@ -104,72 +103,85 @@ struct ConvGather {
 };
 
 template <class T, int KH, int KW, bool AVEC>
-__global__ void __launch_bounds__(256, 2) conv_igemm_k(ConvArgs a) {
-    __shared__ float lds[T::LDS_FLOATS];
-    float* As = lds;
-    float* Bs = lds + T::BK * T::LDA;
-    const int total = a.tiles_m * a.tiles_n * a.splits;
-    const int lin = xcd_remap(blockIdx.x, total);
-    const int mt = lin % a.tiles_m;
-    const int rest = lin / a.tiles_m;
-    const int nt = rest % a.tiles_n;
-    const int s = rest / a.tiles_n;
-    const int i0 = mt * T::BM, j0 = nt * T::BN;
-    const int kb = s * a.k_per_split;
-    const int ke = min(a.K, kb + a.k_per_split);
-
-    typedef typename std::conditional<AVEC, KContigLoader4<T::BM, T::BK, T::LDA>,
-                                      KContigLoader<T::BM, T::BK, T::LDA>>::type LA;
-    LA la;
-    la.init(a.w + (int64_t)i0 * a.K, a.K, a.Co - i0, a.K);
-    ConvGather<T::BN, T::BK, T::LDB, KH, KW> lb;
-    lb.init(a, j0);
-
-    floatx16 sum[T::TM][T::TN];
-    mfma_mainloop<T>(la, lb, kb, ke, As, Bs, sum);
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wi = (wave / T::WN) * T::WAVE_M;
-    const int wj = (wave % T::WN) * T::WAVE_N;
+__global__ void __launch_bounds__(256, 2) conv_streamk_k(ConvArgs a, StreamK sk) {
+    extern __shared__ float lds[];
+    const int g = xcd_remap(blockIdx.x, sk.G);
     const int hw = a.Ho * a.Wo;
+    SegmentWalker walk(sk, g);
+    Segment seg;
+    while (walk.next(sk, seg)) {
+        const int mt = seg.tile % a.tiles_m, nt = seg.tile / a.tiles_m;
+        const int i0 = mt * T::BM, j0 = nt * T::BN;
+
+        typedef typename std::conditional<AVEC, KContigLoader4<T::BM, T::BK, T::LDA>,
+                                          KContigLoader<T::BM, T::BK, T::LDA>>::type LA;
+        LA la;
+        la.init(a.w + (int64_t)i0 * a.K, a.K, a.Co - i0, a.K);
+        ConvGather<T::BN, T::BK, T::LDB, KH, KW> lb;
+        lb.init(a, j0);
+        floatx16 sum[T::TM][T::TN];
+        mfma_mainloop<T, false>(la, lb, seg.kb * T::BK, min(a.K, seg.ke * T::BK), lds, sum);
+
+        if (seg.slot < 0) {
 #pragma unroll
-    for (int tn = 0; tn < T::TN; ++tn) {
-        const int pix = j0 + wj + tn * 32 + (lane & 31);
-        if (pix >= a.Npix) continue;
-        const int n = pix / hw;
-        const int p = pix - n * hw;
-        float* obase = a.ws ? a.ws + (int64_t)s * a.Co * a.Npix + pix
-                            : a.out + (int64_t)n * a.Co * hw + p;
-        const int64_t cstride = a.ws ? (int64_t)a.Npix : (int64_t)hw;
+            for (int tn = 0; tn < T::TN; ++tn) {
+                const int pix = j0 + acc_col<T>(tn);
+                if (pix >= a.Npix) continue;
+                const int n = pix / hw;
+                float* obase = a.out + (int64_t)n * a.Co * hw + (pix - n * hw);
 #pragma unroll
-        for (int tm = 0; tm < T::TM; ++tm)
+                for (int tm = 0; tm < T::TM; ++tm)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int co = i0 + wi + tm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (co >= a.Co) continue;
-                float v = sum[tm][tn][r];
-                if (!a.ws) v = activate(v + (a.bias ? a.bias[co] : 0.f), a.act);
-                obase[co * cstride] = v;
+                    for (int r = 0; r < 16; ++r) {
+                        const int co = i0 + acc_row<T>(tm, r);
+                        if (co < a.Co)
+                            obase[(int64_t)co * hw] = activate(sum[tm][tn][r] + (a.bias ? a.bias[co] : 0.f), a.act);
+                    }
             }
+        } else {
+            float* slot = partial_slot<T>(a.ws, g, seg.slot);
+#pragma unroll
+            for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) slot[acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)] = sum[tm][tn][r];
+        }
     }
 }
 
-// out[n][co][p] = act(bias[co] + sum over splits of ws[s][co][n*hw + p])
-__global__ void __launch_bounds__(256) conv_splitk_reduce_k(const float* ws, const float* bias,
-                                                            float* out, int splits, int Co, int Npix,
-                                                            int hw, int act) {
-    const int64_t total = (int64_t)Co * Npix;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        const int co = (int)(e / Npix);
-        const int pix = (int)(e - (int64_t)co * Npix);
-        float v = 0.f;
-        for (int s = 0; s < splits; ++s) v += ws[((int64_t)s * Co + co) * Npix + pix];
-        v = activate(v + (bias ? bias[co] : 0.f), act);
+// Grid (chunks, stream-K tiles): workgroup (c, t) finishes chunk c of tile t
+// (256 float4 of the BM x BN tile). Tiles covered by a single workgroup were
+// written by it; shared tiles sum their partials in workgroup order, then
+// bias + act. Each thread handles 4 consecutive pixels of a tile row.
+template <class T>
+__global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
+    const int t = blockIdx.y;
+    int g0, g1, first_slot;
+    if (!tile_partials(sk, t, g0, g1, first_slot)) return;
+    const int e4 = blockIdx.x * 256 + threadIdx.x;
+    if (e4 >= T::BM * T::BN / 4) return;
+    const int mt = t % a.tiles_m, nt = t / a.tiles_m;
+    const int co = mt * T::BM + (e4 * 4) / T::BN;
+    const int p0 = nt * T::BN + (e4 * 4) % T::BN;
+    if (co >= a.Co || p0 >= a.Npix) return;
+    float4 v = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g0, first_slot))[e4];
+    for (int g = g0 + 1; g <= g1; ++g) {
+        const float4 p = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g, 0))[e4];
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
+    }
+    const int hw = a.Ho * a.Wo;
+    const float b = a.bias ? a.bias[co] : 0.f;
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int pix = p0 + q;
+        if (pix >= a.Npix) break;
         const int n = pix / hw;
-        const int p = pix - n * hw;
-        out[((int64_t)n * Co + co) * hw + p] = v;
+        a.out[((int64_t)n * a.Co + co) * hw + (pix - n * hw)] = activate(vals[q] + b, a.act);
     }
 }
 
@@ -177,66 +189,54 @@ typedef Tile<128, 128, 32, 2, 2> ConvT128;  // Co >= 128: 2x2 blocks per wave
 typedef Tile<64, 128, 32, 1, 4> ConvT64;    // Co == 64: 2x1 blocks per wave
 typedef Tile<64, 64, 32, 2, 2> ConvTSmall;  // small problems: 1 block per wave
 
-// Timing-table key of one kernel instance: conv_igemm_<BM>x<BN>_k<kh>x<kw>_<v4|s1>
-template <class T, int KH, int KW>
-static void launch_conv_t(const ConvArgs& a, bool avec, const char*) {
-    const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(256);
+template <class T, int KH, int KW, bool AVEC>
+static void launch_conv_t(ConvArgs& a, const char* entry) {
+    auto kernel = conv_streamk_k<T, KH, KW, AVEC>;
+    const size_t lds = (size_t)T::LDS_FLOATS * sizeof(float);
+    static bool configured = false;
+    static int slots = 0;
+    if (!configured) {
+        if (!hip_ok(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)lds),
+                    entry, "hipFuncSetAttribute"))
+            return;
+        slots = resident_groups(kernel, lds);
+        configured = true;
+    }
+    // K == 0 (no input channels) still runs one empty slice so the epilogue
+    // writes act(bias)
+    const int iters = a.K > 0 ? (int)ceil_div(a.K, T::BK) : 1;
+    const StreamK sk = plan_streamk(a.tiles_m * a.tiles_n, iters, slots);
+    if (sk.G < 1) return;
+    float* ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
+    if (!ws) return fail(NNC_HIP_ENOMEM, entry, "no workspace for stream-K partials");
+    a.ws = ws;
     char name[64];
     if (KH > 0)
-        snprintf(name, sizeof name, "conv_igemm_%dx%d_k%dx%d_%s", T::BM, T::BN, KH, KW, avec ? "v4" : "s1");
+        snprintf(name, sizeof name, "conv_igemm_%dx%d_k%dx%d_%s", T::BM, T::BN, KH, KW, AVEC ? "v4" : "s1");
     else
-        snprintf(name, sizeof name, "conv_igemm_%dx%d_kany_%s", T::BM, T::BN, avec ? "v4" : "s1");
+        snprintf(name, sizeof name, "conv_igemm_%dx%d_kany_%s", T::BM, T::BN, AVEC ? "v4" : "s1");
     set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
-    if (avec)
-        launch(name, conv_igemm_k<T, KH, KW, true>, grid, block, 0, a);
-    else
-        launch(name, conv_igemm_k<T, KH, KW, false>, grid, block, 0, a);
+    launch(name, kernel, dim3(sk.G), dim3(256), lds, a, sk);
+    if (sk.needs_fixup()) {
+        set_work(0.0, 0.0);
+        launch("conv_streamk_fixup", conv_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, a, sk);
+    }
 }
 
 template <class T>
-static void launch_conv_k(ConvArgs& a, bool avec, const char* name) {
+static void launch_conv(ConvArgs& a, bool avec, const char* entry) {
     a.tiles_m = (int)ceil_div(a.Co, T::BM);
     a.tiles_n = (int)ceil_div(a.Npix, T::BN);
-    // split K when the tiles alone leave CUs idle
-    const int tiles = a.tiles_m * a.tiles_n;
-    const int target = 2 * ctx().cu_count;
-    int splits = 1;
-    if (tiles < target) {
-        const int max_by_k = (int)(a.K / (4 * T::BK));
-        splits = (int)ceil_div(target, tiles);
-        if (splits > max_by_k) splits = max_by_k;
-        if (splits > 32) splits = 32;
-        if (splits < 1) splits = 1;
-    }
-    a.ws = nullptr;
-    if (splits > 1) {
-        size_t need = (size_t)splits * a.Co * a.Npix * sizeof(float);
-        float* ws = workspace(need);
-        while (!ws && splits > 1) {  // capture in progress: fit what exists
-            --splits;
-            need = (size_t)splits * a.Co * a.Npix * sizeof(float);
-            ws = need <= workspace_capacity() ? workspace(need) : nullptr;
-        }
-        a.ws = splits > 1 ? ws : nullptr;
-    }
-    a.splits = splits;
-    a.k_per_split = (int)(ceil_div(ceil_div(a.K, splits), T::BK) * T::BK);
-    a.splits = (int)ceil_div(a.K, a.k_per_split);
-    if (a.splits <= 1) a.ws = nullptr;
-    if (a.kh == 1 && a.kw == 1)
-        launch_conv_t<T, 1, 1>(a, avec, name);
-    else if (a.kh == 3 && a.kw == 3)
-        launch_conv_t<T, 3, 3>(a, avec, name);
-    else if (a.kh == 7 && a.kw == 7)
-        launch_conv_t<T, 7, 7>(a, avec, name);
-    else
-        launch_conv_t<T, 0, 0>(a, avec, name);
-    if (a.ws) {
-        const int64_t total = (int64_t)a.Co * a.Npix;
-        set_work(0.0, 4.0 * (double)total * (a.splits + 1));
-        launch("conv_splitk_reduce", conv_splitk_reduce_k, dim3(grid_for(total, 1)), dim3(256), 0,
-               (const float*)a.ws, a.bias, a.out, a.splits, a.Co, a.Npix, a.Ho * a.Wo, a.act);
-    }
+#define NNC_CONV_KS(KH, KW)                                                 \
+    if (avec) launch_conv_t<T, KH, KW, true>(a, entry);                     \
+    else launch_conv_t<T, KH, KW, false>(a, entry);                         \
+    return;
+    if (a.kh == 1 && a.kw == 1) { NNC_CONV_KS(1, 1) }
+    if (a.kh == 3 && a.kw == 3) { NNC_CONV_KS(3, 3) }
+    if (a.kh == 7 && a.kw == 7) { NNC_CONV_KS(7, 7) }
+    NNC_CONV_KS(0, 0)
+#undef NNC_CONV_KS
 }
 
 static bool conv_check(Tensor* in, Tensor* w, Tensor* out, const char* name) {
@@ -293,20 +293,22 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     if (a.bias && numel(b) < a.Co) return fail(NNC_HIP_EINVAL, name, "bias smaller than Co");
     const int64_t K = (int64_t)a.Ci * kh * kw;
     const int64_t npix = (int64_t)a.N * a.Ho * a.Wo;
-    if (K >= (1 << 30) || npix >= (1 << 30) || numel(in) >= ((int64_t)1 << 31))
-        return fail(NNC_HIP_EUNSUPP, name, "tensor too large for 32-bit indexing");
+    // the kernels address input and weights with 32-bit byte offsets
+    const int64_t in_bytes = (int64_t)a.N * a.Ci * a.H * a.W * 4;
+    const int64_t w_bytes = (int64_t)a.Co * K * 4;
+    if (K >= (1 << 30) || npix >= (1 << 30) || in_bytes >= ((int64_t)1 << 31) || w_bytes >= ((int64_t)1 << 31))
+        return fail(NNC_HIP_EUNSUPP, name, "input or weights of 2 GiB or more");
     a.K = (int)K;
     a.Npix = (int)npix;
     if (a.N == 0 || a.Co == 0 || a.Ho <= 0 || a.Wo <= 0) return;
     const bool avec = (a.K % 4 == 0) && aligned16(a.w);
     const int64_t work = (int64_t)a.Co * a.Npix;
-    if (a.Co <= 64 && work < 64 * 64 * 512) {
-        launch_conv_k<ConvTSmall>(a, avec, name);
-    } else if (a.Co <= 64) {
-        launch_conv_k<ConvT64>(a, avec, name);
-    } else {
-        launch_conv_k<ConvT128>(a, avec, name);
-    }
+    if (a.Co <= 64 && work < 64 * 64 * 512)
+        launch_conv<ConvTSmall>(a, avec, name);
+    else if (a.Co <= 64)
+        launch_conv<ConvT64>(a, avec, name);
+    else
+        launch_conv<ConvT128>(a, avec, name);
 }
 
 }  // namespace nnc
@@ -318,7 +320,7 @@ extern "C" {
 #define NNC_CONV_ENTRY(fname, act)                                                                \
     void fname(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw,      \
                int ph, int pw) {                                                                  \
-        if (!conv_check(in, w, out, #fname)) return;                                       \
+        if (!conv_check(in, w, out, #fname)) return;                                              \
         conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, act, #fname);                              \
     }
 NNC_CONV_ENTRY(nnc_conv, kActNone)
@@ -327,7 +329,7 @@ NNC_CONV_ENTRY(nnc_conv_sigmoid, kActSigmoid)
 
 #define NNC_CONV1X1_ENTRY(fname, act)                                                              \
     void fname(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int sh, int sw, int ph, int pw) {     \
-        if (!conv_check(in, w, out, #fname)) return;                                         \
+        if (!conv_check(in, w, out, #fname)) return;                                               \
         conv_run(in, w, b, out, 1, 1, sh, sw, ph, pw, act, #fname);                                 \
     }
 NNC_CONV1X1_ENTRY(nnc_conv1x1, kActNone)
@@ -337,7 +339,7 @@ NNC_CONV1X1_ENTRY(nnc_conv_relu1x1, kActRelu)
 // otherwise leaves the output untouched.
 #define NNC_CONV3X3_ENTRY(fname, act)                                                  \
     void fname(Tensor* in, Tensor* w, Tensor* b, Tensor* out) {                        \
-        if (!conv_check(in, w, out, #fname)) return;                             \
+        if (!conv_check(in, w, out, #fname)) return;                                   \
         if (out->shape[2] != in->shape[2] || out->shape[3] != in->shape[3])            \
             return fail(NNC_HIP_EINVAL, #fname, "expected same-padding output shape"); \
         conv_run(in, w, b, out, 3, 3, 1, 1, 1, 1, act, #fname);                         \
@@ -348,7 +350,7 @@ NNC_CONV3X3_ENTRY(nnc_conv_relu3x3_s1, kActRelu)
 // ops.c:1310-1311, 1403: stride 2 with the pad fixed at 3.
 #define NNC_CONV7X7_ENTRY(fname, act)                                   \
     void fname(Tensor* in, Tensor* w, Tensor* b, Tensor* out) {         \
-        if (!conv_check(in, w, out, #fname)) return;              \
+        if (!conv_check(in, w, out, #fname)) return;                    \
         conv_run(in, w, b, out, 7, 7, 2, 2, 3, 3, act, #fname);          \
     }
 NNC_CONV7X7_ENTRY(nnc_conv7x7_s2, kActNone)

@@ -2,7 +2,9 @@
 //
 // Dense products run on the fp32 MFMA tile engine (mfma_tile.h) with one of
 // four operand layouts per side (k-contiguous or x-contiguous, 16-byte or
-// scalar loads), optional batching (grid.y) and split-K. Products with one
+// scalar loads), stream-K scheduled over batches x tiles x K slices (a
+// fixup kernel applies the epilogue to tiles shared between workgroups, in
+// fixed workgroup order). Products with one
 // output row or column are HBM-bound and use dedicated kernels:
 //   gemv_xc_k  out[j] = sum_k a[k] * B[k][j]   (B row-major; float4 columns,
 //              K split across workgroups, deterministic partial reduction)
@@ -31,7 +33,7 @@ struct GemmArgs {
     float alpha, beta;
     int c_mode;  // 0 none, 1 C[j], 2 C[i*N + j]
     int relu;
-    int tiles_m, tiles_n, splits, k_per_split;
+    int tiles_m, tiles_n, splits;  // splits: K-split count of the GEMV path
 };
 
 __device__ __forceinline__ float gemm_finish(const GemmArgs& g, int i, int j, float v) {
@@ -69,66 +71,78 @@ struct PickLoader<kXC, X, BK, LD> {
 };
 
 template <class T, int AK, int BKIND>
-__global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g) {
-    __shared__ float lds[T::LDS_FLOATS];
-    float* As = lds;
-    float* Bs = lds + T::BK * T::LDA;
-    const int total = g.tiles_m * g.tiles_n * g.splits;
-    const int lin = xcd_remap(blockIdx.x, total);
-    const int mt = lin % g.tiles_m;
-    const int rest = lin / g.tiles_m;
-    const int nt = rest % g.tiles_n;
-    const int s = rest / g.tiles_n;
-    const int batch = blockIdx.y;
-    const int i0 = mt * T::BM, j0 = nt * T::BN;
-    const int kb = s * g.k_per_split;
-    const int ke = min(g.K, kb + g.k_per_split);
-
+__global__ void __launch_bounds__(256, 2) gemm_streamk_k(GemmArgs g, StreamK sk) {
+    extern __shared__ float lds[];
+    const int wg = xcd_remap(blockIdx.x, sk.G);
+    const int per_batch = g.tiles_m * g.tiles_n;
     typedef PickLoader<AK, T::BM, T::BK, T::LDA> PA;
     typedef PickLoader<BKIND, T::BN, T::BK, T::LDB> PB;
-    typename PA::type la;
-    typename PB::type lb;
-    la.init(g.A + batch * g.sa + PA::offset(i0, g.lda), g.lda, g.M - i0, g.K);
-    lb.init(g.B + batch * g.sb + PB::offset(j0, g.ldb), g.ldb, g.N - j0, g.K);
-
-    floatx16 sum[T::TM][T::TN];
-    mfma_mainloop<T>(la, lb, kb, ke, As, Bs, sum);
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wi = (wave / T::WN) * T::WAVE_M;
-    const int wj = (wave % T::WN) * T::WAVE_N;
+    SegmentWalker walk(sk, wg);
+    Segment seg;
+    while (walk.next(sk, seg)) {
+        const int batch = seg.tile / per_batch, rem = seg.tile - batch * per_batch;
+        const int mt = rem % g.tiles_m, nt = rem / g.tiles_m;
+        const int i0 = mt * T::BM, j0 = nt * T::BN;
+        typename PA::type la;
+        typename PB::type lb;
+        la.init(g.A + batch * g.sa + PA::offset(i0, g.lda), g.lda, g.M - i0, g.K);
+        lb.init(g.B + batch * g.sb + PB::offset(j0, g.ldb), g.ldb, g.N - j0, g.K);
+        floatx16 sum[T::TM][T::TN];
+        mfma_mainloop<T, true>(la, lb, seg.kb * T::BK, min(g.K, seg.ke * T::BK), lds, sum);
+        if (seg.slot < 0) {
 #pragma unroll
-    for (int tn = 0; tn < T::TN; ++tn) {
-        const int j = j0 + wj + tn * 32 + (lane & 31);
-        if (j >= g.N) continue;
+            for (int tn = 0; tn < T::TN; ++tn) {
+                const int j = j0 + acc_col<T>(tn);
+                if (j >= g.N) continue;
 #pragma unroll
-        for (int tm = 0; tm < T::TM; ++tm)
+                for (int tm = 0; tm < T::TM; ++tm)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = i0 + wi + tm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (i >= g.M) continue;
-                const float v = sum[tm][tn][r];
-                if (g.ws)
-                    g.ws[(((int64_t)batch * g.splits + s) * g.M + i) * g.N + j] = v;
-                else
-                    g.out[batch * g.so + (int64_t)i * g.N + j] = gemm_finish(g, i, j, v);
+                    for (int r = 0; r < 16; ++r) {
+                        const int i = i0 + acc_row<T>(tm, r);
+                        if (i < g.M) g.out[batch * g.so + (int64_t)i * g.N + j] = gemm_finish(g, i, j, sum[tm][tn][r]);
+                    }
             }
+        } else {
+            float* slot = partial_slot<T>(g.ws, wg, seg.slot);
+#pragma unroll
+            for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+                for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) slot[acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)] = sum[tm][tn][r];
+        }
     }
 }
 
-__global__ void __launch_bounds__(256) gemm_splitk_reduce_k(GemmArgs g, int batches) {
-    const int64_t mn = (int64_t)g.M * g.N;
-    const int64_t total = mn * batches;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        const int64_t b = e / mn;
-        const int64_t ij = e - b * mn;
-        float v = 0.f;
-        for (int s = 0; s < g.splits; ++s) v += g.ws[(b * g.splits + s) * mn + ij];
-        const int i = (int)(ij / g.N), j = (int)(ij - (int64_t)i * g.N);
-        g.out[b * g.so + ij] = gemm_finish(g, i, j, v);
+// Grid (chunks, stream-K tiles): workgroup (c, t) finishes chunk c of tile t
+// (256 float4 of the BM x BN tile): shared tiles sum their partials in
+// workgroup order and apply alpha / beta * C / relu. Each thread handles 4
+// consecutive columns of a tile row.
+template <class T>
+__global__ void __launch_bounds__(256) gemm_fixup_k(GemmArgs g, StreamK sk) {
+    const int t = blockIdx.y;
+    int g0, g1, first_slot;
+    if (!tile_partials(sk, t, g0, g1, first_slot)) return;
+    const int e4 = blockIdx.x * 256 + threadIdx.x;
+    if (e4 >= T::BM * T::BN / 4) return;
+    const int per_batch = g.tiles_m * g.tiles_n;
+    const int batch = t / per_batch, rem = t - batch * per_batch;
+    const int i = (rem % g.tiles_m) * T::BM + (e4 * 4) / T::BN;
+    const int j = (rem / g.tiles_m) * T::BN + (e4 * 4) % T::BN;
+    if (i >= g.M || j >= g.N) return;
+    float4 v = reinterpret_cast<const float4*>(partial_slot<T>(g.ws, g0, first_slot))[e4];
+    for (int w = g0 + 1; w <= g1; ++w) {
+        const float4 p = reinterpret_cast<const float4*>(partial_slot<T>(g.ws, w, 0))[e4];
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
     }
+    float* o = g.out + batch * g.so + (int64_t)i * g.N;
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (j + q < g.N) o[j + q] = gemm_finish(g, i, j + q, vals[q]);
 }
 
 // out[j] partials: thread owns 4 consecutive columns (VEC) or 1.
@@ -215,46 +229,37 @@ __global__ void __launch_bounds__(256) dot_k(GemmArgs g) {
 typedef Tile<128, 128, 32, 2, 2> GemmT128;
 typedef Tile<64, 64, 32, 2, 2> GemmT64;
 
+// Stream-K launch over batches x tiles x (K / BK) slice iterations.
 template <class T, int AK, int BKIND>
 static void launch_mfma(GemmArgs& g, int batches, const char* name) {
+    auto kernel = gemm_streamk_k<T, AK, BKIND>;
+    const size_t lds = (size_t)T::LDS_FLOATS * sizeof(float);
+    static bool configured = false;
+    static int slots = 0;
+    if (!configured) {
+        if (!hip_ok(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)lds),
+                    name, "hipFuncSetAttribute"))
+            return;
+        slots = resident_groups(kernel, lds);
+        configured = true;
+    }
     g.tiles_m = (int)ceil_div(g.M, T::BM);
     g.tiles_n = (int)ceil_div(g.N, T::BN);
-    const int tiles = g.tiles_m * g.tiles_n * batches;
-    const int target = 2 * ctx().cu_count;
-    int splits = 1;
-    if (tiles < target) {
-        const int max_by_k = (int)(g.K / (4 * T::BK));
-        splits = (int)ceil_div(target, tiles);
-        if (splits > max_by_k) splits = max_by_k;
-        if (splits > 32) splits = 32;
-        if (splits < 1) splits = 1;
-    }
-    g.ws = nullptr;
-    if (splits > 1) {
-        size_t need = (size_t)splits * batches * g.M * g.N * sizeof(float);
-        float* ws = workspace(need);
-        while (!ws && splits > 1) {
-            --splits;
-            need = (size_t)splits * batches * g.M * g.N * sizeof(float);
-            ws = need <= workspace_capacity() ? workspace(need) : nullptr;
-        }
-        g.ws = splits > 1 ? ws : nullptr;
-    }
-    g.k_per_split = (int)(ceil_div(ceil_div(g.K, splits), T::BK) * T::BK);
-    g.splits = (int)ceil_div(g.K, g.k_per_split);
-    if (g.splits < 1) g.splits = 1;
-    if (g.splits == 1) g.ws = nullptr;
+    if ((int64_t)g.tiles_m * g.tiles_n * batches >= (1 << 30))
+        return fail(NNC_HIP_EUNSUPP, name, "too many output tiles");
+    const StreamK sk = plan_streamk(g.tiles_m * g.tiles_n * batches, (int)ceil_div(g.K, T::BK), slots);
+    if (sk.G < 1) return;
+    g.ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
+    if (!g.ws) return fail(NNC_HIP_ENOMEM, name, "no workspace for stream-K partials");
     static const char* kinds[4] = {"k4", "k1", "x4", "x1"};
     char kname[64];
     snprintf(kname, sizeof kname, "gemm_mfma_%dx%d_%s%s", T::BM, T::BN, kinds[AK], kinds[BKIND]);
     set_work(2.0 * g.M * (double)g.N * g.K * batches, 0.0);
-    launch(kname, gemm_mfma_k<T, AK, BKIND>, dim3(g.tiles_m * g.tiles_n * g.splits, batches),
-           dim3(256), 0, g);
-    (void)name;
-    if (g.ws) {
-        set_work(0.0, 4.0 * (double)g.M * g.N * batches * (g.splits + 1));
-        launch("gemm_splitk_reduce", gemm_splitk_reduce_k, dim3(grid_for((int64_t)g.M * g.N * batches, 1)),
-               dim3(256), 0, g, batches);
+    launch(kname, kernel, dim3(sk.G), dim3(256), lds, g, sk);
+    if (sk.needs_fixup()) {
+        set_work(0.0, 0.0);
+        launch("gemm_streamk_fixup", gemm_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, g, sk);
     }
 }
 
@@ -351,11 +356,20 @@ static void gemm_run(const GemmProblem& p, const char* name) {
         else launch("dot_rows_s1", dot_k<false>, grid, dim3(256), 0, g);
         return;
     }
-    // MFMA tiles. 16-byte loads need 4-float alignment of every row/batch start.
+    // MFMA tiles address each operand tile with 32-bit byte offsets from the
+    // tile origin: at most 128 rows of lda (k-contiguous) or K rows of lda
+    // (x-contiguous).
+    const int64_t a_span = p.a_kc ? 128 * p.lda + p.K : (int64_t)p.K * p.lda + 128;
+    const int64_t b_span = p.b_kc ? 128 * p.ldb + p.K : (int64_t)p.K * p.ldb + 128;
+    if (a_span * 4 >= ((int64_t)1 << 31) || b_span * 4 >= ((int64_t)1 << 31))
+        return fail(NNC_HIP_EUNSUPP, name, "operand tile spans 2 GiB or more");
+    // 16-byte loads need 4-float alignment of every row/batch start.
     const bool a_al = aligned16(p.A) && p.lda % 4 == 0 && p.sa % 4 == 0;
     const bool b_al = aligned16(p.B) && p.ldb % 4 == 0 && p.sb % 4 == 0;
-    const int akind = p.a_kc ? ((a_al && p.K % 4 == 0) ? kKC4 : kKC) : (a_al ? kXC4 : kXC);
-    const int bkind = p.b_kc ? ((b_al && p.K % 4 == 0) ? kKC4 : kKC) : (b_al ? kXC4 : kXC);
+    // (the x-contiguous 16-byte loader also needs the row length M or N to be
+    // a multiple of 4)
+    const int akind = p.a_kc ? ((a_al && p.K % 4 == 0) ? kKC4 : kKC) : ((a_al && p.M % 4 == 0) ? kXC4 : kXC);
+    const int bkind = p.b_kc ? ((b_al && p.K % 4 == 0) ? kKC4 : kKC) : ((b_al && p.N % 4 == 0) ? kXC4 : kXC);
     const bool big = (int64_t)p.M * p.N * p.batches >= (int64_t)128 * 128 * 2 * ctx().cu_count / 4 &&
                      p.M >= 128 && p.N >= 128;
     if (big && (akind == kKC4 || akind == kXC4) && (bkind == kKC4 || bkind == kXC4)) {

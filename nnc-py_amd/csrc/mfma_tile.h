@@ -1,23 +1,35 @@
 // fp32 MFMA tile engine for gfx950 shared by implicit-GEMM convolution and
 // GEMM/MatMul.
 //
-// One workgroup = 256 threads = 4 wave64s computes a BM x BN tile of
+// One workgroup = 256 threads = 4 wave64s computes BM x BN tiles of
 // D[i][j] = sum_k A[i][k] * B[k][j]. The waves form a WM x WN grid; each wave
 // owns a (BM/WM) x (BN/WN) sub-tile made of 32x32 blocks, each block one
 // v_mfma_f32_32x32x2_f32 accumulator (16 VGPRs per lane).
 //
 // Operand staging: every BK-deep slice of A and B is read from HBM/L2 into
-// registers by a loader, stored into LDS as S[k][x] (x = i for A, j for B,
-// rows padded so that both the transposed stores and the MFMA operand reads
-// stay bank-conflict-free), and consumed by the MFMAs. The next slice's
-// global loads are issued before the current slice's MFMAs so their latency
-// overlaps the matrix work.
+// registers by a loader and stored into LDS as S[k][x] (x = i for A, j for
+// B; rows padded by one float so transposed stores and MFMA operand reads
+// stay bank-conflict-free). LDS is double-buffered: while the MFMAs consume
+// slice t from one buffer, slice t+1's global loads are in flight and are
+// then stored to the other buffer, so each slice costs one barrier. Loads are
+// raw buffer loads (buffer resource in SGPRs, 32-bit byte offsets): an
+// out-of-range element gets an offset past the resource's size and the
+// hardware returns 0, so loads need no branch and no select afterwards, the
+// loaded registers go straight to LDS and the wait for the loads falls after
+// the slice's MFMAs. Byte offsets must stay below 2^31 (checked on the host).
 //
-// Accumulation is two-level: the MFMAs of one BK slice accumulate into a
-// fresh accumulator which is then added to a running fp32 sum. This keeps the
-// longest fp32 rounding chain at BK/2 MFMA steps plus K/BK slice additions
-// instead of K/2, which holds the error of K = 4608 contractions well inside
-// 1e-4 absolute / 1e-3 relative of the fp64-accumulated reference.
+// Scheduling is hybrid stream-K: a persistent grid of G workgroups (at
+// most the number resident on the GPU at once). Tiles [0, sk_tiles) form
+// the stream-K region: their tiles x (K/BK) slice iterations are split into
+// G equal contiguous ranges, one per workgroup. Tiles [sk_tiles, tiles) are
+// whole tiles dealt round-robin (tile sk_tiles + g + m*G to workgroup g).
+// A workgroup writes tiles it covers completely straight to the output; for
+// a tile shared by several workgroups each writes its partial tile to the
+// workspace and a fixup kernel adds the partials in workgroup order
+// (deterministic) and applies the epilogue. The region sizes keep every CU
+// busy to the end whatever the tile count (a tiles-times-splits grid cannot:
+// 588 workgroups on 512 slots leave the second round 15% full) while
+// splitting no more tiles than needed.
 //
 // MFMA 32x32x2 f32 operand/result layout (lane l of 64):
 //   A operand: A[i = l % 32][k = l / 32]
@@ -31,6 +43,24 @@ namespace nnc {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// ---------------------------------------------------------------------------
+// raw buffer loads. gfx9 buffer resource: base, stride 0, num_records bytes,
+// dword3 0x00020000 (32-bit data format). An offset >= num_records reads 0.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+static constexpr uint32_t kOutOfRange = 0x80000000u;  // any offset >= kRecords
+static constexpr int kRecords = 0x7FFFFFFF;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, kRecords, 0x00020000);
+}
+__device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0));
+}
+__device__ __forceinline__ f32x4 load_f32x4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
+
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
@@ -40,13 +70,16 @@ struct Tile {
     static constexpr int TM = WAVE_M / 32, TN = WAVE_N / 32;
     static_assert(TM >= 1 && TN >= 1 && WAVE_M % 32 == 0 && WAVE_N % 32 == 0, "32x32 blocks");
     static_assert(BK % 2 == 0, "k step of 2");
-    // LDS row lengths (floats). +1 keeps transposed scalar stores conflict-free.
     static constexpr int LDA = BM + 1, LDB = BN + 1;
-    static constexpr int LDS_FLOATS = BK * (LDA + LDB);
+    static constexpr int STAGE = BK * (LDA + LDB);  // floats per LDS buffer
+    static constexpr int LDS_FLOATS = 2 * STAGE;
+    static_assert((BM * BN) % 1024 == 0, "fixup chunks of 256 float4");
 };
 
 // ---------------------------------------------------------------------------
-// operand loaders: fill S[k][x] for x in [0, X), k in [k0, k0 + BK)
+// operand loaders: fill S[k][x] for x in [0, X), k in [k0, k0 + BK); elements
+// outside [0, xlim) x [0, K) are zero. `base` is the tile origin; every
+// in-range element's byte offset from it is below 2^31.
 // ---------------------------------------------------------------------------
 
 // element (x, k) at base[x * ld + k]  (row-major A, or B stored [N][K])
@@ -55,14 +88,13 @@ struct KContigLoader {
     static constexpr int ROWS_PER_PASS = 256 / BK;
     static constexpr int PER = X * BK / 256;
     static_assert(256 % BK == 0 && X % ROWS_PER_PASS == 0, "loader shape");
-    const float* base;
-    int64_t ld;
-    int xlim, K, kk, xx;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int ld, xlim, K, kk, xx;
     float v[PER];
 
     __device__ void init(const float* b, int64_t ld_, int xlim_, int K_) {
-        base = b;
-        ld = ld_;
+        rsrc = make_rsrc(b);
+        ld = (int)ld_;
         xlim = xlim_;
         K = K_;
         kk = threadIdx.x % BK;
@@ -73,9 +105,8 @@ struct KContigLoader {
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
             const int x = xx + p * ROWS_PER_PASS;
-            float t = 0.f;
-            if (x < xlim && k < K) t = base[(int64_t)x * ld + k];
-            v[p] = t;
+            const bool ok = x < xlim && k < K;
+            v[p] = load_f32(rsrc, ok ? (uint32_t)(x * ld + k) * 4u : kOutOfRange);
         }
     }
     __device__ void store(float* S) const {
@@ -84,22 +115,20 @@ struct KContigLoader {
     }
 };
 
-// As KContigLoader with 16-byte loads; requires ld % 4 == 0, K % 4 == 0 and a
-// 16-byte aligned base.
+// 16-byte loads; requires ld % 4 == 0, K % 4 == 0, 16-byte aligned base
 template <int X, int BK, int LD>
 struct KContigLoader4 {
     static constexpr int KQ = BK / 4;
     static constexpr int ROWS_PER_PASS = 256 / KQ;
     static constexpr int PER = X * BK / (256 * 4);
     static_assert(BK % 4 == 0 && 256 % KQ == 0 && X % ROWS_PER_PASS == 0 && PER >= 1, "loader4");
-    const float* base;
-    int64_t ld;
-    int xlim, K, kk, xx;
-    float4 v[PER];
+    __amdgpu_buffer_rsrc_t rsrc;
+    int ld, xlim, K, kk, xx;
+    f32x4 v[PER];
 
     __device__ void init(const float* b, int64_t ld_, int xlim_, int K_) {
-        base = b;
-        ld = ld_;
+        rsrc = make_rsrc(b);
+        ld = (int)ld_;
         xlim = xlim_;
         K = K_;
         kk = (threadIdx.x % KQ) * 4;
@@ -110,9 +139,8 @@ struct KContigLoader4 {
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
             const int x = xx + p * ROWS_PER_PASS;
-            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (x < xlim && k < K) t = *reinterpret_cast<const float4*>(base + (int64_t)x * ld + k);
-            v[p] = t;
+            const bool ok = x < xlim && k < K;
+            v[p] = load_f32x4(rsrc, ok ? (uint32_t)(x * ld + k) * 4u : kOutOfRange);
         }
     }
     __device__ void store(float* S) const {
@@ -133,14 +161,13 @@ struct XContigLoader {
     static constexpr int KROWS_PER_PASS = 256 / X;
     static constexpr int PER = X * BK / 256;
     static_assert(256 % X == 0 && BK % KROWS_PER_PASS == 0, "loader shape");
-    const float* base;
-    int64_t ld;
-    int xlim, K, xx, kk;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int ld, xlim, K, xx, kk;
     float v[PER];
 
     __device__ void init(const float* b, int64_t ld_, int xlim_, int K_) {
-        base = b;
-        ld = ld_;
+        rsrc = make_rsrc(b);
+        ld = (int)ld_;
         xlim = xlim_;
         K = K_;
         xx = threadIdx.x % X;
@@ -150,9 +177,8 @@ struct XContigLoader {
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
             const int k = k0 + kk + p * KROWS_PER_PASS;
-            float t = 0.f;
-            if (xx < xlim && k < K) t = base[(int64_t)k * ld + xx];
-            v[p] = t;
+            const bool ok = xx < xlim && k < K;
+            v[p] = load_f32(rsrc, ok ? (uint32_t)(k * ld + xx) * 4u : kOutOfRange);
         }
     }
     __device__ void store(float* S) const {
@@ -161,22 +187,21 @@ struct XContigLoader {
     }
 };
 
-// 16-byte variant: requires ld % 4 == 0 and a 16-byte aligned base; x bounds
-// are checked per element so any xlim works.
+// 16-byte variant: requires ld % 4 == 0, xlim % 4 == 0 (so a group of four
+// is wholly inside or outside) and a 16-byte aligned base.
 template <int X, int BK, int LD>
 struct XContigLoader4 {
     static constexpr int XQ = X / 4;
     static constexpr int KROWS_PER_PASS = 256 / XQ;
     static constexpr int PER = X * BK / (256 * 4);
     static_assert(X % 4 == 0 && 256 % XQ == 0 && BK % KROWS_PER_PASS == 0 && PER >= 1, "loader4");
-    const float* base;
-    int64_t ld;
-    int xlim, K, xx, kk;
-    float4 v[PER];
+    __amdgpu_buffer_rsrc_t rsrc;
+    int ld, xlim, K, xx, kk;
+    f32x4 v[PER];
 
     __device__ void init(const float* b, int64_t ld_, int xlim_, int K_) {
-        base = b;
-        ld = ld_;
+        rsrc = make_rsrc(b);
+        ld = (int)ld_;
         xlim = xlim_;
         K = K_;
         xx = (threadIdx.x % XQ) * 4;
@@ -186,18 +211,8 @@ struct XContigLoader4 {
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
             const int k = k0 + kk + p * KROWS_PER_PASS;
-            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k < K) {
-                const float* src = base + (int64_t)k * ld + xx;
-                if (xx + 3 < xlim) {
-                    t = *reinterpret_cast<const float4*>(src);
-                } else {
-                    if (xx + 0 < xlim) t.x = src[0];
-                    if (xx + 1 < xlim) t.y = src[1];
-                    if (xx + 2 < xlim) t.z = src[2];
-                }
-            }
-            v[p] = t;
+            const bool ok = xx < xlim && k < K;
+            v[p] = load_f32x4(rsrc, ok ? (uint32_t)(k * ld + xx) * 4u : kOutOfRange);
         }
     }
     __device__ void store(float* S) const {
@@ -213,18 +228,20 @@ struct XContigLoader4 {
 };
 
 // ---------------------------------------------------------------------------
-// main loop over k in [k_begin, k_end): loaders must zero-fill k >= K.
+// main loop over k in [k_begin, k_end) (k_begin a multiple of BK); LDS holds
+// two stages of T::STAGE floats. TWO_LEVEL adds each slice's products into
+// the running sum through a fresh accumulator (shorter fp32 rounding chains
+// for very long K); otherwise the MFMAs accumulate into `sum` directly.
 // ---------------------------------------------------------------------------
-template <class T, class LA, class LB>
-__device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k_end, float* As,
-                                              float* Bs, floatx16 (&sum)[T::TM][T::TN]) {
+template <class T, bool TWO_LEVEL, class LA, class LB>
+__device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k_end, float* lds,
+                                              floatx16 (&sum)[T::TM][T::TN]) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wi = (wave / T::WN) * T::WAVE_M;
     const int wj = (wave % T::WN) * T::WAVE_N;
-    const int lrow = lane >> 5, lcol = lane & 31;
-    const float* Ap = As + lrow * T::LDA + wi + lcol;
-    const float* Bp = Bs + lrow * T::LDB + wj + lcol;
+    const int a_off = (lane >> 5) * T::LDA + wi + (lane & 31);
+    const int b_off = T::BK * T::LDA + (lane >> 5) * T::LDB + wj + (lane & 31);
 
 #pragma unroll
     for (int tm = 0; tm < T::TM; ++tm)
@@ -232,27 +249,32 @@ __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k
         for (int tn = 0; tn < T::TN; ++tn)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sum[tm][tn][r] = 0.f;
-
     if (k_begin >= k_end) return;
+
     la.load(k_begin);
     lb.load(k_begin);
-    la.store(As);
-    lb.store(Bs);
+    la.store(lds);
+    lb.store(lds + T::BK * T::LDA);
     __syncthreads();
 
+    int stage = 0;
     for (int k0 = k_begin; k0 < k_end; k0 += T::BK) {
         const bool more = k0 + T::BK < k_end;
         if (more) {
             la.load(k0 + T::BK);
             lb.load(k0 + T::BK);
         }
+        const float* Ap = lds + stage * T::STAGE + a_off;
+        const float* Bp = lds + stage * T::STAGE + b_off;
         floatx16 acc[T::TM][T::TN];
+        if (TWO_LEVEL) {
 #pragma unroll
-        for (int tm = 0; tm < T::TM; ++tm)
+            for (int tm = 0; tm < T::TM; ++tm)
 #pragma unroll
-            for (int tn = 0; tn < T::TN; ++tn)
+                for (int tn = 0; tn < T::TN; ++tn)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[tm][tn][r] = 0.f;
+                    for (int r = 0; r < 16; ++r) acc[tm][tn][r] = 0.f;
+        }
 #pragma unroll
         for (int kk = 0; kk < T::BK; kk += 2) {
             float a[T::TM], b[T::TN];
@@ -263,48 +285,182 @@ __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k
 #pragma unroll
             for (int tm = 0; tm < T::TM; ++tm)
 #pragma unroll
-                for (int tn = 0; tn < T::TN; ++tn)
-                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm], b[tn], acc[tm][tn], 0, 0, 0);
+                for (int tn = 0; tn < T::TN; ++tn) {
+                    if (TWO_LEVEL)
+                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm], b[tn], acc[tm][tn], 0, 0, 0);
+                    else
+                        sum[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm], b[tn], sum[tm][tn], 0, 0, 0);
+                }
         }
+        if (TWO_LEVEL) {
 #pragma unroll
-        for (int tm = 0; tm < T::TM; ++tm)
+            for (int tm = 0; tm < T::TM; ++tm)
 #pragma unroll
-            for (int tn = 0; tn < T::TN; ++tn) sum[tm][tn] += acc[tm][tn];
-        __syncthreads();
+                for (int tn = 0; tn < T::TN; ++tn) sum[tm][tn] += acc[tm][tn];
+        }
         if (more) {
-            la.store(As);
-            lb.store(Bs);
+            float* next = lds + (stage ^ 1) * T::STAGE;
+            la.store(next);
+            lb.store(next + T::BK * T::LDA);
         }
         __syncthreads();
+        stage ^= 1;
     }
 }
 
-// Visit every (i, j, value) of the wave's accumulators in tile coordinates.
-template <class T, class F>
-__device__ __forceinline__ void for_each_acc(const floatx16 (&sum)[T::TM][T::TN], F&& f) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wi = (wave / T::WN) * T::WAVE_M;
-    const int wj = (wave % T::WN) * T::WAVE_N;
-#pragma unroll
-    for (int tm = 0; tm < T::TM; ++tm)
-#pragma unroll
-        for (int tn = 0; tn < T::TN; ++tn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = wi + tm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const int j = wj + tn * 32 + (lane & 31);
-                f(i, j, sum[tm][tn][r]);
-            }
+// Tile-local coordinates of accumulator element (tm, tn, r) for this lane.
+template <class T>
+__device__ __forceinline__ int acc_row(int tm, int r) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    return (wave / T::WN) * T::WAVE_M + tm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
+template <class T>
+__device__ __forceinline__ int acc_col(int tn) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    return (wave % T::WN) * T::WAVE_N + tn * 32 + (lane & 31);
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
-// L2). Remap the launch index so that consecutive logical tiles - which share
-// an operand slice - run on the same XCD. Bijective on [0, total).
+// L2). Remap the launch index so that consecutive logical workgroups - whose
+// stream-K ranges hold neighbouring tiles sharing operand slices - run on the
+// same XCD. Bijective on [0, total).
 __device__ __forceinline__ int xcd_remap(int lin, int total) {
     const int per = total / 8;
     if (lin >= per * 8) return lin;
     return (lin % 8) * per + lin / 8;
+}
+
+// ---------------------------------------------------------------------------
+// stream-K bookkeeping. The stream-K region holds S = sk_tiles * iters slice
+// iterations; workgroup g owns [lo(g), hi(g)) with lo(g) = g*S/G.
+// ---------------------------------------------------------------------------
+struct StreamK {
+    int tiles, iters, G, sk_tiles;
+    __host__ __device__ int64_t total() const { return (int64_t)sk_tiles * iters; }
+    __host__ __device__ int64_t lo(int g) const { return total() * g / G; }
+    __host__ __device__ int64_t hi(int g) const { return total() * (g + 1) / G; }
+    // first workgroup whose range reaches into stream-K tile t
+    __host__ __device__ int first_owner(int t) const {
+        const int64_t start = (int64_t)t * iters;
+        int g = (int)(start * G / total());
+        while (g > 0 && hi(g - 1) > start) --g;
+        while (hi(g) <= start) ++g;
+        return g;
+    }
+    // true if some stream-K tile is shared (a range boundary inside a tile)
+    __host__ bool needs_fixup() const {
+        if (sk_tiles == 0 || iters == 1) return false;
+        return !(total() % G == 0 && (total() / G) % iters == 0);
+    }
+};
+
+// One unit of a workgroup's work: slices [kb, ke) of `tile`. `slot` is the
+// partial slot (0: first segment of the range, 1: last) or -1 for a whole
+// tile written straight to the output.
+struct Segment {
+    int tile, kb, ke, slot;
+};
+
+// Walks workgroup g's work: its stream-K range, then its whole tiles.
+struct SegmentWalker {
+    int64_t it, lo, hi;
+    int dp;
+    __host__ __device__ SegmentWalker(const StreamK& sk, int g) {
+        lo = sk.sk_tiles ? sk.lo(g) : 0;
+        hi = sk.sk_tiles ? sk.hi(g) : 0;
+        it = lo;
+        dp = sk.sk_tiles + g;
+    }
+    __host__ __device__ bool next(const StreamK& sk, Segment& s) {
+        if (it < hi) {
+            s.tile = (int)(it / sk.iters);
+            s.kb = (int)(it - (int64_t)s.tile * sk.iters);
+            const int64_t left = hi - it;
+            s.ke = left < sk.iters - s.kb ? s.kb + (int)left : sk.iters;
+            s.slot = (s.kb == 0 && s.ke == sk.iters) ? -1 : (it == lo ? 0 : 1);
+            it += s.ke - s.kb;
+            return true;
+        }
+        if (dp < sk.tiles) {
+            s.tile = dp;
+            s.kb = 0;
+            s.ke = sk.iters;
+            s.slot = -1;
+            dp += sk.G;
+            return true;
+        }
+        return false;
+    }
+};
+
+// Partials of shared stream-K tile t: workgroups g0..g1 in order; g0's
+// segment sits in slot `first_slot`, the others in slot 0 (their ranges
+// start inside the tile). Returns false if one workgroup covers the tile.
+__host__ __device__ inline bool tile_partials(const StreamK& sk, int t, int& g0, int& g1, int& first_slot) {
+    const int64_t start = (int64_t)t * sk.iters, end = start + sk.iters;
+    g0 = sk.first_owner(t);
+    const int64_t lo0 = sk.lo(g0);
+    if (lo0 <= start && sk.hi(g0) >= end) return false;
+    first_slot = lo0 < start ? 1 : 0;
+    g1 = g0;
+    while (g1 + 1 < sk.G && sk.lo(g1 + 1) < end) ++g1;
+    return true;
+}
+
+// Host: choose the grid and the stream-K region for `tiles` tiles of
+// `iters` slices on `slots` resident workgroups.
+//  - few slices per tile (< 4): splitting costs more than the tail; plain
+//    round-robin over min(tiles, slots) workgroups
+//  - tiles >= slots with the last round empty or >= 80% full: round-robin
+//  - tiles >= slots otherwise: all but the last full round plus the partial
+//    round go to stream-K, so every workgroup ends at the same time
+//  - tiles < slots: everything is stream-K, each workgroup taking at least
+//    4 slices (fewer workgroups for short problems)
+inline StreamK plan_streamk(int tiles, int iters, int slots) {
+    StreamK sk{};
+    sk.tiles = tiles;
+    sk.iters = iters;
+    const int kMinSplitIters = 4, kMinRangeIters = 4;
+    if (iters < kMinSplitIters) {
+        sk.G = tiles < slots ? tiles : slots;
+        sk.sk_tiles = 0;
+        return sk;
+    }
+    if (tiles >= slots) {
+        const int rem = tiles % slots;
+        sk.G = slots;
+        if (rem == 0 || (int64_t)rem * 5 >= (int64_t)slots * 4) {
+            sk.sk_tiles = 0;
+        } else {
+            sk.sk_tiles = tiles - (tiles / slots - 1) * slots;
+        }
+        return sk;
+    }
+    const int64_t total = (int64_t)tiles * iters;
+    int64_t G = total / kMinRangeIters;
+    if (G > slots) G = slots;
+    if (G < tiles) G = tiles;
+    sk.G = (int)G;
+    sk.sk_tiles = tiles;
+    return sk;
+}
+
+// Persistent-grid size: workgroups of `kernel` resident on the device at once.
+template <typename K>
+static int resident_groups(K kernel, size_t lds_bytes) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds_bytes) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    return per_cu * ctx().cu_count;
+}
+
+// Partial-tile slots in the workspace: two per workgroup (the segment where
+// its range starts, and the one where it ends), each BM*BN floats, row-major
+// in tile coordinates.
+template <class T>
+__device__ __forceinline__ float* partial_slot(float* ws, int g, int which) {
+    return ws + ((int64_t)g * 2 + which) * (T::BM * T::BN);
 }
 
 }  // namespace nnc

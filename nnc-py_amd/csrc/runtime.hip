@@ -46,9 +46,9 @@ bool ready(const char* who) {
     return false;
 }
 
-// Default workspace: enough for split-K over the ResNet-18 / GEMM-sweep
-// shapes without growing; grows (outside capture) when a call needs more.
-static const size_t kDefaultWorkspace = 64u << 20;
+// Default workspace: stream-K partials of a full persistent grid (2 slots of
+// 128x128 floats for 512 workgroups = 64 MiB) with room; grows outside capture.
+static const size_t kDefaultWorkspace = 128u << 20;
 
 float* workspace(size_t bytes) {
     if (bytes <= g_ctx.workspace_bytes) return g_ctx.workspace;
