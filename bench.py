@@ -13,17 +13,27 @@ Printed as one JSON line (rank 0): images/s at batch 32 (value), batch 1 as
 an extra figure, the roofline of the dominant kernel measured live from the
 library's per-launch hipEvent table, a per-kernel table, and the reference
 CPU runtime timed on this host as a baseline.
+
+HBM traffic of the dominant kernel (roofline.traffic) comes from two
+`rocprofv3 --pmc` child runs of this script in --pmc-child mode (FETCH_SIZE,
+then WRITE_SIZE), each scaled by what the same counter reads for a plain
+device copy of known size run in the same child; --no-traffic skips them.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
 import importlib.util
 import json
 import os
 import platform
+import re
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -84,6 +94,11 @@ def kernel_table(ex, runtime, steps: int) -> list[dict]:
         if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma")):
             bound, unit, peak = "mfma", "TFLOP/s", PEAK_FP32_MFMA_TF
             achieved = r["flops"] / (r["ms"] * 1e-3) / 1e12
+        elif r["name"].endswith("_fixup"):
+            # stream-K partial-tile reduction: no algorithmic work of its own,
+            # its time counts against the MFMA kernels it completes
+            bound, unit, peak = "mfma-fixup", "TFLOP/s", PEAK_FP32_MFMA_TF
+            achieved = 0.0
         else:
             bound, unit, peak = "hbm", "GB/s", PEAK_HBM_GBS
             achieved = r["bytes"] / (r["ms"] * 1e-3) / 1e9 if r["ms"] > 0 else 0.0
@@ -133,6 +148,97 @@ def cpu_baseline(pkg, iters: int) -> dict | None:
                        f"host {cpu}, nproc {os.cpu_count()}")}
 
 
+COPY_PROBE_BYTES = 256 << 20
+
+
+def conv_symbol_pattern(name: str) -> re.Pattern | None:
+    """Kernel-table name -> regex over the HIP kernel symbol rocprofv3 reports,
+    e.g. conv_igemm_128x128_k3x3_v4 -> conv_streamk_k<nnc::Tile<128, 128, ...>, 3, 3, true>."""
+    m = re.fullmatch(r"conv_igemm_(\d+)x(\d+)_k(\d+|any)(?:x(\d+))?_(v4|s1)", name)
+    if m:
+        bm, bn, kh, kw, vec = m.groups()
+        kh, kw = ("0", "0") if kh == "any" else (kh, kw)
+        return re.compile(rf"conv_streamk_k<nnc::Tile<{bm}, {bn},[^>]*>, {kh}, {kw}, "
+                          rf"{'true' if vec == 'v4' else 'false'}>")
+    m = re.fullmatch(r"gemm_mfma_(\d+)x(\d+)_\w+", name)
+    if m:
+        return re.compile(rf"gemm_streamk_k<nnc::Tile<{m.group(1)}, {m.group(2)},")
+    return None
+
+
+def pmc_child(args) -> int:
+    """Run under rocprofv3 --pmc: two eager nnc_run() of the benchmark program,
+    then a plain device copy of COPY_PROBE_BYTES (the calibration probe)."""
+    load_package()
+    from nnc_py_amd import runtime
+    from nnc_py_amd.compiler import Executor, build_program, zoo
+    lib = runtime.init(0)
+    prog = build_program(zoo.resnet18(batch=args.batch, seed=1), opt_level=3)
+    ex = Executor(prog, device=True)
+    ex.set_input("input", np.random.default_rng(0).standard_normal((args.batch, 3, 224, 224)).astype(np.float32))
+    for _ in range(2):
+        ex.run()
+    runtime.sync()
+    ex.close()
+    n = COPY_PROBE_BYTES // 4
+    src = runtime.DeviceBuffer.empty((n,))
+    dst = runtime.DeviceBuffer.empty((n,))
+    ts, ks = src.tensor(), dst.tensor()
+    for _ in range(3):
+        lib.nnc_identity(ctypes.byref(ts[0]), ctypes.byref(ks[0]))
+    runtime.sync()
+    runtime.check(lib.nnc_hip_last_error(), "copy probe")
+    return 0
+
+
+def _pmc_run(counter: str, batch: int, timeout: int = 120) -> list[dict] | None:
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None
+    with tempfile.TemporaryDirectory(prefix="nnc_pmc_") as tmp:
+        cmd = ["timeout", "-s", "KILL", str(timeout), prof, "--pmc", counter, "--output-format", "csv",
+               "-d", tmp, "-o", "pmc", "--", sys.executable, str(ROOT / "bench.py"), "--pmc-child",
+               "--batch", str(batch)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        files = list(Path(tmp).rglob("*counter_collection.csv"))
+        if res.returncode != 0 or not files:
+            log(f"rocprofv3 --pmc {counter} failed (rc {res.returncode})")
+            return None
+        with open(files[0]) as f:
+            return list(csv.DictReader(f))
+
+
+def measure_traffic(kernel: str, batch: int) -> dict | None:
+    """HBM bytes per launch of `kernel`: FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch, summed over channels), each scaled by COPY_PROBE_BYTES / the
+    reading of the same counter for the copy probe's dispatches."""
+    pat = conv_symbol_pattern(kernel)
+    if pat is None:
+        return None
+    out = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        rows = _pmc_run(counter, batch)
+        if not rows:
+            return None
+        per_dispatch: dict[tuple, float] = {}
+        names: dict[tuple, str] = {}
+        for r in rows:
+            if r.get("Counter_Name") != counter:
+                continue
+            key = (r.get("Dispatch_Id"), r.get("Correlation_Id"))
+            per_dispatch[key] = per_dispatch.get(key, 0.0) + float(r["Counter_Value"])
+            names[key] = r.get("Kernel_Name", "")
+        kern = [v for k, v in per_dispatch.items() if pat.search(names[k])]
+        copy = [v for k, v in per_dispatch.items() if "copy16_k" in names[k]]
+        if not kern or not copy:
+            return None
+        probe_kib = max(copy[-3:])  # the last dispatches are the 256 MiB probe copies
+        scale = (COPY_PROBE_BYTES / 1024.0) / probe_kib
+        out[counter] = {"kib_per_launch_raw": sum(kern) / len(kern), "probe_kib_raw": probe_kib,
+                        "scale": scale, "bytes_per_launch": sum(kern) / len(kern) * 1024.0 * scale}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,10 +247,14 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-graph", action="store_true", help="launch each nnc_* call instead of a hipGraph")
     ap.add_argument("--profile-steps", type=int, default=5)
-    ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--cpu-iters", type=int, default=25)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--no-b1", action="store_true", help="measure batch 32 only (profiling runs)")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.pmc_child:
+        return pmc_child(args)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build runs the nnc program on a single MI355X "
@@ -182,12 +292,22 @@ def main() -> int:
     table = tables[args.batch]
     dom = table[0]
     peak = PEAK_FP32_MFMA_TF if dom["bound"] == "mfma" else PEAK_HBM_GBS
+    traffic = None
+    traffic_detail = None
+    if not args.no_traffic:
+        log(f"HBM traffic of {dom['kernel']}: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE")
+        traffic_detail = measure_traffic(dom["kernel"], args.batch)
+        if traffic_detail:
+            traffic = round(traffic_detail["FETCH_SIZE"]["bytes_per_launch"]
+                            + traffic_detail["WRITE_SIZE"]["bytes_per_launch"])
     roofline = {"kernel": dom["kernel"], "bound": dom["bound"], "achieved": dom["achieved"],
                 "peak": peak, "unit": dom["unit"], "frac": round(dom["achieved"] / peak, 4),
-                "traffic": None, "avg_launch_us": dom["avg_us"],
+                "traffic": traffic, "avg_launch_us": dom["avg_us"],
                 "work_per_launch": dom["work_per_launch"]}
+    if traffic_detail:
+        roofline["traffic_detail"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in traffic_detail.items()}
     gpu_ms = sum(r["ms_per_step"] for r in table)
-    conv_ms = sum(r["ms_per_step"] for r in table if r["bound"] == "mfma")
+    conv_ms = sum(r["ms_per_step"] for r in table if r["bound"] in ("mfma", "mfma-fixup"))
     conv_flops = zoo.resnet18_flops(args.batch)
 
     cpu = None
