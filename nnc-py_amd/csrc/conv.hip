@@ -44,24 +44,29 @@ struct ConvArgs {
     int tiles_m, tiles_n;
 };
 
-// B operand: gathers input taps for X consecutive output pixels. KH/KW > 0
-// fix the kernel size at compile time (k -> (ci, r, c) by constant division).
-// Buffer loads over the whole input tensor (byte offsets < 2^31, checked on
-// the host); out-of-image taps get an out-of-range offset and read 0.
+// B operand: gathers input taps for X consecutive output pixels; each thread
+// takes one pixel and a run of KRUN consecutive k, so loads coalesce across
+// lanes (consecutive pixels) and the run is written to LDS as 16-byte
+// stores. k -> (ci, tap) is decomposed once per slice and then stepped. KH/KW
+// > 0 fix the kernel size at compile time; then the taps inside the image
+// are a per-tile bit mask. Buffer loads over the whole input tensor (byte
+// offsets < 2^31, checked on the host); out-of-image taps get an
+// out-of-range offset and read 0.
 template <int X, int BK, int LD, int KH, int KW>
 struct ConvGather {
-    static constexpr int KROWS = 256 / X;
-    static constexpr int PER = X * BK / 256;
-    static_assert(256 % X == 0 && BK % KROWS == 0, "gather shape");
+    static constexpr int KRUN = X * BK / 256;
+    static constexpr bool MASK = KH > 0 && KH * KW <= 64;
+    static_assert(256 % X == 0 && KRUN % 4 == 0, "gather shape");
     __amdgpu_buffer_rsrc_t rsrc;
-    int img, h0, w0, H, W, K, kw_rt, khw_rt, HW;
+    int pix_off, h0, w0, H, W, K, kw_rt, khw_rt, HW;
+    uint64_t taps;  // bit t: tap t of this pixel is inside the image (MASK)
     bool valid;
-    int xx, kk;
-    float v[PER];
+    int xx, kbase;
+    float v[KRUN];
 
     __device__ void init(const ConvArgs& a, int j0) {
         xx = threadIdx.x % X;
-        kk = threadIdx.x / X;
+        kbase = (threadIdx.x / X) * KRUN;
         const int pix = j0 + xx;
         valid = pix < a.Npix;
         const int p = valid ? pix : 0;
@@ -78,33 +83,52 @@ struct ConvGather {
         K = a.K;
         kw_rt = a.kw;
         khw_rt = a.kh * a.kw;
-        img = n * a.Ci * HW;
+        pix_off = n * a.Ci * HW + h0 * W + w0;  // element offset of tap (0, 0), channel 0
         rsrc = make_rsrc(a.in);
+        taps = 0;
+        if constexpr (MASK) {
+#pragma unroll
+            for (int r = 0; r < KH; ++r)
+#pragma unroll
+                for (int c = 0; c < KW; ++c) {
+                    const bool in = valid && (unsigned)(h0 + r) < (unsigned)H && (unsigned)(w0 + c) < (unsigned)W;
+                    taps |= (uint64_t)in << (r * KW + c);
+                }
+        }
     }
     __device__ void load(int k0) {
         const int khw = KH > 0 ? KH * KW : khw_rt;
         const int kwid = KW > 0 ? KW : kw_rt;
+        const int kstart = k0 + kbase;
+        int ci = kstart / khw;
+        int t = kstart - ci * khw;
 #pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int k = k0 + kk + p * KROWS;
-            const int ci = k / khw;
-            const int t = k - ci * khw;
+        for (int p = 0; p < KRUN; ++p) {
             const int r = t / kwid;
             const int c = t - r * kwid;
-            const int h = h0 + r, w = w0 + c;
-            const bool ok = valid && k < K && (unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W;
-            v[p] = load_f32(rsrc, ok ? (uint32_t)(img + ci * HW + h * W + w) * 4u : kOutOfRange);
+            bool ok;
+            if constexpr (MASK)
+                ok = ((taps >> t) & 1) != 0;
+            else
+                ok = valid && (unsigned)(h0 + r) < (unsigned)H && (unsigned)(w0 + c) < (unsigned)W;
+            ok = ok && kstart + p < K;
+            v[p] = load_f32(rsrc, ok ? (uint32_t)(pix_off + ci * HW + r * W + c) * 4u : kOutOfRange);
+            // step to k + 1
+            ++t;
+            const bool wrap = t == khw;
+            t = wrap ? 0 : t;
+            ci += wrap ? 1 : 0;
         }
     }
     __device__ void store(float* S) const {
 #pragma unroll
-        for (int p = 0; p < PER; ++p) S[(kk + p * KROWS) * LD + xx] = v[p];
+        for (int p = 0; p < KRUN; p += 4) lds_store4(S + xx * LD + kbase + p, v[p], v[p + 1], v[p + 2], v[p + 3]);
     }
 };
 
 template <class T, int KH, int KW, bool AVEC>
 __global__ void __launch_bounds__(256, 2) conv_streamk_k(ConvArgs a, StreamK sk) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     const int g = xcd_remap(blockIdx.x, sk.G);
     const int hw = a.Ho * a.Wo;
     SegmentWalker walk(sk, g);
@@ -113,11 +137,11 @@ __global__ void __launch_bounds__(256, 2) conv_streamk_k(ConvArgs a, StreamK sk)
         const int mt = seg.tile % a.tiles_m, nt = seg.tile / a.tiles_m;
         const int i0 = mt * T::BM, j0 = nt * T::BN;
 
-        typedef typename std::conditional<AVEC, KContigLoader4<T::BM, T::BK, T::LDA>,
-                                          KContigLoader<T::BM, T::BK, T::LDA>>::type LA;
+        typedef typename std::conditional<AVEC, KContigLoader4<T::BM, T::BK, T::LDK>,
+                                          KContigLoader<T::BM, T::BK, T::LDK>>::type LA;
         LA la;
         la.init(a.w + (int64_t)i0 * a.K, a.K, a.Co - i0, a.K);
-        ConvGather<T::BN, T::BK, T::LDB, KH, KW> lb;
+        ConvGather<T::BN, T::BK, T::LDK, KH, KW> lb;
         lb.init(a, j0);
         floatx16 sum[T::TM][T::TN];
         mfma_mainloop<T, false>(la, lb, seg.kb * T::BK, min(a.K, seg.ke * T::BK), lds, sum);

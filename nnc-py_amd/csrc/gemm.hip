@@ -72,11 +72,11 @@ struct PickLoader<kXC, X, BK, LD> {
 
 template <class T, int AK, int BKIND>
 __global__ void __launch_bounds__(256, 2) gemm_streamk_k(GemmArgs g, StreamK sk) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     const int wg = xcd_remap(blockIdx.x, sk.G);
     const int per_batch = g.tiles_m * g.tiles_n;
-    typedef PickLoader<AK, T::BM, T::BK, T::LDA> PA;
-    typedef PickLoader<BKIND, T::BN, T::BK, T::LDB> PB;
+    typedef PickLoader<AK, T::BM, T::BK, T::LDK> PA;
+    typedef PickLoader<BKIND, T::BN, T::BK, T::LDK> PB;
     SegmentWalker walk(sk, wg);
     Segment seg;
     while (walk.next(sk, seg)) {

@@ -6,17 +6,22 @@
 // owns a (BM/WM) x (BN/WN) sub-tile made of 32x32 blocks, each block one
 // v_mfma_f32_32x32x2_f32 accumulator (16 VGPRs per lane).
 //
-// Operand staging: every BK-deep slice of A and B is read from HBM/L2 into
-// registers by a loader and stored into LDS as S[k][x] (x = i for A, j for
-// B; rows padded by one float so transposed stores and MFMA operand reads
-// stay bank-conflict-free). LDS is double-buffered: while the MFMAs consume
-// slice t from one buffer, slice t+1's global loads are in flight and are
-// then stored to the other buffer, so each slice costs one barrier. Loads are
-// raw buffer loads (buffer resource in SGPRs, 32-bit byte offsets): an
-// out-of-range element gets an offset past the resource's size and the
-// hardware returns 0, so loads need no branch and no select afterwards, the
-// loaded registers go straight to LDS and the wait for the loads falls after
-// the slice's MFMAs. Byte offsets must stay below 2^31 (checked on the host).
+// Operand staging: every BK = 32 deep slice of A and B is read from HBM/L2
+// into registers by a loader and stored into LDS as S[x][k] (x = i for A, j
+// for B), k contiguous, rows padded to 36 floats so 16-byte reads and writes
+// of eight consecutive rows hit distinct banks. An MFMA step consumes one k
+// per lane half; lane half h takes k = 16h + s at step s, so over the slice
+// each lane reads 16 consecutive k of its row: one ds_read_b128 per operand
+// block feeds four MFMA steps. Loaders write runs of 4 consecutive k as
+// ds_write_b128 where their thread mapping allows. LDS is double-buffered:
+// while the MFMAs consume slice t from one buffer, slice t+1's global loads
+// are in flight and are then stored to the other buffer, so each slice costs
+// one barrier. Loads are raw buffer loads (buffer resource in SGPRs, 32-bit
+// byte offsets): an out-of-range element gets an offset past the resource's
+// size and the hardware returns 0, so loads need no branch and no select
+// afterwards, the loaded registers go straight to LDS and the wait for the
+// loads falls after the slice's MFMAs. Byte offsets must stay below 2^31
+// (checked on the host).
 //
 // Scheduling is hybrid stream-K: a persistent grid of G workgroups (at
 // most the number resident on the GPU at once). Tiles [0, sk_tiles) form
@@ -31,9 +36,10 @@
 // 588 workgroups on 512 slots leave the second round 15% full) while
 // splitting no more tiles than needed.
 //
-// MFMA 32x32x2 f32 operand/result layout (lane l of 64):
-//   A operand: A[i = l % 32][k = l / 32]
-//   B operand: B[k = l / 32][j = l % 32]
+// MFMA 32x32x2 f32 operand/result layout (lane l of 64): the instruction
+// sums over its two k, one per lane half:
+//   A operand: A[i = l % 32][k-half l / 32]
+//   B operand: B[k-half l / 32][j = l % 32]
 //   D register r: D[i = 8*(r/4) + 4*(l/32) + r%4][j = l % 32]
 #pragma once
 
@@ -69,20 +75,27 @@ struct Tile {
     static constexpr int WAVE_M = BM / WM, WAVE_N = BN / WN;
     static constexpr int TM = WAVE_M / 32, TN = WAVE_N / 32;
     static_assert(TM >= 1 && TN >= 1 && WAVE_M % 32 == 0 && WAVE_N % 32 == 0, "32x32 blocks");
-    static_assert(BK % 2 == 0, "k step of 2");
-    static constexpr int LDA = BM + 1, LDB = BN + 1;
-    static constexpr int STAGE = BK * (LDA + LDB);  // floats per LDS buffer
+    static_assert(BK == 32, "lane halves take 16 consecutive k each");
+    static constexpr int LDK = BK + 4;  // row stride of S[x][k] in floats
+    static constexpr int A_FLOATS = BM * LDK, B_FLOATS = BN * LDK;
+    static constexpr int STAGE = A_FLOATS + B_FLOATS;  // floats per LDS buffer
     static constexpr int LDS_FLOATS = 2 * STAGE;
     static_assert((BM * BN) % 1024 == 0, "fixup chunks of 256 float4");
 };
 
+// four consecutive floats of one LDS row (16-byte aligned)
+__device__ __forceinline__ void lds_store4(float* dst, float a, float b, float c, float d) {
+    *reinterpret_cast<f32x4*>(dst) = f32x4{a, b, c, d};
+}
+
 // ---------------------------------------------------------------------------
-// operand loaders: fill S[k][x] for x in [0, X), k in [k0, k0 + BK); elements
-// outside [0, xlim) x [0, K) are zero. `base` is the tile origin; every
-// in-range element's byte offset from it is below 2^31.
+// operand loaders: fill S[x][k] (row stride LD) for x in [0, X), k in
+// [k0, k0 + BK); elements outside [0, xlim) x [0, K) are zero. `base` is the
+// tile origin; every in-range element's byte offset from it is below 2^31.
 // ---------------------------------------------------------------------------
 
-// element (x, k) at base[x * ld + k]  (row-major A, or B stored [N][K])
+// element (x, k) at base[x * ld + k]  (row-major A, or B stored [N][K]);
+// lanes along k
 template <int X, int BK, int LD>
 struct KContigLoader {
     static constexpr int ROWS_PER_PASS = 256 / BK;
@@ -111,11 +124,12 @@ struct KContigLoader {
     }
     __device__ void store(float* S) const {
 #pragma unroll
-        for (int p = 0; p < PER; ++p) S[kk * LD + xx + p * ROWS_PER_PASS] = v[p];
+        for (int p = 0; p < PER; ++p) S[(xx + p * ROWS_PER_PASS) * LD + kk] = v[p];
     }
 };
 
-// 16-byte loads; requires ld % 4 == 0, K % 4 == 0, 16-byte aligned base
+// 16-byte loads along k; requires ld % 4 == 0, K % 4 == 0, 16-byte aligned
+// base. Each thread's float4 is one 16-byte LDS write.
 template <int X, int BK, int LD>
 struct KContigLoader4 {
     static constexpr int KQ = BK / 4;
@@ -145,25 +159,19 @@ struct KContigLoader4 {
     }
     __device__ void store(float* S) const {
 #pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int x = xx + p * ROWS_PER_PASS;
-            S[(kk + 0) * LD + x] = v[p].x;
-            S[(kk + 1) * LD + x] = v[p].y;
-            S[(kk + 2) * LD + x] = v[p].z;
-            S[(kk + 3) * LD + x] = v[p].w;
-        }
+        for (int p = 0; p < PER; ++p) *reinterpret_cast<f32x4*>(S + (xx + p * ROWS_PER_PASS) * LD + kk) = v[p];
     }
 };
 
-// element (x, k) at base[k * ld + x]  (A stored [K][M], or row-major B)
+// element (x, k) at base[k * ld + x]  (A stored [K][M], or row-major B);
+// lanes along x, each thread a run of KRUN consecutive k of one x
 template <int X, int BK, int LD>
 struct XContigLoader {
-    static constexpr int KROWS_PER_PASS = 256 / X;
-    static constexpr int PER = X * BK / 256;
-    static_assert(256 % X == 0 && BK % KROWS_PER_PASS == 0, "loader shape");
+    static constexpr int KRUN = X * BK / 256;
+    static_assert(256 % X == 0 && KRUN % 4 == 0, "loader shape");
     __amdgpu_buffer_rsrc_t rsrc;
-    int ld, xlim, K, xx, kk;
-    float v[PER];
+    int ld, xlim, K, xx, kbase;
+    float v[KRUN];
 
     __device__ void init(const float* b, int64_t ld_, int xlim_, int K_) {
         rsrc = make_rsrc(b);
@@ -171,33 +179,35 @@ struct XContigLoader {
         xlim = xlim_;
         K = K_;
         xx = threadIdx.x % X;
-        kk = threadIdx.x / X;
+        kbase = (threadIdx.x / X) * KRUN;
     }
     __device__ void load(int k0) {
 #pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int k = k0 + kk + p * KROWS_PER_PASS;
+        for (int p = 0; p < KRUN; ++p) {
+            const int k = k0 + kbase + p;
             const bool ok = xx < xlim && k < K;
             v[p] = load_f32(rsrc, ok ? (uint32_t)(k * ld + xx) * 4u : kOutOfRange);
         }
     }
     __device__ void store(float* S) const {
 #pragma unroll
-        for (int p = 0; p < PER; ++p) S[(kk + p * KROWS_PER_PASS) * LD + xx] = v[p];
+        for (int p = 0; p < KRUN; p += 4) lds_store4(S + xx * LD + kbase + p, v[p], v[p + 1], v[p + 2], v[p + 3]);
     }
 };
 
-// 16-byte variant: requires ld % 4 == 0, xlim % 4 == 0 (so a group of four
-// is wholly inside or outside) and a 16-byte aligned base.
+// 16-byte loads along x: requires ld % 4 == 0, xlim % 4 == 0 (so a group of
+// four is wholly inside or outside) and a 16-byte aligned base. A thread
+// loads a 4 (x) by KRUN (k) block and writes it transposed, one run of KRUN
+// floats per x.
 template <int X, int BK, int LD>
 struct XContigLoader4 {
     static constexpr int XQ = X / 4;
-    static constexpr int KROWS_PER_PASS = 256 / XQ;
-    static constexpr int PER = X * BK / (256 * 4);
-    static_assert(X % 4 == 0 && 256 % XQ == 0 && BK % KROWS_PER_PASS == 0 && PER >= 1, "loader4");
+    static constexpr int KG = 256 / XQ;
+    static constexpr int KRUN = BK / KG;
+    static_assert(X % 4 == 0 && 256 % XQ == 0 && BK % KG == 0 && (KRUN == 2 || KRUN == 4), "loader4");
     __amdgpu_buffer_rsrc_t rsrc;
-    int ld, xlim, K, xx, kk;
-    f32x4 v[PER];
+    int ld, xlim, K, xx, kbase;
+    f32x4 v[KRUN];
 
     __device__ void init(const float* b, int64_t ld_, int xlim_, int K_) {
         rsrc = make_rsrc(b);
@@ -205,33 +215,36 @@ struct XContigLoader4 {
         xlim = xlim_;
         K = K_;
         xx = (threadIdx.x % XQ) * 4;
-        kk = threadIdx.x / XQ;
+        kbase = (threadIdx.x / XQ) * KRUN;
     }
     __device__ void load(int k0) {
 #pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int k = k0 + kk + p * KROWS_PER_PASS;
+        for (int p = 0; p < KRUN; ++p) {
+            const int k = k0 + kbase + p;
             const bool ok = xx < xlim && k < K;
             v[p] = load_f32x4(rsrc, ok ? (uint32_t)(k * ld + xx) * 4u : kOutOfRange);
         }
     }
     __device__ void store(float* S) const {
 #pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            float* dst = S + (kk + p * KROWS_PER_PASS) * LD + xx;
-            dst[0] = v[p].x;
-            dst[1] = v[p].y;
-            dst[2] = v[p].z;
-            dst[3] = v[p].w;
+        for (int i = 0; i < 4; ++i) {
+            float* dst = S + (xx + i) * LD + kbase;
+            if constexpr (KRUN == 4) {
+                lds_store4(dst, v[0][i], v[1][i], v[2][i], v[3][i]);
+            } else {
+                typedef float f32x2 __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<f32x2*>(dst) = f32x2{v[0][i], v[1][i]};
+            }
         }
     }
 };
 
 // ---------------------------------------------------------------------------
 // main loop over k in [k_begin, k_end) (k_begin a multiple of BK); LDS holds
-// two stages of T::STAGE floats. TWO_LEVEL adds each slice's products into
-// the running sum through a fresh accumulator (shorter fp32 rounding chains
-// for very long K); otherwise the MFMAs accumulate into `sum` directly.
+// two stages of T::STAGE floats (A rows, then B rows). TWO_LEVEL adds each
+// slice's products into the running sum through a fresh accumulator
+// (shorter fp32 rounding chains for very long K); otherwise the MFMAs
+// accumulate into `sum` directly.
 // ---------------------------------------------------------------------------
 template <class T, bool TWO_LEVEL, class LA, class LB>
 __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k_end, float* lds,
@@ -240,8 +253,9 @@ __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k
     const int wave = threadIdx.x >> 6;
     const int wi = (wave / T::WN) * T::WAVE_M;
     const int wj = (wave % T::WN) * T::WAVE_N;
-    const int a_off = (lane >> 5) * T::LDA + wi + (lane & 31);
-    const int b_off = T::BK * T::LDA + (lane >> 5) * T::LDB + wj + (lane & 31);
+    // this lane's row of A (i) and of B (j), and its half of the slice's k
+    const int a_off = (wi + (lane & 31)) * T::LDK + 16 * (lane >> 5);
+    const int b_off = T::A_FLOATS + (wj + (lane & 31)) * T::LDK + 16 * (lane >> 5);
 
 #pragma unroll
     for (int tm = 0; tm < T::TM; ++tm)
@@ -254,7 +268,7 @@ __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k
     la.load(k_begin);
     lb.load(k_begin);
     la.store(lds);
-    lb.store(lds + T::BK * T::LDA);
+    lb.store(lds + T::A_FLOATS);
     __syncthreads();
 
     int stage = 0;
@@ -275,22 +289,40 @@ __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[tm][tn][r] = 0.f;
         }
+        // four quads of four k per lane half
+        f32x4 a[T::TM], b[T::TN];
 #pragma unroll
-        for (int kk = 0; kk < T::BK; kk += 2) {
-            float a[T::TM], b[T::TN];
+        for (int tm = 0; tm < T::TM; ++tm) a[tm] = *reinterpret_cast<const f32x4*>(Ap + tm * 32 * T::LDK);
 #pragma unroll
-            for (int tm = 0; tm < T::TM; ++tm) a[tm] = Ap[kk * T::LDA + tm * 32];
+        for (int tn = 0; tn < T::TN; ++tn) b[tn] = *reinterpret_cast<const f32x4*>(Bp + tn * 32 * T::LDK);
 #pragma unroll
-            for (int tn = 0; tn < T::TN; ++tn) b[tn] = Bp[kk * T::LDB + tn * 32];
+        for (int q = 0; q < 4; ++q) {
+            f32x4 an[T::TM], bn[T::TN];
+            if (q < 3) {
 #pragma unroll
-            for (int tm = 0; tm < T::TM; ++tm)
+                for (int tm = 0; tm < T::TM; ++tm)
+                    an[tm] = *reinterpret_cast<const f32x4*>(Ap + tm * 32 * T::LDK + 4 * (q + 1));
 #pragma unroll
-                for (int tn = 0; tn < T::TN; ++tn) {
-                    if (TWO_LEVEL)
-                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm], b[tn], acc[tm][tn], 0, 0, 0);
-                    else
-                        sum[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm], b[tn], sum[tm][tn], 0, 0, 0);
-                }
+                for (int tn = 0; tn < T::TN; ++tn)
+                    bn[tn] = *reinterpret_cast<const f32x4*>(Bp + tn * 32 * T::LDK + 4 * (q + 1));
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                    for (int tn = 0; tn < T::TN; ++tn) {
+                        if (TWO_LEVEL)
+                            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm][st], b[tn][st], acc[tm][tn], 0, 0, 0);
+                        else
+                            sum[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm][st], b[tn][st], sum[tm][tn], 0, 0, 0);
+                    }
+            if (q < 3) {
+#pragma unroll
+                for (int tm = 0; tm < T::TM; ++tm) a[tm] = an[tm];
+#pragma unroll
+                for (int tn = 0; tn < T::TN; ++tn) b[tn] = bn[tn];
+            }
         }
         if (TWO_LEVEL) {
 #pragma unroll
@@ -301,7 +333,7 @@ __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k
         if (more) {
             float* next = lds + (stage ^ 1) * T::STAGE;
             la.store(next);
-            lb.store(next + T::BK * T::LDA);
+            lb.store(next + T::A_FLOATS);
         }
         __syncthreads();
         stage ^= 1;
