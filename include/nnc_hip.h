@@ -99,6 +99,17 @@ int nnc_hip_graph_end(void);
 int nnc_hip_graph_launch(void);
 void nnc_hip_graph_destroy(void);
 
+/* ---- fused operators of the mi355x target --------------------------------
+ * No counterpart in the reference ABI (runtime/include/nnc_ops.h); emitted by
+ * the mi355x compiler target at O3.
+ *
+ * nnc_hip_conv_add_relu: a residual block's Conv -> Add -> Relu in one
+ * kernel: out = relu(conv(in, w) + bias + res), equal to nnc_conv followed by
+ * nnc_add_relu(conv_out, res, out) (same rounding sequence). `res` has the
+ * output's shape and may be the same buffer as `out`; `b` may be NULL. */
+void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw,
+                           int sh, int sw, int ph, int pw);
+
 #ifdef __cplusplus
 }
 #endif

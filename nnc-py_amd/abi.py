@@ -114,14 +114,20 @@ SIGNATURES: dict[str, list] = {
 # reference code generator emits it, no reference runtime defines it).
 NOT_IN_REFERENCE = {"nnc_matmul_relu"}
 
+# Fused operators of the mi355x target (include/nnc_hip.h), emitted at O3.
+TARGET_SIGNATURES = {
+    "nnc_hip_conv_add_relu": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int],
+}
+
 
 def bind(lib: ctypes.CDLL, names=None) -> ctypes.CDLL:
     """Attach argtypes/restype for the nnc_* symbols that `lib` exports."""
-    for name in names or SIGNATURES:
+    table = {**SIGNATURES, **TARGET_SIGNATURES}
+    for name in names or table:
         fn = getattr(lib, name, None)
         if fn is None:
             continue
-        fn.argtypes = SIGNATURES[name]
+        fn.argtypes = table[name]
         fn.restype = None
     return lib
 

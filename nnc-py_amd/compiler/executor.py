@@ -22,7 +22,7 @@ import numpy as np
 from .. import abi
 from .ir import Graph, Node
 from .lower import Call, lower
-from .passes import (MemoryPlan, check_plan, eliminate_dead_code, eliminate_identity, fuse_patterns,
+from .passes import (MemoryPlan, check_plan, eliminate_dead_code, eliminate_identity, fuse_patterns, fuse_residual,
                      plan_memory, prepack_lowering)
 
 
@@ -35,6 +35,13 @@ class Program:
     opt_level: int
 
 
+# Conv -> Add -> Relu fusion into nnc_hip_conv_add_relu: switched off. Its
+# first GPU run (together with new kernel-shape tests) ended in a GPU fault
+# whose cause has not been found; the pass and the entry point stay for CPU
+# tests until it is.
+RESIDUAL_FUSION = False
+
+
 def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None = None,
                   max_memory: int | None = None) -> Program:
     """Pass pipeline per optimisation level (passes/base.py:67-161 of the
@@ -44,6 +51,8 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
         eliminate_dead_code(graph)
     if opt_level >= 3:
         fuse_patterns(graph)
+        if RESIDUAL_FUSION:
+            fuse_residual(graph)
         prepack_lowering(graph)
     order = graph.topological_sort()
     strategy = memory_strategy or ("basic" if opt_level == 0 else "cost_aware")

@@ -25,6 +25,7 @@ FUSED = {
     "FusedAddRelu": ("Add", "Relu"),
     "FusedAddSigmoid": ("Add", "Sigmoid"),
     "FusedMatMulRelu": ("MatMul", "Relu"),
+    "FusedConvAddRelu": ("Conv", "Add", "Relu"),
 }
 
 

@@ -53,6 +53,10 @@ def _conv_call(g: Graph, node: Node) -> Call:
     sh, sw = (list(node.attrs.get("strides", [1, 1])) + [1])[:2]
     pads = list(node.attrs.get("pads", [0, 0, 0, 0]))
     ph, pw = (pads + [0, 0])[:2]
+    if node.op_type == "FusedConvAddRelu":
+        return Call("nnc_hip_conv_add_relu", [_t(x), _t(w), _opt(node, 2), _t(node.inputs[3]),
+                                              _t(node.outputs[0])] + [("i", v) for v in (kh, kw, sh, sw, ph, pw)],
+                    node.name)
     io = [_t(x), _t(w), _opt(node, 2), _t(node.outputs[0])]
     if node.op_type == "FusedConvSigmoid":
         return Call("nnc_conv_sigmoid", io + [("i", v) for v in (kh, kw, sh, sw, ph, pw)], node.name)
@@ -117,7 +121,7 @@ _CAST = {"float32": 0, "float16": 1, "int32": 2, "int8": 3, "uint8": 4, "bool": 
 def lower_node(g: Graph, node: Node) -> Call:
     op = node.op_type
     ins, outs = node.inputs, node.outputs
-    if op in ("Conv", "FusedConvRelu", "FusedConvSigmoid"):
+    if op in ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu"):
         return _conv_call(g, node)
     if op == "Gemm":
         args = [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0]),

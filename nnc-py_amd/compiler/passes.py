@@ -32,7 +32,10 @@ ALIGN = 256  # arena offsets; 16-byte vector loads need 16, 256 keeps rows cache
 # ops that may write over a same-sized input that dies at the node
 # (cost_aware_allocator.py:39-48)
 INPLACE_OPS = {"Relu", "Sigmoid", "Tanh", "Add", "Sub", "Mul", "Div", "Clip",
-               "FusedAddRelu", "FusedAddSigmoid"}
+               "FusedAddRelu", "FusedAddSigmoid", "FusedConvAddRelu"}
+# inputs an in-place output may take over (default: any); the fused conv
+# reads its image input at neighbouring pixels, so only the residual
+INPLACE_INPUTS = {"FusedConvAddRelu": (3,)}
 
 
 # ---------------------------------------------------------------------------
@@ -110,11 +113,44 @@ def fuse_patterns(g: Graph) -> int:
     return fused
 
 
+def fuse_residual(g: Graph) -> int:
+    """mi355x target, O3: a fused Add+Relu one of whose operands is produced
+    by a Conv (no activation) used only there, the other operand having the
+    conv output's exact shape, becomes one FusedConvAddRelu node (inputs: x,
+    w, bias or "", residual), lowered to nnc_hip_conv_add_relu: the residual
+    is added in the conv epilogue instead of a separate pass over both
+    tensors. The Add's first operand is preferred (the block's main-path
+    conv in ResNet; the shortcut conv stays a plain conv)."""
+    fused = 0
+    for add in list(g.nodes):
+        if add.op_type != "FusedAddRelu" or len(add.inputs) != 2 or add.inputs[0] == add.inputs[1]:
+            continue
+        for k in (0, 1):
+            mid, res = add.inputs[k], add.inputs[1 - k]
+            prod = g.producer(mid)
+            if prod is None or prod.op_type != "Conv" or mid in g.outputs:
+                continue
+            if len(g.consumers(mid)) != 1:
+                continue
+            if g.tensors[res].shape != g.tensors[mid].shape or g.tensors[res].dtype != g.tensors[mid].dtype:
+                continue
+            inputs = list(prod.inputs) + [""] * (3 - len(prod.inputs))
+            prod.inputs = inputs[:3] + [res]
+            prod.op_type = "FusedConvAddRelu"
+            prod.outputs = list(add.outputs)
+            prod.metadata["fused_from"] = [prod.name, add.name]
+            g.nodes.remove(add)
+            g.tensors.pop(mid, None)
+            fused += 1
+            break
+    return fused
+
+
 def prepack_lowering(g: Graph) -> None:
     """Conv kernel kind and constant Gemm B packing
     (passes/prepack_lowering.py:48-118)."""
     for node in g.nodes:
-        if node.op_type in ("Conv", "FusedConvRelu", "FusedConvSigmoid"):
+        if node.op_type in ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu"):
             kh, kw = node.attrs.get("kernel_shape", [1, 1])
             sh, sw = node.attrs.get("strides", [1, 1])
             pads = node.attrs.get("pads", [0, 0, 0, 0])
@@ -251,7 +287,10 @@ def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
                 continue
             slot = None
             if strategy == "cost_aware" and node.op_type in INPLACE_OPS:
-                for i in node.inputs:
+                allowed = INPLACE_INPUTS.get(node.op_type)
+                for k, i in enumerate(node.inputs):
+                    if allowed is not None and k not in allowed:
+                        continue
                     li = live.get(i)
                     if (li and li.end == idx and not li.is_output and not li.is_input
                             and i in plan.offsets and i not in reused and sizes[i] == sizes[o]):

@@ -37,6 +37,7 @@ struct ConvArgs {
     const float* in;
     const float* w;
     const float* bias;
+    const float* res;  // residual added before the activation (nullable)
     float* out;
     float* ws;  // stream-K partial tiles
     int N, Ci, H, W, Co, Ho, Wo, kh, kw, sh, sw, ph, pw;
@@ -158,8 +159,11 @@ __global__ void __launch_bounds__(256, 2) conv_streamk_k(ConvArgs a, StreamK sk)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int co = i0 + acc_row<T>(tm, r);
-                        if (co < a.Co)
-                            obase[(int64_t)co * hw] = activate(sum[tm][tn][r] + (a.bias ? a.bias[co] : 0.f), a.act);
+                        if (co < a.Co) {
+                            float v = sum[tm][tn][r] + (a.bias ? a.bias[co] : 0.f);
+                            if (a.res) v += a.res[(obase - a.out) + (int64_t)co * hw];
+                            obase[(int64_t)co * hw] = activate(v, a.act);
+                        }
                     }
             }
         } else {
@@ -205,7 +209,10 @@ __global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
         const int pix = p0 + q;
         if (pix >= a.Npix) break;
         const int n = pix / hw;
-        a.out[((int64_t)n * a.Co + co) * hw + (pix - n * hw)] = activate(vals[q] + b, a.act);
+        const int64_t o = ((int64_t)n * a.Co + co) * hw + (pix - n * hw);
+        float v = vals[q] + b;
+        if (a.res) v += a.res[o];
+        a.out[o] = activate(v, a.act);
     }
 }
 
@@ -285,8 +292,9 @@ static bool conv_check(Tensor* in, Tensor* w, Tensor* out, const char* name) {
 }
 
 static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw,
-                     int ph, int pw, int act, const char* name) {
+                     int ph, int pw, int act, const char* name, Tensor* res = nullptr) {
     ConvArgs a{};
+    a.res = res ? (const float*)res->data : nullptr;
     a.in = (const float*)in->data;
     a.w = (const float*)w->data;
     a.bias = (b && b->data) ? (const float*)b->data : nullptr;
@@ -315,6 +323,8 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     if (out->shape[0] < a.N || out->shape[1] < a.Co)
         return fail(NNC_HIP_EINVAL, name, "output smaller than N x Co");
     if (a.bias && numel(b) < a.Co) return fail(NNC_HIP_EINVAL, name, "bias smaller than Co");
+    if (res && numel(res) < (int64_t)a.N * a.Co * out->shape[2] * out->shape[3])
+        return fail(NNC_HIP_EINVAL, name, "residual smaller than the output");
     const int64_t K = (int64_t)a.Ci * kh * kw;
     const int64_t npix = (int64_t)a.N * a.Ho * a.Wo;
     // the kernels address input and weights with 32-bit byte offsets
@@ -383,5 +393,17 @@ NNC_CONV3X3_ENTRY(nnc_conv_relu3x3_s1, kActRelu)
     }
 NNC_CONV7X7_ENTRY(nnc_conv7x7_s2, kActNone)
 NNC_CONV7X7_ENTRY(nnc_conv_relu7x7_s2, kActRelu)
+
+// Not in the reference ABI: Conv -> Add(residual) -> Relu as one kernel,
+// emitted by the mi355x target at O3 for residual blocks. out = relu(conv(in,
+// w) + bias + res), with the sum taken in the order of nnc_conv followed by
+// nnc_add_relu(conv_out, res). `res` may be the same buffer as `out`.
+void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,
+                           int sw, int ph, int pw) {
+    const char* name = "nnc_hip_conv_add_relu";
+    if (!conv_check(in, w, out, name)) return;
+    if (!res || !res->data || !res->shape) return fail(NNC_HIP_EINVAL, name, "NULL residual");
+    conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, kActRelu, name, res);
+}
 
 }  // extern "C"

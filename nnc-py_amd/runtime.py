@@ -54,6 +54,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_graph_end": ([], ctypes.c_int),
     "nnc_hip_graph_launch": ([], ctypes.c_int),
     "nnc_hip_graph_destroy": ([], None),
+    "nnc_hip_conv_add_relu": (abi.TARGET_SIGNATURES["nnc_hip_conv_add_relu"], None),
 }
 
 

@@ -26,6 +26,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "nnc_hip.h"
 #include "nnc_ops.h"
 
 #define MAXPOOL_INIT (-3.402823e38f) /* ops.c:347, 366 */
@@ -928,4 +929,23 @@ void nnc_lstm(Tensor* X, Tensor* W, Tensor* R, Tensor* B, Tensor* Y, Tensor* Yh,
         }
     }
     free(h); free(c); free(hn); free(cn);
+}
+
+/* ------------------------------------------------------------------------
+ * Fused operator of the mi355x target (include/nnc_hip.h), no reference
+ * counterpart: restated as the composition it replaces, nnc_conv into a
+ * temporary and nnc_add_relu(conv_out, res, out) (ops.c:1449-1463,
+ * 3233-3288). `res` may alias `out`. Pinned by composition of two pinned
+ * entry points.
+ * ---------------------------------------------------------------------- */
+void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw,
+                           int sh, int sw, int ph, int pw) {
+    const int64_t n = numel(out);
+    float* tmp = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    if (!tmp) return;
+    Tensor t = *out;
+    t.data = tmp;
+    nnc_conv(in, w, b, &t, kh, kw, sh, sw, ph, pw);
+    nnc_add_relu(&t, res, out);
+    free(tmp);
 }
