@@ -35,11 +35,8 @@ class Program:
     opt_level: int
 
 
-# Conv -> Add -> Relu fusion into nnc_hip_conv_add_relu: switched off. Its
-# first GPU run (together with new kernel-shape tests) ended in a GPU fault
-# whose cause has not been found; the pass and the entry point stay for CPU
-# tests until it is.
-RESIDUAL_FUSION = False
+# Conv -> Add -> Relu fusion into nnc_hip_conv_add_relu at O3 (mi355x target).
+RESIDUAL_FUSION = True
 
 
 def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None = None,

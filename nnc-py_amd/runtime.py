@@ -70,7 +70,9 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     p = Path(path) if path else LIB_PATH
     if not p.exists():
         raise HipError(f"{p} is not built; run `python nnc-py_amd/build.py` (or __graft_entry__.build())")
-    lib = ctypes.CDLL(str(p), mode=ctypes.RTLD_GLOBAL)
+    # RTLD_LOCAL: the library's nnc_* names must not interpose on another
+    # implementation of the ABI loaded in the same process (the CPU oracle)
+    lib = ctypes.CDLL(str(p), mode=ctypes.RTLD_LOCAL)
     abi.bind(lib)
     for name, (args, res) in _HIP_SIGNATURES.items():
         fn = getattr(lib, name)

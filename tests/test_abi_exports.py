@@ -53,3 +53,29 @@ def test_product_does_not_link_the_oracle(pkg):
     from nnc_py_amd import runtime
     data = runtime.LIB_PATH.read_bytes()
     assert b"liboracle" not in data and b"libref_ops" not in data
+
+
+def test_oracle_internal_calls_never_reach_the_hip_library(pkg, oracle_lib):
+    """The oracle's composed entry points (nnc_matmul_relu,
+    nnc_hip_conv_add_relu) call its own nnc_conv / nnc_matmul / nnc_add_relu /
+    nnc_relu. In a GPU test process libnnc_hip.so exports the same names; if
+    those calls bound to it they would launch GPU kernels on host pointers.
+    Both libraries are loaded here as a GPU test would (the HIP library even
+    with RTLD_GLOBAL), with eager binding, and the dynamic linker's binding
+    log must show no oracle reference resolved into libnnc_hip.so. No GPU call
+    is made."""
+    import os
+    import subprocess
+    import sys
+    from nnc_py_amd import runtime
+    if not runtime.LIB_PATH.exists():
+        pytest.fail("libnnc_hip.so is not built: run __graft_entry__.build()")
+    oracle = ROOT / "oracle" / "liboracle.so"
+    code = (f"import ctypes; ctypes.CDLL({str(runtime.LIB_PATH)!r}, mode=ctypes.RTLD_GLOBAL); "
+            f"ctypes.CDLL({str(oracle)!r})")
+    env = dict(os.environ, LD_DEBUG="bindings", LD_BIND_NOW="1")
+    res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr[-2000:]
+    bad = [l for l in res.stderr.splitlines()
+           if "liboracle.so" in l.split(" to ")[0] and "libnnc_hip.so" in l.split(" to ")[-1]]
+    assert not bad, bad[:5]

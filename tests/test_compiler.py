@@ -60,38 +60,35 @@ def test_o1_call_sequence_matches_reference_snapshot(model, pkg):
 
 
 def test_o3_fusion_and_prepack_on_resnet18(pkg):
-    """O3: conv+relu and add+relu fusion, conv entry selection, constant FC
+    """O3: conv+relu fusion, each residual block's conv+add+relu as one call
+    (in place only over the residual), conv entry selection, constant FC
     weight as gemm_nt."""
     from nnc_py_amd.compiler import build_program, zoo
     prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
     ops = [c.op for c in prog.calls]
-    assert len(ops) == 32
-    assert ops.count("nnc_add_relu") == 8 and "nnc_relu" not in ops
-    assert ops.count("nnc_conv_relu3x3_s1") == 5  # conv1 of the five stride-1 blocks
-    assert ops[0] == "nnc_conv_relu7x7_s2" and ops.count("nnc_conv1x1") == 3
-    assert ops[-1] == "nnc_gemm_nt"
-
-
-def test_residual_fusion_pass(pkg):
-    """The Conv -> Add -> Relu pass (off by default): one fused call per
-    residual block, in place only over the residual."""
-    from nnc_py_amd.compiler import Executor, build_program, zoo
-    from nnc_py_amd.compiler import executor as ex_mod
-    ex_mod.RESIDUAL_FUSION = True
-    try:
-        prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
-    finally:
-        ex_mod.RESIDUAL_FUSION = False
-    ops = [c.op for c in prog.calls]
     assert len(ops) == 24
     assert ops.count("nnc_hip_conv_add_relu") == 8
     assert "nnc_add_relu" not in ops and "nnc_relu" not in ops
-    assert ops.count("nnc_conv_relu3x3_s1") == 5 and ops.count("nnc_conv1x1") == 3
+    assert ops.count("nnc_conv_relu3x3_s1") == 5  # conv1 of the five stride-1 blocks
+    assert ops[0] == "nnc_conv_relu7x7_s2" and ops.count("nnc_conv1x1") == 3
+    assert ops[-1] == "nnc_gemm_nt"
     for c in prog.calls:
         if c.op == "nnc_hip_conv_add_relu":
             res, out = c.args[3][1], c.args[4][1]
             assert prog.graph.tensors[res].shape == prog.graph.tensors[out].shape
             assert prog.plan.offsets[out] != prog.plan.offsets[c.args[0][1]]
+
+
+def test_residual_fusion_can_be_switched_off(pkg):
+    from nnc_py_amd.compiler import build_program, zoo
+    from nnc_py_amd.compiler import executor as ex_mod
+    ex_mod.RESIDUAL_FUSION = False
+    try:
+        prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
+    finally:
+        ex_mod.RESIDUAL_FUSION = True
+    ops = [c.op for c in prog.calls]
+    assert len(ops) == 32 and ops.count("nnc_add_relu") == 8
 
 
 def test_arena_plan_reuses_memory_and_keeps_invariants(pkg):

@@ -14,9 +14,7 @@ import pytest
 
 import caserun
 
-pytestmark = [pytest.mark.gpu,
-              pytest.mark.skip(reason="the first GPU run of this file (with the then new conv+add+relu "
-                                      "fusion) ended in a GPU fault whose cause is not yet found")]
+pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 1e-4, 1e-3
 
