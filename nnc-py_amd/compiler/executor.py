@@ -53,9 +53,9 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
         prepack_lowering(graph)
     order = graph.topological_sort()
     strategy = memory_strategy or ("basic" if opt_level == 0 else "cost_aware")
-    plan = plan_memory(graph, order, strategy, max_memory)
+    plan = plan_memory(graph, order, strategy, max_memory, alias_views=opt_level >= 3)
     check_plan(graph, order, plan)
-    return Program(graph, order, plan, lower(graph, order), opt_level)
+    return Program(graph, order, plan, lower(graph, order, plan.aliases), opt_level)
 
 
 class Executor:

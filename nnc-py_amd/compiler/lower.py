@@ -213,5 +213,7 @@ def lower_node(g: Graph, node: Node) -> Call:
     raise NotImplementedError(f"no nnc_* lowering for op {op!r} ({node.name})")
 
 
-def lower(g: Graph, order: list[Node]) -> list[Call]:
-    return [lower_node(g, n) for n in order]
+def lower(g: Graph, order: list[Node], aliases: dict[str, str] | None = None) -> list[Call]:
+    """One call per node, except view ops the plan turned into aliases."""
+    aliases = aliases or {}
+    return [lower_node(g, n) for n in order if not (n.outputs and n.outputs[0] in aliases)]

@@ -223,15 +223,23 @@ class MemoryPlan:
     constant_offset: int = 0
     total_bytes: int = 0
     inplace: dict[str, str] = field(default_factory=dict)  # output -> reused input
+    aliases: dict[str, str] = field(default_factory=dict)  # view output -> its input (no copy)
 
 
 def _align(x: int) -> int:
     return (x + ALIGN - 1) // ALIGN * ALIGN
 
 
+# ops whose output is the input's bytes under another shape
+VIEW_OPS = {"Flatten", "Reshape", "Squeeze", "Unsqueeze", "Identity"}
+
+
 def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
-                max_memory: int | None = None) -> MemoryPlan:
+                max_memory: int | None = None, alias_views: bool = False) -> MemoryPlan:
     """Greedy offset assignment over the execution order.
+
+    alias_views (mi355x O3): a view op whose input dies there gets the
+    input's offset and no call at all (plan.aliases).
 
     basic:       every activation gets its own region (no reuse).
     cost_aware:  freed regions are reused best-fit; element-wise nodes write
@@ -286,7 +294,17 @@ def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
             if not o or o not in live or o in plan.offsets:
                 continue
             slot = None
-            if strategy == "cost_aware" and node.op_type in INPLACE_OPS:
+            if strategy == "cost_aware" and alias_views and node.op_type in VIEW_OPS and node.inputs:
+                i = node.inputs[0]
+                li = live.get(i)
+                if (li and li.end == idx and not li.is_output and not li.is_input and i in plan.offsets
+                        and i not in reused and sizes[i] == sizes[o]
+                        and g.tensors[i].nbytes == g.tensors[o].nbytes):
+                    slot = plan.offsets[i]
+                    reused.add(i)
+                    plan.inplace[o] = i
+                    plan.aliases[o] = i
+            if slot is None and strategy == "cost_aware" and node.op_type in INPLACE_OPS:
                 allowed = INPLACE_INPUTS.get(node.op_type)
                 for k, i in enumerate(node.inputs):
                     if allowed is not None and k not in allowed:

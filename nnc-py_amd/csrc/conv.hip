@@ -43,6 +43,7 @@ struct ConvArgs {
     int N, Ci, H, W, Co, Ho, Wo, kh, kw, sh, sw, ph, pw;
     int K, Npix, act;
     int tiles_m, tiles_n;
+    int vec_out;  // out (and res) 16-byte aligned: the fixup may store float4
 };
 
 // B operand: gathers input taps for X consecutive output pixels; each thread
@@ -181,7 +182,9 @@ __global__ void __launch_bounds__(256, 2) conv_streamk_k(ConvArgs a, StreamK sk)
 // Grid (chunks, stream-K tiles): workgroup (c, t) finishes chunk c of tile t
 // (256 float4 of the BM x BN tile). Tiles covered by a single workgroup were
 // written by it; shared tiles sum their partials in workgroup order, then
-// bias + act. Each thread handles 4 consecutive pixels of a tile row.
+// bias (+ residual) + act. Each thread handles 4 consecutive pixels of a
+// tile row; partial loads are issued four at a time, and when the 4 pixels
+// are in one image (Ho*Wo % 4 == 0) residual and output move as float4.
 template <class T>
 __global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
     const int t = blockIdx.y;
@@ -194,7 +197,20 @@ __global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
     const int p0 = nt * T::BN + (e4 * 4) % T::BN;
     if (co >= a.Co || p0 >= a.Npix) return;
     float4 v = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g0, first_slot))[e4];
-    for (int g = g0 + 1; g <= g1; ++g) {
+    int g = g0 + 1;
+    for (; g + 3 <= g1; g += 4) {
+        float4 p[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g + q, 0))[e4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v.x += p[q].x;
+            v.y += p[q].y;
+            v.z += p[q].z;
+            v.w += p[q].w;
+        }
+    }
+    for (; g <= g1; ++g) {
         const float4 p = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g, 0))[e4];
         v.x += p.x;
         v.y += p.y;
@@ -203,16 +219,31 @@ __global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
     }
     const int hw = a.Ho * a.Wo;
     const float b = a.bias ? a.bias[co] : 0.f;
+    const int n = p0 / hw;
+    const int64_t o = ((int64_t)n * a.Co + co) * hw + (p0 - n * hw);
+    if (a.vec_out && (hw & 3) == 0 && p0 + 3 < a.Npix) {
+        float4 x = make_float4(v.x + b, v.y + b, v.z + b, v.w + b);
+        if (a.res) {
+            const float4 r = *reinterpret_cast<const float4*>(a.res + o);
+            x.x += r.x;
+            x.y += r.y;
+            x.z += r.z;
+            x.w += r.w;
+        }
+        *reinterpret_cast<float4*>(a.out + o) =
+            make_float4(activate(x.x, a.act), activate(x.y, a.act), activate(x.z, a.act), activate(x.w, a.act));
+        return;
+    }
     const float vals[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int pix = p0 + q;
         if (pix >= a.Npix) break;
-        const int n = pix / hw;
-        const int64_t o = ((int64_t)n * a.Co + co) * hw + (pix - n * hw);
-        float v = vals[q] + b;
-        if (a.res) v += a.res[o];
-        a.out[o] = activate(v, a.act);
+        const int nq = pix / hw;
+        const int64_t oq = ((int64_t)nq * a.Co + co) * hw + (pix - nq * hw);
+        float x = vals[q] + b;
+        if (a.res) x += a.res[oq];
+        a.out[oq] = activate(x, a.act);
     }
 }
 
@@ -334,6 +365,7 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
         return fail(NNC_HIP_EUNSUPP, name, "input or weights of 2 GiB or more");
     a.K = (int)K;
     a.Npix = (int)npix;
+    a.vec_out = aligned16(a.out) && (!a.res || aligned16(a.res));
     if (a.N == 0 || a.Co == 0 || a.Ho <= 0 || a.Wo <= 0) return;
     const bool avec = (a.K % 4 == 0) && aligned16(a.w);
     // Tile choice (measured on ResNet-18 layers at batch 1 and 32): big tiles

@@ -2,7 +2,8 @@
 //
 // One thread per output element, lanes along the output row so stores
 // coalesce; each window is read straight from HBM/L2 (a 3x3 s2 window
-// re-reads ~2.25x the input, served by L2). The window is clamped to the
+// re-reads ~2.25x the input, served by L2). Global average pooling has its
+// own kernel that stages whole planes through LDS with coalesced loads. The window is clamped to the
 // input like the reference, scanned in the same h-major order with the same
 // comparisons / float additions, so both kernels are bit-exact with it:
 //   MaxPool: start at -3.402823e38f, take v when no element was seen yet or
@@ -20,22 +21,23 @@ struct PoolArgs {
     int NC, H, W, Ho, Wo, kh, kw, sh, sw, ph, pw;
 };
 
+// grid (ceil(Ho*Wo / 256), min(NC, 65535)): blockIdx.y strides over the
+// N*C planes, x over the output positions of a plane (32-bit index math).
 template <bool MAX>
 __global__ void __launch_bounds__(256) pool2d_k(PoolArgs a) {
-    const int64_t total = (int64_t)a.NC * a.Ho * a.Wo;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        const int ow = (int)(e % a.Wo);
-        const int64_t t = e / a.Wo;
-        const int oh = (int)(t % a.Ho);
-        const int64_t nc = t / a.Ho;
-        int h0 = oh * a.sh - a.ph, h1 = h0 + a.kh;
-        int w0 = ow * a.sw - a.pw, w1 = w0 + a.kw;
-        if (h0 < 0) h0 = 0;
-        if (w0 < 0) w0 = 0;
-        if (h1 > a.H) h1 = a.H;
-        if (w1 > a.W) w1 = a.W;
-        const float* plane = a.in + nc * a.H * a.W;
+    const int hw_out = a.Ho * a.Wo;
+    const int pos = blockIdx.x * 256 + threadIdx.x;
+    if (pos >= hw_out) return;
+    const int oh = pos / a.Wo, ow = pos - oh * a.Wo;
+    int h0 = oh * a.sh - a.ph, h1 = h0 + a.kh;
+    int w0 = ow * a.sw - a.pw, w1 = w0 + a.kw;
+    if (h0 < 0) h0 = 0;
+    if (w0 < 0) w0 = 0;
+    if (h1 > a.H) h1 = a.H;
+    if (w1 > a.W) w1 = a.W;
+    for (int nc = blockIdx.y; nc < a.NC; nc += gridDim.y) {
+        const float* plane = a.in + (int64_t)nc * a.H * a.W;
+        float* o = a.out + (int64_t)nc * hw_out + pos;
         if (MAX) {
             float best = -3.402823e38f;
             bool seen = false;
@@ -47,7 +49,7 @@ __global__ void __launch_bounds__(256) pool2d_k(PoolArgs a) {
                         seen = true;
                     }
                 }
-            a.out[e] = best;
+            *o = best;
         } else {
             float acc = 0.0f;
             int cnt = 0;
@@ -56,8 +58,49 @@ __global__ void __launch_bounds__(256) pool2d_k(PoolArgs a) {
                     acc += plane[h * a.W + w];
                     ++cnt;
                 }
-            a.out[e] = cnt > 0 ? acc / (float)cnt : 0.0f;
+            *o = cnt > 0 ? acc / (float)cnt : 0.0f;
         }
+    }
+}
+
+// Global average pool (window = whole plane, one output per plane): the
+// workgroup's `planes` consecutive planes (at most 64) are one contiguous
+// block, read with coalesced loads (16-byte when aligned) into LDS rows
+// padded by one float; then thread t sums plane t sequentially in the
+// reference's h-major order (bit-exact).
+__global__ void __launch_bounds__(256) global_avgpool_k(const float* __restrict__ in, float* __restrict__ out,
+                                                        int NC, int HW, int planes_per_wg) {
+    extern __shared__ float tile[];
+    const int p0 = blockIdx.x * planes_per_wg;
+    const int planes = min(planes_per_wg, NC - p0);
+    const int n = planes * HW;
+    const float* src = in + (int64_t)p0 * HW;
+    const int ld = HW + 1;
+    int done = 0;
+    if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+        const int n4 = n / 4;
+        for (int i = threadIdx.x; i < n4; i += 256) {
+            const float4 v = reinterpret_cast<const float4*>(src)[i];
+            const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int e = 4 * i + q;
+                const int pl = e / HW;
+                tile[pl * ld + (e - pl * HW)] = vals[q];
+            }
+        }
+        done = n4 * 4;
+    }
+    for (int e = done + threadIdx.x; e < n; e += 256) {
+        const int pl = e / HW;
+        tile[pl * ld + (e - pl * HW)] = src[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < planes) {
+        const float* row = tile + threadIdx.x * ld;
+        float acc = 0.0f;
+        for (int i = 0; i < HW; ++i) acc += row[i];
+        out[p0 + threadIdx.x] = acc / (float)HW;
     }
 }
 
@@ -95,7 +138,22 @@ static void pool_entry(const char* name, Tensor* in, Tensor* out, int kh, int kw
                -3.402823e38f);
     }
     set_work(0.0, 4.0 * ((double)numel(in) + (double)nc * a.Ho * a.Wo));
-    launch(name, pool2d_k<MAX>, dim3(grid_for(nc * a.Ho * a.Wo, 1)), dim3(256), 0, a);
+    const int64_t hw = (int64_t)a.H * a.W;
+    if (!MAX && a.Ho == 1 && a.Wo == 1 && kh >= a.H && kw >= a.W && ph == 0 && pw == 0 && hw > 0 &&
+        hw <= 4096) {
+        // global pool: every output is the mean of one whole plane; as many
+        // planes per workgroup as fit 64 KB of LDS (at most 64)
+        int planes = (int)(16384 / (hw + 1));
+        planes = planes < 1 ? 1 : (planes > 64 ? 64 : planes);
+        const size_t lds = (size_t)planes * (hw + 1) * sizeof(float);
+        launch("nnc_avgpool2d_global", global_avgpool_k, dim3((unsigned)ceil_div(nc, planes)), dim3(256), lds,
+               a.in, a.out, a.NC, (int)hw, planes);
+        return;
+    }
+    if ((int64_t)a.Ho * a.Wo >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "output plane too large");
+    const unsigned gy = (unsigned)(nc < 65535 ? nc : 65535);
+    if (nc > 0 && a.Ho > 0 && a.Wo > 0)
+        launch(name, pool2d_k<MAX>, dim3((unsigned)ceil_div((int64_t)a.Ho * a.Wo, 256), gy), dim3(256), 0, a);
 }
 
 }  // namespace nnc
