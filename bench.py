@@ -239,6 +239,113 @@ def measure_traffic(kernel: str, batch: int) -> dict | None:
     return out
 
 
+def _op_roofline(runtime, fn, reps: int = 10, warmup: int = 3) -> list[dict]:
+    """Per-kernel table of `fn()` (one or more nnc_* calls) over `reps` calls."""
+    for _ in range(warmup):
+        fn()
+    runtime.sync()
+    runtime.profile_reset()
+    runtime.profile_enable(True)
+    for _ in range(reps):
+        fn()
+    runtime.sync()
+    table = runtime.profile_table()
+    runtime.profile_enable(False)
+    rows = []
+    for r in table:
+        if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma")):
+            achieved, unit, peak = r["flops"] / (r["ms"] * 1e-3) / 1e12, "TFLOP/s", PEAK_FP32_MFMA_TF
+        else:
+            achieved, unit, peak = (r["bytes"] / (r["ms"] * 1e-3) / 1e9 if r["ms"] > 0 else 0.0), "GB/s", PEAK_HBM_GBS
+        rows.append({"kernel": r["name"], "launches": r["launches"] // reps, "avg_us": round(r["ms"] / r["launches"] * 1e3, 2),
+                     "achieved": round(achieved, 2), "unit": unit, "frac": round(achieved / peak, 4)})
+    return rows
+
+
+def run_suite() -> int:
+    """The other workloads, one JSON line per item: GEMM sweep (Gemm
+    M=N=K 1024/2048/4096 with bias, as emitted (transB=0) and after O3 weight
+    packing (gemm_nt); batched MatMul [64,128,64]x[64,64,128]; vector MatMul
+    [1,4096]x[4096,4096]), the bandwidth-bound ops at their workload sizes,
+    and the 2-layer transformer encoder (B8 S128 D256 H4 FFN1024) as one
+    hipGraph per step. Per-kernel achieved rates are algorithmic work over
+    the library's per-launch hipEvent times."""
+    load_package()
+    from nnc_py_amd import abi, runtime
+    from nnc_py_amd.compiler import Executor, build_program, zoo
+    lib = runtime.init(0)
+    rng = np.random.default_rng(0)
+    keep = []
+
+    def dev(arr, shape=None):
+        """Device copy of `arr`; returns a Tensor* argument (kept alive in `keep`)."""
+        buf = runtime.DeviceBuffer.from_array(np.ascontiguousarray(arr))
+        t = buf.tensor(shape)
+        keep.append((buf, t))
+        return ctypes.pointer(t[0])
+
+    def emit(suite, workload, rows, **extra):
+        print(json.dumps({"suite": suite, "workload": workload, **extra, "kernels": rows}), flush=True)
+
+    for n in (1024, 2048, 4096):
+        a, b, c = (rng.uniform(-1, 1, s).astype(np.float32) for s in ((n, n), (n, n), (n,)))
+        ta, tb, tc, to = dev(a), dev(b), dev(c), dev(np.zeros((n, n), np.float32))
+        emit("gemm", f"Gemm {n}x{n}x{n} + bias[N], transB=0",
+             _op_roofline(runtime, lambda: lib.nnc_gemm(ta, tb, tc, to, 1.0, 1.0, 0, 0)))
+        tbt = dev(b.T.copy())
+        emit("gemm", f"Gemm_nt {n}x{n}x{n} + bias[N] (O3 packed B)",
+             _op_roofline(runtime, lambda: lib.nnc_gemm_nt(ta, tbt, tc, to, 1.0, 1.0)))
+        keep.clear()
+    ta, tb = dev(rng.uniform(-1, 1, (64, 128, 64)).astype(np.float32)), dev(rng.uniform(-1, 1, (64, 64, 128)).astype(np.float32))
+    to = dev(np.zeros((64, 128, 128), np.float32))
+    emit("gemm", "MatMul [64,128,64]x[64,64,128]", _op_roofline(runtime, lambda: lib.nnc_matmul(ta, tb, to)))
+    tv, tm = dev(rng.uniform(-1, 1, (1, 4096)).astype(np.float32)), dev(rng.uniform(-1, 1, (4096, 4096)).astype(np.float32))
+    to = dev(np.zeros((1, 4096), np.float32))
+    emit("gemm", "MatMul [1,4096]x[4096,4096]", _op_roofline(runtime, lambda: lib.nnc_matmul(tv, tm, to)))
+    keep.clear()
+
+    shape = (32, 256, 56, 56)
+    tx, ty = dev(rng.standard_normal(shape).astype(np.float32)), dev(rng.standard_normal(shape).astype(np.float32))
+    to = dev(np.zeros(shape, np.float32))
+    for op in ("nnc_add", "nnc_mul", "nnc_add_relu"):
+        emit("bandwidth", f"{op} [32,256,56,56]", _op_roofline(runtime, lambda op=op: getattr(lib, op)(tx, ty, to)))
+    for op in ("nnc_relu", "nnc_sigmoid", "nnc_tanh"):
+        emit("bandwidth", f"{op} [32,256,56,56]", _op_roofline(runtime, lambda op=op: getattr(lib, op)(tx, to)))
+    emit("bandwidth", "nnc_clip(-6,6) [32,256,56,56]", _op_roofline(runtime, lambda: lib.nnc_clip(tx, to, -6.0, 6.0)))
+    tcat = dev(np.zeros((32, 512, 56, 56), np.float32))
+    pair = (abi.TP * 2)(tx, ty)
+    emit("bandwidth", "nnc_concat axis 1: 2 x [32,256,56,56]",
+         _op_roofline(runtime, lambda: lib.nnc_concat(ctypes.cast(pair, abi.TPP), tcat, 2, 1)))
+    emit("bandwidth", "nnc_split axis 1: [32,512,56,56] -> 2",
+         _op_roofline(runtime, lambda: lib.nnc_split(tcat, ctypes.cast(pair, abi.TPP), 2, 1)))
+    keep.clear()
+    ts, tso = dev(rng.standard_normal((4096, 1024)).astype(np.float32)), dev(np.zeros((4096, 1024), np.float32))
+    emit("bandwidth", "nnc_softmax [4096,1024] axis -1", _op_roofline(runtime, lambda: lib.nnc_softmax(ts, tso, -1)))
+    tl, tg, tb0 = dev(rng.standard_normal((8192, 768)).astype(np.float32)), dev(np.ones(768, np.float32)), dev(np.zeros(768, np.float32))
+    tlo = dev(np.zeros((8192, 768), np.float32))
+    emit("bandwidth", "nnc_layernorm [8192,768] eps 1e-5",
+         _op_roofline(runtime, lambda: lib.nnc_layernorm(tl, tg, tb0, tlo, -1, 1e-5)))
+    r = rng.standard_normal((32, 512, 28, 28)).astype(np.float32)
+    tr, tro = dev(r, (32, 512, 784)), dev(np.zeros((32, 512, 1), np.float32))
+    for op in ("nnc_reducemean", "nnc_reducesum"):
+        emit("bandwidth", f"{op} axes (2,3) of [32,512,28,28]",
+             _op_roofline(runtime, lambda op=op: getattr(lib, op)(tr, tro, 2, 1)))
+    keep.clear()
+
+    prog = build_program(zoo.transformer_encoder(seed=1), opt_level=3)
+    ex = Executor(prog, device=True)
+    ex.set_input("input", (rng.standard_normal((8, 128, 256)) * 0.02).astype(np.float32))
+    steps = 50
+    dt = timed_steps(ex, steps, 10, True, runtime)
+    ms = dt / steps * 1e3
+    flops = zoo.transformer_flops()
+    emit("transformer", "encoder 2 layers, B8 S128 D256 H4 FFN1024, O3, hipGraph", kernel_table(ex, runtime, 5),
+         ms_per_step=round(ms, 4), gflops_per_s=round(flops / (ms * 1e-3) / 1e9, 1),
+         mfma_frac_whole_step=round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TF, 4))
+    ex.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -252,9 +359,17 @@ def main() -> int:
     ap.add_argument("--no-b1", action="store_true", help="measure batch 32 only (profiling runs)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--suite", action="store_true",
+                    help="instead of the ResNet-18 line: GEMM sweep, bandwidth ops and transformer encoder, "
+                         "one JSON line each")
     args = ap.parse_args()
     if args.pmc_child:
         return pmc_child(args)
+    if args.suite:
+        if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+            print("bench.py --suite measures one GPU", file=sys.stderr)
+            return 2
+        return run_suite()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build runs the nnc program on a single MI355X "
