@@ -22,7 +22,7 @@ import numpy as np
 from .. import abi
 from .ir import Graph, Node
 from .lower import Call, lower
-from .passes import (MemoryPlan, check_plan, eliminate_dead_code, eliminate_identity, fuse_patterns, fuse_residual,
+from .passes import (MemoryPlan, check_plan, eliminate_dead_code, eliminate_identity, fuse_matmul_bias, fuse_patterns, fuse_residual,
                      plan_memory, prepack_lowering)
 
 
@@ -50,6 +50,7 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
         fuse_patterns(graph)
         if RESIDUAL_FUSION:
             fuse_residual(graph)
+        fuse_matmul_bias(graph)
         prepack_lowering(graph)
     order = graph.topological_sort()
     strategy = memory_strategy or ("basic" if opt_level == 0 else "cost_aware")

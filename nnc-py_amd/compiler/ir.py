@@ -26,6 +26,8 @@ FUSED = {
     "FusedAddSigmoid": ("Add", "Sigmoid"),
     "FusedMatMulRelu": ("MatMul", "Relu"),
     "FusedConvAddRelu": ("Conv", "Add", "Relu"),
+    "FusedMatMulBias": ("MatMul", "Add"),
+    "FusedMatMulBiasRelu": ("MatMul", "Add", "Relu"),
 }
 
 

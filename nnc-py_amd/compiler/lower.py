@@ -118,11 +118,25 @@ _GENERIC = {
 _CAST = {"float32": 0, "float16": 1, "int32": 2, "int8": 3, "uint8": 4, "bool": 5, "int64": 6}
 
 
+def _matmul_bias_call(g: Graph, node: Node) -> Call:
+    a, w, bias = node.inputs
+    out = node.outputs[0]
+    if node.op_type == "FusedMatMulBiasRelu":
+        return Call("nnc_matmul_relu", [_t(a), _t(w), _t(bias), _t(out)], node.name)
+    sa = g.tensors[a].shape
+    m = int(np.prod(sa[:-1]))
+    n, k = g.tensors[w].shape  # packed [N, K]
+    return Call("nnc_gemm_nt", [("tv", a, (m, k)), _t(w), _t(bias), ("tv", out, (m, n)), ("f", 1.0), ("f", 1.0)],
+                node.name)
+
+
 def lower_node(g: Graph, node: Node) -> Call:
     op = node.op_type
     ins, outs = node.inputs, node.outputs
     if op in ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu"):
         return _conv_call(g, node)
+    if op in ("FusedMatMulBias", "FusedMatMulBiasRelu"):
+        return _matmul_bias_call(g, node)
     if op == "Gemm":
         args = [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0]),
                 ("f", float(node.attrs.get("alpha", 1.0))), ("f", float(node.attrs.get("beta", 1.0)))]

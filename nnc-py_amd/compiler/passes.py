@@ -146,6 +146,48 @@ def fuse_residual(g: Graph) -> int:
     return fused
 
 
+def fuse_matmul_bias(g: Graph) -> int:
+    """mi355x target, O3: MatMul(activation, constant W [K, N]) whose only
+    consumer adds a constant 1-D bias [N] becomes one GEMM with the bias in
+    its epilogue: FusedMatMulBias (lowered to nnc_gemm_nt on [M, K] / [M, N]
+    views, W packed to [N, K] at compile time) or, when the Add was fused
+    with a Relu, FusedMatMulBiasRelu (lowered to nnc_matmul_relu with the
+    bias). The sum is the same fp32 add of the bias to the product."""
+    fused = 0
+    for mm in list(g.nodes):
+        if mm.op_type != "MatMul" or len(mm.inputs) != 2 or mm.outputs[0] in g.outputs:
+            continue
+        a, w = mm.inputs
+        wt = g.tensors[w]
+        if not wt.is_constant or len(wt.shape) != 2 or len(g.tensors[a].shape) < 2:
+            continue
+        mid = mm.outputs[0]
+        users = g.consumers(mid)
+        if len(users) != 1 or users[0].op_type not in ("Add", "FusedAddRelu") or len(users[0].inputs) != 2:
+            continue
+        add = users[0]
+        bias = add.inputs[1] if add.inputs[0] == mid else add.inputs[0]
+        bt = g.tensors[bias]
+        n = wt.shape[1]
+        if bias == mid or not bt.is_constant or tuple(bt.shape) != (n,):
+            continue
+        relu = add.op_type == "FusedAddRelu"
+        if not relu and len(g.consumers(w)) == 1:
+            wt.data = np.ascontiguousarray(wt.data.T)
+            wt.shape = tuple(wt.data.shape)
+            mm.attrs["transB"] = 1
+        elif not relu:
+            continue  # a shared weight keeps its layout; leave the pair unfused
+        mm.op_type = "FusedMatMulBiasRelu" if relu else "FusedMatMulBias"
+        mm.inputs = [a, w, bias]
+        mm.outputs = list(add.outputs)
+        mm.metadata["fused_from"] = [mm.name, add.name]
+        g.nodes.remove(add)
+        g.tensors.pop(mid, None)
+        fused += 1
+    return fused
+
+
 def prepack_lowering(g: Graph) -> None:
     """Conv kernel kind and constant Gemm B packing
     (passes/prepack_lowering.py:48-118)."""

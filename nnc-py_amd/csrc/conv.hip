@@ -268,7 +268,7 @@ static void launch_conv_t(ConvArgs& a, const char* entry) {
     // K == 0 (no input channels) still runs one empty slice so the epilogue
     // writes act(bias)
     const int iters = a.K > 0 ? (int)ceil_div(a.K, T::BK) : 1;
-    const StreamK sk = plan_streamk(a.tiles_m * a.tiles_n, iters, slots);
+    const StreamK sk = plan_streamk(a.tiles_m * a.tiles_n, iters, slots, fixup_slices<T>());
     if (sk.G < 1) return;
     float* ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
     if (!ws) return fail(NNC_HIP_ENOMEM, entry, "no workspace for stream-K partials");

@@ -187,12 +187,33 @@ __global__ void __launch_bounds__(256) gemv_xc_k(const float* a, int64_t a_strid
     }
 }
 
+// Sums the K-split partials of 64 columns per workgroup: each wave adds a
+// contiguous quarter of the splits in order (lanes on consecutive columns,
+// loads issued eight at a time), then the four quarter sums are added in
+// wave order: a fixed summation order, whatever the timing.
 __global__ void __launch_bounds__(256) gemv_reduce_k(GemmArgs g) {
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= g.N) return;
+    __shared__ float part[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane;
+    const int q = (g.splits + 3) / 4;
+    const int s0 = wave * q, s1 = min(g.splits, s0 + q);
     float v = 0.f;
-    for (int s = 0; s < g.splits; ++s) v += g.ws[(int64_t)s * g.N + j];
-    g.out[j] = gemm_finish(g, 0, j, v);
+    if (j < g.N) {
+        const float* col = g.ws + j;
+        int s = s0;
+        for (; s + 8 <= s1; s += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = col[(int64_t)(s + u) * g.N];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
+        }
+        for (; s < s1; ++s) v += col[(int64_t)s * g.N];
+    }
+    part[wave][lane] = v;
+    __syncthreads();
+    if (wave == 0 && j < g.N)
+        g.out[j] = gemm_finish(g, 0, j, ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -248,7 +269,8 @@ static void launch_mfma(GemmArgs& g, int batches, const char* name) {
     g.tiles_n = (int)ceil_div(g.N, T::BN);
     if ((int64_t)g.tiles_m * g.tiles_n * batches >= (1 << 30))
         return fail(NNC_HIP_EUNSUPP, name, "too many output tiles");
-    const StreamK sk = plan_streamk(g.tiles_m * g.tiles_n * batches, (int)ceil_div(g.K, T::BK), slots);
+    const StreamK sk = plan_streamk(g.tiles_m * g.tiles_n * batches, (int)ceil_div(g.K, T::BK), slots,
+                                    fixup_slices<T>());
     if (sk.G < 1) return;
     g.ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
     if (!g.ws) return fail(NNC_HIP_ENOMEM, name, "no workspace for stream-K partials");
@@ -345,7 +367,7 @@ static void gemm_run(const GemmProblem& p, const char* name) {
             launch("gemv_xc_s1", gemv_xc_k<false>, dim3(col_blocks, splits), dim3(256), 0, p.A, a_stride,
                    p.B, p.ldb, ws, p.N, p.K, k_per);
         set_work(0.0, 4.0 * (double)p.N * (splits + 1));
-        launch("gemv_reduce", gemv_reduce_k, dim3((unsigned)ceil_div(p.N, 256)), dim3(256), 0, g);
+        launch("gemv_reduce", gemv_reduce_k, dim3((unsigned)ceil_div(p.N, 64)), dim3(256), 0, g);
         return;
     }
     if (p.batches == 1 && p.a_kc && p.b_kc && (p.M == 1 || p.N == 1 || (int64_t)p.M * p.N <= 64)) {

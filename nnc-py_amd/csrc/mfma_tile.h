@@ -440,19 +440,25 @@ __host__ __device__ inline bool tile_partials(const StreamK& sk, int t, int& g0,
 }
 
 // Host: choose the grid and the stream-K region for `tiles` tiles of
-// `iters` slices on `slots` resident workgroups.
+// `iters` slices on `slots` resident workgroups. `fixup_slices` is what
+// finishing the shared tiles costs, in slice times of this tile shape (the
+// fixup kernel's launch and partial traffic).
 //  - few slices per tile (< 4): splitting costs more than the tail; plain
 //    round-robin over min(tiles, slots) workgroups
-//  - tiles >= slots with the last round empty or >= 80% full: round-robin
-//  - tiles >= slots otherwise: all but the last full round plus the partial
-//    round go to stream-K, so every workgroup ends at the same time
-//  - tiles < slots: everything is stream-K, each workgroup taking at least
-//    4 slices (fewer workgroups for short problems)
-inline StreamK plan_streamk(int tiles, int iters, int slots) {
+//  - otherwise round-robin (every tile whole) unless stream-K's estimated
+//    time, ceil(tiles * iters / G) + fixup_slices, is shorter than
+//    round-robin's ceil(tiles / slots) * iters
+//  - stream-K with tiles >= slots: all but the last full round plus the
+//    partial round are split, so every workgroup ends at the same time
+//  - stream-K with tiles < slots: everything is split, each workgroup
+//    taking at least 4 slices (fewer workgroups for short problems)
+inline StreamK plan_streamk(int tiles, int iters, int slots, int fixup_slices) {
     StreamK sk{};
     sk.tiles = tiles;
     sk.iters = iters;
     const int kMinSplitIters = 4, kMinRangeIters = 4;
+    const int64_t total = (int64_t)tiles * iters;
+    const int64_t dp_time = (int64_t)((tiles + slots - 1) / slots) * iters;
     if (iters < kMinSplitIters) {
         sk.G = tiles < slots ? tiles : slots;
         sk.sk_tiles = 0;
@@ -461,20 +467,30 @@ inline StreamK plan_streamk(int tiles, int iters, int slots) {
     if (tiles >= slots) {
         const int rem = tiles % slots;
         sk.G = slots;
-        if (rem == 0 || (int64_t)rem * 5 >= (int64_t)slots * 4) {
-            sk.sk_tiles = 0;
-        } else {
-            sk.sk_tiles = tiles - (tiles / slots - 1) * slots;
-        }
+        const int64_t sk_time = (total + slots - 1) / slots + fixup_slices;
+        sk.sk_tiles = (rem == 0 || sk_time >= dp_time) ? 0 : tiles - (tiles / slots - 1) * slots;
         return sk;
     }
-    const int64_t total = (int64_t)tiles * iters;
     int64_t G = total / kMinRangeIters;
     if (G > slots) G = slots;
     if (G < tiles) G = tiles;
+    const int64_t sk_time = (total + G - 1) / G + fixup_slices;
+    if (sk_time >= dp_time) {
+        sk.G = tiles;
+        sk.sk_tiles = 0;
+        return sk;
+    }
     sk.G = (int)G;
     sk.sk_tiles = tiles;
     return sk;
+}
+
+// Fixup cost in slice times: about 13 us for 128x128 tiles (~4 slices of
+// 3.4 us at two workgroups per CU), scaled by tile area for smaller tiles,
+// whose slices are shorter.
+template <class T>
+constexpr int fixup_slices() {
+    return 4 * (128 * 128) / (T::BM * T::BN);
 }
 
 // Persistent-grid size: workgroups of `kernel` resident on the device at once.

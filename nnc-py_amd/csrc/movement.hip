@@ -87,15 +87,29 @@ __global__ void __launch_bounds__(256) transpose2d_k(const float* in, float* out
 // ---------------------------------------------------------------------------
 // concat / split: strided 2-D copies [outer][slab] <-> [outer][row] at column
 // ---------------------------------------------------------------------------
+// grid (ceil(slab / 256), rows): one element per thread, 32-bit index
+// within a row, rows strided by grid.y; no per-element division
 template <typename E>
 __global__ void __launch_bounds__(256) slab_copy_k(const E* src, int64_t src_row, E* dst,
-                                                   int64_t dst_row, int64_t outer, int64_t slab) {
-    const int64_t total = outer * slab;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        const int64_t o = e / slab, i = e - o * slab;
-        dst[o * dst_row + i] = src[o * src_row + i];
+                                                   int64_t dst_row, int64_t outer, uint32_t slab) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= slab) return;
+    for (int64_t o = blockIdx.y; o < outer; o += gridDim.y) dst[o * dst_row + i] = src[o * src_row + i];
+}
+
+template <typename E>
+static void slab_launch(const char* name, const E* src, int64_t src_row, E* dst, int64_t dst_row, int64_t outer,
+                        int64_t slab) {
+    if (slab >= ((int64_t)1 << 32) - 256) {
+        // rows longer than 2^32 elements: one launch per 2^31-element chunk
+        const int64_t chunk = (int64_t)1 << 31;
+        for (int64_t c = 0; c < slab; c += chunk)
+            slab_launch(name, src + c, src_row, dst + c, dst_row, outer, slab - c < chunk ? slab - c : chunk);
+        return;
     }
+    const int64_t gy = outer < 65535 ? outer : 65535;
+    launch(name, slab_copy_k<E>, dim3((unsigned)ceil_div(slab, 256), (unsigned)gy), dim3(256), 0, src, src_row,
+           dst, dst_row, outer, (uint32_t)slab);
 }
 
 template <typename E>
@@ -107,12 +121,10 @@ static void slab_copy(const char* name, const void* src, int64_t src_row, void* 
     const int64_t per16 = 16 / (int64_t)sizeof(E);
     if (aligned16(src) && aligned16(dst) && slab % per16 == 0 && src_row % per16 == 0 &&
         dst_row % per16 == 0) {
-        launch(name, slab_copy_k<uint4>, dim3(grid_for(outer * slab / per16, 1)), dim3(256), 0,
-               (const uint4*)src, src_row / per16, (uint4*)dst, dst_row / per16, outer, slab / per16);
+        slab_launch(name, (const uint4*)src, src_row / per16, (uint4*)dst, dst_row / per16, outer, slab / per16);
         return;
     }
-    launch(name, slab_copy_k<E>, dim3(grid_for(outer * slab, 1)), dim3(256), 0, (const E*)src, src_row,
-           (E*)dst, dst_row, outer, slab);
+    slab_launch(name, (const E*)src, src_row, (E*)dst, dst_row, outer, slab);
 }
 
 // ---------------------------------------------------------------------------

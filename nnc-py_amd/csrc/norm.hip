@@ -127,7 +127,7 @@ __global__ void __launch_bounds__(256) softmax_cols_k(const float* in, float* ou
 // ---------------------------------------------------------------------------
 // layernorm over a contiguous span of D*inner floats per outer row
 // ---------------------------------------------------------------------------
-template <int PER>
+template <int PER, bool INNER1>
 __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, const float* g,
                                                            const float* b, float* out, int64_t rows,
                                                            int span, int inner, float eps) {
@@ -163,12 +163,27 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
             if (idx < s4) {
                 const int e = idx * 4;
                 float r[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+                float gv[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (INNER1) {
+                    // scale/bias indexed by the element itself: 16-byte loads
+                    if (g) {
+                        const float4 t = reinterpret_cast<const float4*>(g)[idx];
+                        gv[0] = t.x, gv[1] = t.y, gv[2] = t.z, gv[3] = t.w;
+                    }
+                    if (b) {
+                        const float4 t = reinterpret_cast<const float4*>(b)[idx];
+                        bv[0] = t.x, bv[1] = t.y, bv[2] = t.z, bv[3] = t.w;
+                    }
+                } else {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int i = (e + c) / inner;
-                    const float gi = g ? g[i] : 1.0f, bi = b ? b[i] : 0.0f;
-                    r[c] = gi * ((r[c] - mean) / sd) + bi;
+                    for (int c = 0; c < 4; ++c) {
+                        const int i = (e + c) / inner;
+                        if (g) gv[c] = g[i];
+                        if (b) bv[c] = b[i];
+                    }
                 }
+#pragma unroll
+                for (int c = 0; c < 4; ++c) r[c] = gv[c] * ((r[c] - mean) / sd) + bv[c];
                 y[idx] = make_float4(r[0], r[1], r[2], r[3]);
             }
         }
@@ -233,6 +248,39 @@ __global__ void __launch_bounds__(256) reduce_rows_k(const float* in, float* out
     }
 }
 
+// contiguous rows of len % 4 == 0 (16-byte aligned), up to 256*PER floats:
+// the row is loaded into registers with 16-byte loads first (all loads in
+// flight at once), then Kahan-summed per lane and combined by shuffles
+template <bool MEAN, int PER>
+__global__ void __launch_bounds__(256) reduce_rows_v4_k(const float* in, float* out, int64_t rows, int len) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wstride = (int64_t)gridDim.x * 4;
+    const int l4 = len / 4;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += wstride) {
+        const float4* x = reinterpret_cast<const float4*>(in + row * len);
+        float4 v[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int idx = lane + 64 * q;
+            v[q] = idx < l4 ? x[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float s = 0.f, c = 0.f;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const float e[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float y = e[u] - c;
+                const float t = s + y;
+                c = (t - s) - y;
+                s = t;
+            }
+        }
+        s = wave_sum(s);
+        if (lane == 0) out[row] = MEAN ? s / (float)len : s;
+    }
+}
+
 // strided axis: thread per (outer, inner), the reference's sequential Kahan sum
 template <bool MEAN>
 __global__ void __launch_bounds__(256) reduce_cols_k(const float* in, float* out, int64_t outer,
@@ -275,8 +323,13 @@ static void softmax_v4(const float* x, float* y, int64_t rows, int dim, const ch
 template <int PER>
 static void layernorm_v4(const float* x, const float* g, const float* b, float* y, int64_t rows,
                          int span, int inner, float eps, const char* name) {
-    launch(name, layernorm_rows_v4_k<PER>, dim3(grid_for(rows, 4, 1)), dim3(256), 0, x, g, b, y, rows,
-           span, inner, eps);
+    // inner == 1 with 16-byte aligned scale/bias: vector loads of those too
+    if (inner == 1 && (!g || aligned16(g)) && (!b || aligned16(b)))
+        launch(name, layernorm_rows_v4_k<PER, true>, dim3(grid_for(rows, 4, 1)), dim3(256), 0, x, g, b, y,
+               rows, span, inner, eps);
+    else
+        launch(name, layernorm_rows_v4_k<PER, false>, dim3(grid_for(rows, 4, 1)), dim3(256), 0, x, g, b, y,
+               rows, span, inner, eps);
 }
 
 }  // namespace nnc
@@ -348,8 +401,23 @@ static void reduce_entry(const char* name, Tensor* in, Tensor* out, int axis, bo
     float* y = (float*)out->data;
     set_work(0.0, 4.0 * (double)(outer * len * inner + outer * inner));
     if (inner == 1) {
-        if (mean) launch(name, reduce_rows_k<true>, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, len);
-        else launch(name, reduce_rows_k<false>, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, len);
+        const dim3 grid(grid_for(outer, 4, 1));
+        if (len % 4 == 0 && len <= 4096 && aligned16(x)) {
+#define NNC_REDUCE_V4(PER)                                                                             \
+    if (len <= 256 * PER) {                                                                            \
+        if (mean) launch(name, reduce_rows_v4_k<true, PER>, grid, dim3(256), 0, x, y, outer, (int)len);  \
+        else launch(name, reduce_rows_v4_k<false, PER>, grid, dim3(256), 0, x, y, outer, (int)len);      \
+        return;                                                                                        \
+    }
+            NNC_REDUCE_V4(1)
+            NNC_REDUCE_V4(2)
+            NNC_REDUCE_V4(4)
+            NNC_REDUCE_V4(8)
+            NNC_REDUCE_V4(16)
+#undef NNC_REDUCE_V4
+        }
+        if (mean) launch(name, reduce_rows_k<true>, grid, dim3(256), 0, x, y, outer, len);
+        else launch(name, reduce_rows_k<false>, grid, dim3(256), 0, x, y, outer, len);
         return;
     }
     const dim3 g(grid_for(outer * inner, 1));

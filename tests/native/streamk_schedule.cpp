@@ -10,8 +10,8 @@
 
 using namespace nnc;
 
-static int check(int tiles, int iters, int slots) {
-    const StreamK sk = plan_streamk(tiles, iters, slots);
+static int check(int tiles, int iters, int slots, int fixup) {
+    const StreamK sk = plan_streamk(tiles, iters, slots, fixup);
     if (sk.G < 1 || sk.G > slots || sk.sk_tiles < 0 || sk.sk_tiles > tiles) return 1;
     std::vector<int> cover((size_t)tiles * iters, 0);
     // per tile: workgroups that wrote a partial, with their slot
@@ -60,14 +60,15 @@ int main() {
     const int slots_list[] = {1, 7, 64, 256, 512, 768};
     for (int slots : slots_list)
         for (int tiles = 1; tiles <= 1200; tiles += (tiles < 40 ? 1 : 37))
-            for (int iters = 1; iters <= 160; iters += (iters < 12 ? 1 : 19)) {
-                const int r = check(tiles, iters, slots);
-                ++cases;
-                if (r) {
-                    printf("FAIL code %d tiles %d iters %d slots %d\n", r, tiles, iters, slots);
-                    return 1;
+            for (int iters = 1; iters <= 160; iters += (iters < 12 ? 1 : 19))
+                for (int fixup : {0, 4, 16}) {
+                    const int r = check(tiles, iters, slots, fixup);
+                    ++cases;
+                    if (r) {
+                        printf("FAIL code %d tiles %d iters %d slots %d fixup %d\n", r, tiles, iters, slots, fixup);
+                        return 1;
+                    }
                 }
-            }
     printf("ok %d\n", cases);
     return 0;
 }
