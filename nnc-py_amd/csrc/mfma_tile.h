@@ -485,12 +485,12 @@ inline StreamK plan_streamk(int tiles, int iters, int slots, int fixup_slices) {
     return sk;
 }
 
-// Fixup cost in slice times: about 13 us for 128x128 tiles (~4 slices of
-// 3.4 us at two workgroups per CU), scaled by tile area for smaller tiles,
-// whose slices are shorter.
+// Fixup cost in slice times, measured on ResNet-18 and transformer layers:
+// about one slice for 128x128 tiles, scaled by tile area for smaller tiles
+// (shorter slices). Round-robin wins only when stream-K saves less.
 template <class T>
 constexpr int fixup_slices() {
-    return 4 * (128 * 128) / (T::BM * T::BN);
+    return (128 * 128) / (T::BM * T::BN);
 }
 
 // Persistent-grid size: workgroups of `kernel` resident on the device at once.
