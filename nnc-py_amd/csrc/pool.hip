@@ -104,6 +104,62 @@ __global__ void __launch_bounds__(256) global_avgpool_k(const float* __restrict_
     }
 }
 
+// One workgroup per plane (grid.x strides over planes) when the plane fits
+// in LDS: the plane is read once from HBM with coalesced loads (16-byte when
+// aligned), then every window is evaluated from LDS in the same order and
+// with the same comparisons / additions as pool2d_k (bit-exact). Removes the
+// 2.25x window re-reads of the direct kernel.
+template <bool MAX>
+__global__ void __launch_bounds__(256) pool2d_lds_k(PoolArgs a) {
+    extern __shared__ float plane_s[];
+    const int hw = a.H * a.W, hw_out = a.Ho * a.Wo;
+    for (int nc = blockIdx.x; nc < a.NC; nc += gridDim.x) {
+        const float* src = a.in + (int64_t)nc * hw;
+        int done = 0;
+        if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+            const int n4 = hw / 4;
+            for (int i = threadIdx.x; i < n4; i += 256)
+                reinterpret_cast<float4*>(plane_s)[i] = reinterpret_cast<const float4*>(src)[i];
+            done = n4 * 4;
+        }
+        for (int i = done + threadIdx.x; i < hw; i += 256) plane_s[i] = src[i];
+        __syncthreads();
+        float* dst = a.out + (int64_t)nc * hw_out;
+        for (int pos = threadIdx.x; pos < hw_out; pos += 256) {
+            const int oh = pos / a.Wo, ow = pos - oh * a.Wo;
+            int h0 = oh * a.sh - a.ph, h1 = h0 + a.kh;
+            int w0 = ow * a.sw - a.pw, w1 = w0 + a.kw;
+            if (h0 < 0) h0 = 0;
+            if (w0 < 0) w0 = 0;
+            if (h1 > a.H) h1 = a.H;
+            if (w1 > a.W) w1 = a.W;
+            if (MAX) {
+                float best = -3.402823e38f;
+                bool seen = false;
+                for (int h = h0; h < h1; ++h)
+                    for (int w = w0; w < w1; ++w) {
+                        const float v = plane_s[h * a.W + w];
+                        if (!seen || v > best) {
+                            best = v;
+                            seen = true;
+                        }
+                    }
+                dst[pos] = best;
+            } else {
+                float acc = 0.0f;
+                int cnt = 0;
+                for (int h = h0; h < h1; ++h)
+                    for (int w = w0; w < w1; ++w) {
+                        acc += plane_s[h * a.W + w];
+                        ++cnt;
+                    }
+                dst[pos] = cnt > 0 ? acc / (float)cnt : 0.0f;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 __global__ void fill_value_k(float* out, int64_t n, float v) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = v;
@@ -151,6 +207,13 @@ static void pool_entry(const char* name, Tensor* in, Tensor* out, int kh, int kw
         return;
     }
     if ((int64_t)a.Ho * a.Wo >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "output plane too large");
+    if (hw <= 16384 && hw > 0 && a.Ho > 0 && a.Wo > 0 && nc > 0) {
+        // whole plane in LDS (at most 64 KB): the input is read once
+        const int64_t cap = (int64_t)ctx().cu_count * 8;
+        const unsigned grid = (unsigned)(nc < cap ? nc : cap);
+        launch(name, pool2d_lds_k<MAX>, dim3(grid), dim3(256), (size_t)hw * sizeof(float), a);
+        return;
+    }
     const unsigned gy = (unsigned)(nc < 65535 ? nc : 65535);
     if (nc > 0 && a.Ho > 0 && a.Wo > 0)
         launch(name, pool2d_k<MAX>, dim3((unsigned)ceil_div((int64_t)a.Ho * a.Wo, 256), gy), dim3(256), 0, a);
