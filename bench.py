@@ -126,14 +126,9 @@ def cpu_baseline(pkg, iters: int) -> dict | None:
     else:
         return None
     lib = abi.bind(ctypes.CDLL(str(path)))
-    # the reference's own O3 call sequence: the residual conv+add+relu entry
-    # point is an mi355x addition that the reference runtime does not have
-    from nnc_py_amd.compiler import executor
-    saved, executor.RESIDUAL_FUSION = executor.RESIDUAL_FUSION, False
-    try:
-        prog = build_program(zoo.resnet18(batch=1, seed=1), opt_level=3)
-    finally:
-        executor.RESIDUAL_FUSION = saved
+    # the reference's own O3 call sequence (the mi355x target's fused and
+    # packed-weight entry points do not exist in the reference runtime)
+    prog = build_program(zoo.resnet18(batch=1, seed=1), opt_level=3, target_passes=False)
     ex = Executor(prog, device=False, lib=lib)
     ex.set_input("input", np.random.default_rng(0).standard_normal((1, 3, 224, 224)).astype(np.float32))
     ex.run()  # warmup
@@ -160,7 +155,12 @@ COPY_PROBE_BYTES = 256 << 20
 
 def conv_symbol_pattern(name: str) -> re.Pattern | None:
     """Kernel-table name -> regex over the HIP kernel symbol rocprofv3 reports,
-    e.g. conv_igemm_128x128_k3x3_v4 -> conv_streamk_k<nnc::Tile<128, 128, ...>, 3, 3, true>."""
+    e.g. conv_igemm_128x128_k3x3_v4 -> conv_streamk_k<nnc::Tile<128, 128, ...>, 3, 3, true>,
+    conv_igemm_128x128_k3x3_dma -> conv_dma_k<nnc::Tile<128, 128, ...>, 3, 3>."""
+    m = re.fullmatch(r"conv_igemm_(\d+)x(\d+)_k(\d+)x(\d+)_dma", name)
+    if m:
+        bm, bn, kh, kw = m.groups()
+        return re.compile(rf"conv_dma_k<nnc::Tile<{bm}, {bn},[^>]*>, {kh}, {kw}>")
     m = re.fullmatch(r"conv_igemm_(\d+)x(\d+)_k(\d+|any)(?:x(\d+))?_(v4|s1)", name)
     if m:
         bm, bn, kh, kw, vec = m.groups()

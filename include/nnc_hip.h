@@ -110,6 +110,16 @@ void nnc_hip_graph_destroy(void);
 void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw,
                            int sh, int sw, int ph, int pw);
 
+/* nnc_hip_conv_packed: convolution with the weights packed tap-major,
+ * [Co][kh][kw][Ci] (the compiler transposes the constant), which lets the
+ * kernel stream weights and input straight into LDS. out = act(conv(in, w) +
+ * bias (+ res)); act 0 none, 1 relu, 2 sigmoid. `b` and `res` may be NULL;
+ * `res` has the output's shape and may be the same buffer as `out`. Needs
+ * Ci % 32 == 0, a 1x1 or 3x3 kernel and 16-byte aligned weights
+ * (NNC_HIP_EUNSUPP otherwise). */
+void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,
+                         int sw, int ph, int pw, int act);
+
 #ifdef __cplusplus
 }
 #endif

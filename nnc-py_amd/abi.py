@@ -117,6 +117,7 @@ NOT_IN_REFERENCE = {"nnc_matmul_relu"}
 # Fused operators of the mi355x target (include/nnc_hip.h), emitted at O3.
 TARGET_SIGNATURES = {
     "nnc_hip_conv_add_relu": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int],
+    "nnc_hip_conv_packed": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
 }
 
 

@@ -22,8 +22,8 @@ import numpy as np
 from .. import abi
 from .ir import Graph, Node
 from .lower import Call, lower
-from .passes import (MemoryPlan, check_plan, eliminate_dead_code, eliminate_identity, fuse_matmul_bias, fuse_patterns, fuse_residual,
-                     plan_memory, prepack_lowering)
+from .passes import (MemoryPlan, check_plan, eliminate_dead_code, eliminate_identity, fuse_matmul_bias, fuse_patterns,
+                     fuse_residual, pack_conv_weights, plan_memory, prepack_lowering)
 
 
 @dataclass
@@ -37,24 +37,32 @@ class Program:
 
 # Conv -> Add -> Relu fusion into nnc_hip_conv_add_relu at O3 (mi355x target).
 RESIDUAL_FUSION = True
+# tap-major 3x3 conv weights and nnc_hip_conv_packed at O3 (mi355x target).
+PACK_CONV_WEIGHTS = True
 
 
 def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None = None,
-                  max_memory: int | None = None) -> Program:
+                  max_memory: int | None = None, target_passes: bool = True) -> Program:
     """Pass pipeline per optimisation level (passes/base.py:67-161 of the
-    reference), arena plan, lowering. Mutates `graph`."""
+    reference), arena plan, lowering. Mutates `graph`. `target_passes`
+    False leaves out the mi355x target's own O3 rewrites (residual fusion,
+    MatMul+bias fusion, packed conv weights, view aliasing), giving the call
+    sequence of the reference's own O3 pipeline for the reference runtime."""
     if opt_level >= 1:
         eliminate_identity(graph)
         eliminate_dead_code(graph)
     if opt_level >= 3:
         fuse_patterns(graph)
-        if RESIDUAL_FUSION:
-            fuse_residual(graph)
-        fuse_matmul_bias(graph)
+        if target_passes:
+            if RESIDUAL_FUSION:
+                fuse_residual(graph)
+            fuse_matmul_bias(graph)
+            if PACK_CONV_WEIGHTS:
+                pack_conv_weights(graph)
         prepack_lowering(graph)
     order = graph.topological_sort()
     strategy = memory_strategy or ("basic" if opt_level == 0 else "cost_aware")
-    plan = plan_memory(graph, order, strategy, max_memory, alias_views=opt_level >= 3)
+    plan = plan_memory(graph, order, strategy, max_memory, alias_views=opt_level >= 3 and target_passes)
     check_plan(graph, order, plan)
     return Program(graph, order, plan, lower(graph, order, plan.aliases), opt_level)
 

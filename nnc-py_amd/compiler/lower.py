@@ -53,6 +53,11 @@ def _conv_call(g: Graph, node: Node) -> Call:
     sh, sw = (list(node.attrs.get("strides", [1, 1])) + [1])[:2]
     pads = list(node.attrs.get("pads", [0, 0, 0, 0]))
     ph, pw = (pads + [0, 0])[:2]
+    if node.metadata.get("lowering", {}).get("weight_pack") == "tap_major":
+        act = {"FusedConvRelu": 1, "FusedConvAddRelu": 1, "FusedConvSigmoid": 2}.get(node.op_type, 0)
+        res = _t(node.inputs[3]) if node.op_type == "FusedConvAddRelu" else ("null",)
+        return Call("nnc_hip_conv_packed", [_t(x), _t(w), _opt(node, 2), res, _t(node.outputs[0])]
+                    + [("i", v) for v in (kh, kw, sh, sw, ph, pw, act)], node.name)
     if node.op_type == "FusedConvAddRelu":
         return Call("nnc_hip_conv_add_relu", [_t(x), _t(w), _opt(node, 2), _t(node.inputs[3]),
                                               _t(node.outputs[0])] + [("i", v) for v in (kh, kw, sh, sw, ph, pw)],

@@ -146,6 +146,38 @@ def fuse_residual(g: Graph) -> int:
     return fused
 
 
+CONV_OPS = ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu")
+
+
+def pack_conv_weights(g: Graph) -> int:
+    """mi355x target, O3: 3x3 convolutions with Ci % 32 == 0 whose weight is
+    a constant used only there get the weight transposed at compile time
+    from [Co][Ci][kh][kw] to tap-major [Co][kh][kw][Ci] and are lowered to
+    nnc_hip_conv_packed, whose kernels stream that layout straight into LDS.
+    1x1 weights already have that layout and keep their reference entry
+    points (which take the same kernels)."""
+    packed = 0
+    for node in g.nodes:
+        if node.op_type not in CONV_OPS or len(node.inputs) < 2:
+            continue
+        wname = node.inputs[1]
+        w = g.tensors[wname]
+        x = g.tensors[node.inputs[0]]
+        if not w.is_constant or w.data is None or w.data.ndim != 4 or len(g.consumers(wname)) != 1:
+            continue
+        co, ci, kh, kw = w.data.shape
+        if (kh, kw) != (3, 3) or ci % 32 or len(x.shape) != 4 or x.shape[1] != ci:
+            continue
+        if int(node.attrs.get("group", 1)) != 1 or list(node.attrs.get("dilations", [1, 1])) != [1, 1]:
+            continue
+        w.data = np.ascontiguousarray(w.data.transpose(0, 2, 3, 1))
+        w.shape = tuple(w.data.shape)
+        node.attrs["kernel_shape"] = [kh, kw]
+        node.metadata.setdefault("lowering", {})["weight_pack"] = "tap_major"
+        packed += 1
+    return packed
+
+
 def fuse_matmul_bias(g: Graph) -> int:
     """mi355x target, O3: MatMul(activation, constant W [K, N]) whose only
     consumer adds a constant 1-D bias [N] becomes one GEMM with the bias in
@@ -192,7 +224,7 @@ def prepack_lowering(g: Graph) -> None:
     """Conv kernel kind and constant Gemm B packing
     (passes/prepack_lowering.py:48-118)."""
     for node in g.nodes:
-        if node.op_type in ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu"):
+        if node.op_type in CONV_OPS:
             kh, kw = node.attrs.get("kernel_shape", [1, 1])
             sh, sw = node.attrs.get("strides", [1, 1])
             pads = node.attrs.get("pads", [0, 0, 0, 0])

@@ -128,11 +128,46 @@ struct ConvGather {
     }
 };
 
+// Writes a finished segment: a whole tile straight to the output with bias
+// (+ residual) + act, or a partial tile to the workgroup's stream-K slot.
+template <class T>
+__device__ __forceinline__ void conv_segment_out(const ConvArgs& a, const Segment& seg, int g, int i0, int j0,
+                                                 const floatx16 (&sum)[T::TM][T::TN]) {
+    const int hw = a.Ho * a.Wo;
+    if (seg.slot < 0) {
+#pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn) {
+            const int pix = j0 + acc_col<T>(tn);
+            if (pix >= a.Npix) continue;
+            const int n = pix / hw;
+            float* obase = a.out + (int64_t)n * a.Co * hw + (pix - n * hw);
+#pragma unroll
+            for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int co = i0 + acc_row<T>(tm, r);
+                    if (co < a.Co) {
+                        float v = sum[tm][tn][r] + (a.bias ? a.bias[co] : 0.f);
+                        if (a.res) v += a.res[(obase - a.out) + (int64_t)co * hw];
+                        obase[(int64_t)co * hw] = activate(v, a.act);
+                    }
+                }
+        }
+    } else {
+        float* slot = partial_slot<T>(a.ws, g, seg.slot);
+#pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) slot[acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)] = sum[tm][tn][r];
+    }
+}
+
 template <class T, int KH, int KW, bool AVEC>
 __global__ void __launch_bounds__(256, 2) conv_streamk_k(ConvArgs a, StreamK sk) {
     extern __shared__ __align__(16) float lds[];
     const int g = xcd_remap(blockIdx.x, sk.G);
-    const int hw = a.Ho * a.Wo;
     SegmentWalker walk(sk, g);
     Segment seg;
     while (walk.next(sk, seg)) {
@@ -148,34 +183,191 @@ __global__ void __launch_bounds__(256, 2) conv_streamk_k(ConvArgs a, StreamK sk)
         floatx16 sum[T::TM][T::TN];
         mfma_mainloop<T, false>(la, lb, seg.kb * T::BK, min(a.K, seg.ke * T::BK), lds, sum);
 
-        if (seg.slot < 0) {
+        conv_segment_out<T>(a, seg, g, i0, j0, sum);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant for Ci % 32 == 0 with weights packed tap-major,
+// [Co][kh][kw][Ci] (for 1x1 kernels that is the reference layout). K is
+// walked tap-major too: slice s covers one tap t and 32 consecutive input
+// channels c0..c0+31 (k = t*Ci + c), so within a slice the tap - and with
+// it each pixel's in-image test and offset - is uniform, and channels
+// differ by a wave-uniform stride (an SGPR offset). Operands go from global
+// memory straight into LDS (`buffer_load ... lds`, which writes lane l's
+// data to LDS[M0 + size * l]): no VGPR staging and no LDS store
+// instructions.
+//   A stage: [BM rows][32 k], 16-byte chunks XOR-swizzled (chunk kc of row
+//     x sits at position kc ^ (x & 7)). One dwordx4 load covers 8 rows x
+//     128 contiguous bytes of the packed weights; lane l takes row l / 8,
+//     position l % 8. An MFMA lane reads its four k of a quad as one
+//     ds_read_b128; eight consecutive rows hit eight different positions,
+//     so the reads are free of bank conflicts.
+//   B stage: [32 k][BN pixels]. One dword load covers 64 consecutive pixels
+//     of one (tap, channel): the gather coalesces along image rows. An MFMA
+//     lane reads its k one ds_read_b32 at a time (consecutive lanes,
+//     consecutive floats).
+// Out-of-range lanes (co >= Co, pixel >= Npix, tap outside the image) get an
+// out-of-range offset, and the hardware writes 0 to LDS.
+// ---------------------------------------------------------------------------
+template <class T>
+struct DmaStage {
+    static constexpr int A_FLOATS = T::BM * 32, B_FLOATS = T::BN * 32;
+    static constexpr int STAGE = A_FLOATS + B_FLOATS;
+    static constexpr int LDS_FLOATS = 2 * STAGE;
+    static constexpr int A_LOADS = T::BM / 32;        // dwordx4 loads per wave per slice (8 rows each)
+    static constexpr int PX_GROUPS = T::BN / 64;      // 64-pixel groups of a B row
+    static constexpr int B_LOADS = 32 / (4 / PX_GROUPS);  // dword loads per wave per slice
+    static_assert(T::BM % 32 == 0 && (T::BN == 64 || T::BN == 128) && T::BK == 32, "dma tile");
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+__device__ __forceinline__ void dma_load4(__amdgpu_buffer_rsrc_t r, float* lds_dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_dst, 4, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, float* lds_dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_dst, 16, voff, soff, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): the direct-to-LDS loads of this wave have landed
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// MFMA operands of quad q from a direct-to-LDS stage: A as one 16-byte read
+// per 32-row block, B as four single floats per 32-column block.
+template <class T>
+__device__ __forceinline__ void read_quad_dma(const float* Sa, int a_row, int a_sw, const float* Sb, int q,
+                                              f32x4 (&a)[T::TM], f32x4 (&b)[T::TN]) {
 #pragma unroll
-            for (int tn = 0; tn < T::TN; ++tn) {
-                const int pix = j0 + acc_col<T>(tn);
-                if (pix >= a.Npix) continue;
-                const int n = pix / hw;
-                float* obase = a.out + (int64_t)n * a.Co * hw + (pix - n * hw);
+    for (int tm = 0; tm < T::TM; ++tm)
+        a[tm] = *reinterpret_cast<const f32x4*>(Sa + (a_row + tm * 32) * 32 + ((a_sw ^ q) << 2));
 #pragma unroll
-                for (int tm = 0; tm < T::TM; ++tm)
+    for (int tn = 0; tn < T::TN; ++tn)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int co = i0 + acc_row<T>(tm, r);
-                        if (co < a.Co) {
-                            float v = sum[tm][tn][r] + (a.bias ? a.bias[co] : 0.f);
-                            if (a.res) v += a.res[(obase - a.out) + (int64_t)co * hw];
-                            obase[(int64_t)co * hw] = activate(v, a.act);
-                        }
-                    }
+        for (int s = 0; s < 4; ++s) b[tn][s] = Sb[(4 * q + s) * T::BN + tn * 32];
+}
+
+template <class T, int KH, int KW>
+__global__ void __launch_bounds__(256, 2) conv_dma_k(ConvArgs a, StreamK sk) {
+    typedef DmaStage<T> D;
+    extern __shared__ __align__(16) float lds[];
+    const int g = xcd_remap(blockIdx.x, sk.G);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hw = a.Ho * a.Wo;
+    const int HW = a.H * a.W;
+    const int CB = a.Ci >> 5;  // 32-channel blocks per tap
+    const __amdgpu_buffer_rsrc_t rin = make_rsrc(a.in), rw = make_rsrc(a.w);
+    // MFMA read side: A row and swizzled chunk of quad 0 (kc = 4h), B column
+    const int wi = (wave / T::WN) * T::WAVE_M, wj = (wave % T::WN) * T::WAVE_N;
+    const int a_row = wi + (lane & 31);
+    const int a_sw = (4 * (lane >> 5)) ^ (lane & 7);
+    const int b_off = D::A_FLOATS + 16 * (lane >> 5) * T::BN + wj + (lane & 31);
+    // load side: A rows (wave + 4i) * 8 + lane / 8, chunk (lane % 8) ^ (lane / 8);
+    // B pixel group wave % PX_GROUPS, k rows wave / PX_GROUPS + (4 / PX_GROUPS) * i
+    const int a_kc = (lane & 7) ^ ((lane >> 3) & 7);
+    const int b_grp = wave % D::PX_GROUPS;
+    const int b_kr0 = wave / D::PX_GROUPS;
+    constexpr int B_KSTEP = 4 / D::PX_GROUPS;
+
+    SegmentWalker walk(sk, g);
+    Segment seg;
+    while (walk.next(sk, seg)) {
+        const int mt = seg.tile % a.tiles_m, nt = seg.tile / a.tiles_m;
+        const int i0 = mt * T::BM, j0 = nt * T::BN;
+        uint32_t avo[D::A_LOADS];
+#pragma unroll
+        for (int i = 0; i < D::A_LOADS; ++i) {
+            const int co = i0 + (wave + 4 * i) * 8 + (lane >> 3);
+            avo[i] = co < a.Co ? (uint32_t)(co * a.K) * 4u + (uint32_t)a_kc * 16u : kOutOfRange;
+        }
+        // this lane's pixel: element offset of tap (0, 0) at channel 0, and
+        // the taps that fall inside the image
+        const int px = j0 + b_grp * 64 + lane;
+        const bool valid = px < a.Npix;
+        int bpo;
+        uint32_t bmask = 0;
+        {
+            const int p = valid ? px : 0;
+            const int n = p / hw;
+            const int rem = p - n * hw;
+            const int oh = rem / a.Wo;
+            const int ow = rem - oh * a.Wo;
+            const int h0 = oh * a.sh - a.ph, w0 = ow * a.sw - a.pw;
+            bpo = n * a.Ci * HW + h0 * a.W + w0;
+#pragma unroll
+            for (int r = 0; r < KH; ++r)
+#pragma unroll
+                for (int c = 0; c < KW; ++c) {
+                    const bool in = valid && (unsigned)(h0 + r) < (unsigned)a.H && (unsigned)(w0 + c) < (unsigned)a.W;
+                    bmask |= (uint32_t)in << (r * KW + c);
+                }
+        }
+        // issue slice (t, cb) into stage S
+        auto issue = [&](int t, int cb, float* S) {
+            const int r = t / KW, c = t - r * KW;
+            const uint32_t bv = ((bmask >> t) & 1u) ? (uint32_t)(bpo + r * a.W + c) * 4u : kOutOfRange;
+            const int c0 = cb * 32;
+            const uint32_t sa = (uint32_t)(t * a.Ci + c0) * 4u;
+#pragma unroll
+            for (int i = 0; i < D::A_LOADS; ++i) dma_load16(rw, S + (wave + 4 * i) * 8 * 32, avo[i], sa);
+#pragma unroll
+            for (int i = 0; i < D::B_LOADS; ++i) {
+                const int kr = b_kr0 + B_KSTEP * i;
+                dma_load4(rin, S + D::A_FLOATS + kr * T::BN + b_grp * 64, bv, (uint32_t)((c0 + kr) * HW) * 4u);
             }
-        } else {
-            float* slot = partial_slot<T>(a.ws, g, seg.slot);
+        };
+
+        floatx16 sum[T::TM][T::TN];
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
 #pragma unroll
             for (int tn = 0; tn < T::TN; ++tn)
 #pragma unroll
-                for (int tm = 0; tm < T::TM; ++tm)
+                for (int r = 0; r < 16; ++r) sum[tm][tn][r] = 0.f;
+
+        int t = seg.kb / CB;
+        int cb = seg.kb - t * CB;
+        issue(t, cb, lds);
+        wait_dma();
+        __syncthreads();
+        f32x4 av[T::TM], bw[T::TN];
+        read_quad_dma<T>(lds, a_row, a_sw, lds + b_off, 0, av, bw);
+        int stage = 0;
+        for (int it = seg.kb; it < seg.ke; ++it) {
+            const bool more = it + 1 < seg.ke;
+            float* next = lds + (stage ^ 1) * D::STAGE;
+            if (more) {
+                if (++cb == CB) {
+                    cb = 0;
+                    ++t;
+                }
+                issue(t, cb, next);
+            }
+            const float* S = lds + stage * D::STAGE;
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) slot[acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)] = sum[tm][tn][r];
+            for (int q = 0; q < 3; ++q) {
+                f32x4 an[T::TM], bn[T::TN];
+                read_quad_dma<T>(S, a_row, a_sw, S + b_off, q + 1, an, bn);
+                mfma_quad<T>(av, bw, sum);
+#pragma unroll
+                for (int tm = 0; tm < T::TM; ++tm) av[tm] = an[tm];
+#pragma unroll
+                for (int tn = 0; tn < T::TN; ++tn) bw[tn] = bn[tn];
+            }
+            wait_dma();
+            __syncthreads();
+            f32x4 an[T::TM], bn[T::TN];
+            if (more) read_quad_dma<T>(next, a_row, a_sw, next + b_off, 0, an, bn);
+            mfma_quad<T>(av, bw, sum);
+            if (more) {
+#pragma unroll
+                for (int tm = 0; tm < T::TM; ++tm) av[tm] = an[tm];
+#pragma unroll
+                for (int tn = 0; tn < T::TN; ++tn) bw[tn] = bn[tn];
+            }
+            stage ^= 1;
         }
+        conv_segment_out<T>(a, seg, g, i0, j0, sum);
     }
 }
 
@@ -286,10 +478,46 @@ static void launch_conv_t(ConvArgs& a, const char* entry) {
     }
 }
 
+template <class T, int KH, int KW>
+static void launch_conv_dma_t(ConvArgs& a, const char* entry) {
+    auto kernel = conv_dma_k<T, KH, KW>;
+    const size_t lds = (size_t)DmaStage<T>::LDS_FLOATS * sizeof(float);
+    static bool configured = false;
+    static int slots = 0;
+    if (!configured) {
+        if (!hip_ok(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)lds),
+                    entry, "hipFuncSetAttribute"))
+            return;
+        slots = resident_groups(kernel, lds);
+        configured = true;
+    }
+    const int iters = a.K / T::BK;  // Ci % 32 == 0: whole slices
+    const StreamK sk = plan_streamk(a.tiles_m * a.tiles_n, iters, slots, fixup_slices<T>());
+    if (sk.G < 1) return;
+    float* ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
+    if (!ws) return fail(NNC_HIP_ENOMEM, entry, "no workspace for stream-K partials");
+    a.ws = ws;
+    char name[64];
+    snprintf(name, sizeof name, "conv_igemm_%dx%d_k%dx%d_dma", T::BM, T::BN, KH, KW);
+    set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
+    launch(name, kernel, dim3(sk.G), dim3(256), lds, a, sk);
+    if (sk.needs_fixup()) {
+        set_work(0.0, 0.0);
+        launch("conv_streamk_fixup", conv_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, a, sk);
+    }
+}
+
+// `dma`: weights are tap-major [Co][kh][kw][Ci] (or 1x1), Ci % 32 == 0, kernel
+// 1x1 or 3x3 and weights 16-byte aligned; checked by the caller.
 template <class T>
-static void launch_conv(ConvArgs& a, bool avec, const char* entry) {
+static void launch_conv(ConvArgs& a, bool avec, bool dma, const char* entry) {
     a.tiles_m = (int)ceil_div(a.Co, T::BM);
     a.tiles_n = (int)ceil_div(a.Npix, T::BN);
+    if (dma) {
+        if (a.kh == 3) return launch_conv_dma_t<T, 3, 3>(a, entry);
+        return launch_conv_dma_t<T, 1, 1>(a, entry);
+    }
 #define NNC_CONV_KS(KH, KW)                                                 \
     if (avec) launch_conv_t<T, KH, KW, true>(a, entry);                     \
     else launch_conv_t<T, KH, KW, false>(a, entry);                         \
@@ -322,8 +550,9 @@ static bool conv_check(Tensor* in, Tensor* w, Tensor* out, const char* name) {
     return true;
 }
 
+// `packed`: the weights are [Co][kh][kw][Ci] (nnc_hip_conv_packed)
 static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw,
-                     int ph, int pw, int act, const char* name, Tensor* res = nullptr) {
+                     int ph, int pw, int act, const char* name, Tensor* res = nullptr, bool packed = false) {
     ConvArgs a{};
     a.res = res ? (const float*)res->data : nullptr;
     a.in = (const float*)in->data;
@@ -366,6 +595,16 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     a.K = (int)K;
     a.Npix = (int)npix;
     a.vec_out = aligned16(a.out) && (!a.res || aligned16(a.res));
+    // direct-to-LDS kernels: tap-major weights (1x1 weights already are)
+    const bool dma_ok = a.Ci % 32 == 0 && aligned16(a.w) && ((kh == 3 && kw == 3) || (kh == 1 && kw == 1));
+    if (packed) {
+        if (w->shape[1] != kh || w->shape[2] != kw || w->shape[3] != a.Ci)
+            return fail(NNC_HIP_EINVAL, name, "packed weight shape is not [Co][kh][kw][Ci]");
+        if (!dma_ok)
+            return fail(NNC_HIP_EUNSUPP, name,
+                        "packed weights need Ci % 32 == 0, a 1x1 or 3x3 kernel and 16-byte alignment");
+    }
+    const bool dma = dma_ok && (packed || (kh == 1 && kw == 1));
     if (a.N == 0 || a.Co == 0 || a.Ho <= 0 || a.Wo <= 0) return;
     const bool avec = (a.K % 4 == 0) && aligned16(a.w);
     // Tile choice (measured on ResNet-18 layers at batch 1 and 32): big tiles
@@ -374,11 +613,11 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     // tiles, whose shorter per-tile latency and larger tile count fill the
     // GPU.
     if (a.K >= 512 && a.Co >= 128 && a.Npix >= 1024)
-        launch_conv<ConvT128>(a, avec, name);
+        launch_conv<ConvT128>(a, avec, dma, name);
     else if (a.K >= 512 && a.Co <= 64 && a.Npix >= 4096)
-        launch_conv<ConvT64>(a, avec, name);
+        launch_conv<ConvT64>(a, avec, dma, name);
     else
-        launch_conv<ConvTSmall>(a, avec, name);
+        launch_conv<ConvTSmall>(a, avec, dma, name);
 }
 
 }  // namespace nnc
@@ -436,6 +675,21 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
     if (!conv_check(in, w, out, name)) return;
     if (!res || !res->data || !res->shape) return fail(NNC_HIP_EINVAL, name, "NULL residual");
     conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, kActRelu, name, res);
+}
+
+// No reference counterpart: convolution with weights packed tap-major,
+// [Co][kh][kw][Ci], emitted by the mi355x target at O3 (the compiler packs
+// the constant). out = act(conv(in, w) + bias (+ res)), act 0 none, 1 relu,
+// 2 sigmoid; `b` and `res` may be NULL, `res` may be the same buffer as
+// `out`. Needs Ci % 32 == 0, a 1x1 or 3x3 kernel and 16-byte aligned
+// weights (NNC_HIP_EUNSUPP otherwise).
+void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh, int sw,
+                         int ph, int pw, int act) {
+    const char* name = "nnc_hip_conv_packed";
+    if (!conv_check(in, w, out, name)) return;
+    if (res && (!res->data || !res->shape)) return fail(NNC_HIP_EINVAL, name, "NULL residual data");
+    if (act < kActNone || act > kActSigmoid) return fail(NNC_HIP_EINVAL, name, "act must be 0, 1 or 2");
+    conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, act, name, res, true);
 }
 
 }  // extern "C"

@@ -245,7 +245,39 @@ struct XContigLoader4 {
 // slice's products into the running sum through a fresh accumulator
 // (shorter fp32 rounding chains for very long K); otherwise the MFMAs
 // accumulate into `sum` directly.
+//
+// Per slice (four quads of four k per lane half): the next slice's global
+// loads are issued first; quad q+1's LDS operands are read while quad q's
+// MFMAs run; after quad 2 the loaded registers are stored to the other
+// stage and the workgroup barrier is taken, then the next slice's quad 0 is
+// read from the other stage while quad 3's MFMAs (operands already in
+// registers) run. So no LDS read latency sits in front of a slice's first
+// MFMA. Hazards: stage s is written in slice t+1 only after slice t's
+// barrier, and every wave's reads of stage s were waited for before it
+// passed that barrier (the barrier's LDS fence); stage s^1 is read only
+// after the barrier that follows its writes.
 // ---------------------------------------------------------------------------
+template <class T>
+__device__ __forceinline__ void read_quad(const float* Ap, const float* Bp, int q, f32x4 (&a)[T::TM],
+                                          f32x4 (&b)[T::TN]) {
+#pragma unroll
+    for (int tm = 0; tm < T::TM; ++tm) a[tm] = *reinterpret_cast<const f32x4*>(Ap + tm * 32 * T::LDK + 4 * q);
+#pragma unroll
+    for (int tn = 0; tn < T::TN; ++tn) b[tn] = *reinterpret_cast<const f32x4*>(Bp + tn * 32 * T::LDK + 4 * q);
+}
+
+template <class T>
+__device__ __forceinline__ void mfma_quad(const f32x4 (&a)[T::TM], const f32x4 (&b)[T::TN],
+                                          floatx16 (&acc)[T::TM][T::TN]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < T::TN; ++tn)
+                acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm][st], b[tn][st], acc[tm][tn], 0, 0, 0);
+}
+
 template <class T, bool TWO_LEVEL, class LA, class LB>
 __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k_end, float* lds,
                                               floatx16 (&sum)[T::TM][T::TN]) {
@@ -271,6 +303,8 @@ __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k
     lb.store(lds + T::A_FLOATS);
     __syncthreads();
 
+    f32x4 a[T::TM], b[T::TN];
+    read_quad<T>(lds + a_off, lds + b_off, 0, a, b);
     int stage = 0;
     for (int k0 = k_begin; k0 < k_end; k0 += T::BK) {
         const bool more = k0 + T::BK < k_end;
@@ -289,53 +323,42 @@ __device__ __forceinline__ void mfma_mainloop(LA& la, LB& lb, int k_begin, int k
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[tm][tn][r] = 0.f;
         }
-        // four quads of four k per lane half
-        f32x4 a[T::TM], b[T::TN];
 #pragma unroll
-        for (int tm = 0; tm < T::TM; ++tm) a[tm] = *reinterpret_cast<const f32x4*>(Ap + tm * 32 * T::LDK);
-#pragma unroll
-        for (int tn = 0; tn < T::TN; ++tn) b[tn] = *reinterpret_cast<const f32x4*>(Bp + tn * 32 * T::LDK);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 3; ++q) {
             f32x4 an[T::TM], bn[T::TN];
-            if (q < 3) {
+            read_quad<T>(Ap, Bp, q + 1, an, bn);
+            if (TWO_LEVEL)
+                mfma_quad<T>(a, b, acc);
+            else
+                mfma_quad<T>(a, b, sum);
 #pragma unroll
-                for (int tm = 0; tm < T::TM; ++tm)
-                    an[tm] = *reinterpret_cast<const f32x4*>(Ap + tm * 32 * T::LDK + 4 * (q + 1));
+            for (int tm = 0; tm < T::TM; ++tm) a[tm] = an[tm];
 #pragma unroll
-                for (int tn = 0; tn < T::TN; ++tn)
-                    bn[tn] = *reinterpret_cast<const f32x4*>(Bp + tn * 32 * T::LDK + 4 * (q + 1));
-            }
-#pragma unroll
-            for (int st = 0; st < 4; ++st)
-#pragma unroll
-                for (int tm = 0; tm < T::TM; ++tm)
-#pragma unroll
-                    for (int tn = 0; tn < T::TN; ++tn) {
-                        if (TWO_LEVEL)
-                            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm][st], b[tn][st], acc[tm][tn], 0, 0, 0);
-                        else
-                            sum[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[tm][st], b[tn][st], sum[tm][tn], 0, 0, 0);
-                    }
-            if (q < 3) {
-#pragma unroll
-                for (int tm = 0; tm < T::TM; ++tm) a[tm] = an[tm];
-#pragma unroll
-                for (int tn = 0; tn < T::TN; ++tn) b[tn] = bn[tn];
-            }
+            for (int tn = 0; tn < T::TN; ++tn) b[tn] = bn[tn];
         }
-        if (TWO_LEVEL) {
-#pragma unroll
-            for (int tm = 0; tm < T::TM; ++tm)
-#pragma unroll
-                for (int tn = 0; tn < T::TN; ++tn) sum[tm][tn] += acc[tm][tn];
-        }
+        float* next = lds + (stage ^ 1) * T::STAGE;
         if (more) {
-            float* next = lds + (stage ^ 1) * T::STAGE;
             la.store(next);
             lb.store(next + T::A_FLOATS);
         }
         __syncthreads();
+        f32x4 an[T::TM], bn[T::TN];
+        if (more) read_quad<T>(next + a_off, next + b_off, 0, an, bn);
+        if (TWO_LEVEL) {
+            mfma_quad<T>(a, b, acc);
+#pragma unroll
+            for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < T::TN; ++tn) sum[tm][tn] += acc[tm][tn];
+        } else {
+            mfma_quad<T>(a, b, sum);
+        }
+        if (more) {
+#pragma unroll
+            for (int tm = 0; tm < T::TM; ++tm) a[tm] = an[tm];
+#pragma unroll
+            for (int tn = 0; tn < T::TN; ++tn) b[tn] = bn[tn];
+        }
         stage ^= 1;
     }
 }

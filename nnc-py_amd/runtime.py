@@ -55,6 +55,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_graph_launch": ([], ctypes.c_int),
     "nnc_hip_graph_destroy": ([], None),
     "nnc_hip_conv_add_relu": (abi.TARGET_SIGNATURES["nnc_hip_conv_add_relu"], None),
+    "nnc_hip_conv_packed": (abi.TARGET_SIGNATURES["nnc_hip_conv_packed"], None),
 }
 
 

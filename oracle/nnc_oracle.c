@@ -949,3 +949,54 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
     nnc_add_relu(&t, res, out);
     free(tmp);
 }
+
+/* ------------------------------------------------------------------------
+ * Packed-weight convolution of the mi355x target (include/nnc_hip.h), no
+ * reference counterpart: the weights [Co][kh][kw][Ci] are unpacked to the
+ * reference layout [Co][Ci][kh][kw], then nnc_conv into a temporary
+ * (ops.c:720-1050) followed by the element-wise op that applies residual and
+ * activation: nnc_add / nnc_add_relu / nnc_add_sigmoid with `res`
+ * (ops.c:82-110, 3233-3346), or nnc_relu / nnc_sigmoid without it
+ * (ops.c:230-246). Pinned by composition of pinned entry points.
+ * ---------------------------------------------------------------------- */
+void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,
+                         int sw, int ph, int pw, int act) {
+    if (!in || !w || !out || w->ndim != 4 || in->ndim != 4) return;
+    const int64_t co = w->shape[0], ci = in->shape[1], taps = (int64_t)kh * kw;
+    const int64_t n = numel(out);
+    float* wt = (float*)malloc((size_t)(co * ci * taps > 0 ? co * ci * taps : 1) * sizeof(float));
+    float* tmp = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    if (!wt || !tmp) {
+        free(wt);
+        free(tmp);
+        return;
+    }
+    const float* wp = (const float*)w->data;
+    for (int64_t o = 0; o < co; ++o)
+        for (int64_t t = 0; t < taps; ++t)
+            for (int64_t c = 0; c < ci; ++c) wt[(o * ci + c) * taps + t] = wp[(o * taps + t) * ci + c];
+    int64_t wshape[4] = {co, ci, kh, kw};
+    Tensor wu = *w;
+    wu.data = wt;
+    wu.shape = wshape;
+    wu.nbytes = (size_t)(co * ci * taps) * sizeof(float);
+    Tensor t = *out;
+    t.data = tmp;
+    nnc_conv(in, &wu, b, &t, kh, kw, sh, sw, ph, pw);
+    if (res) {
+        if (act == 1)
+            nnc_add_relu(&t, res, out);
+        else if (act == 2)
+            nnc_add_sigmoid(&t, res, out);
+        else
+            nnc_add(&t, res, out);
+    } else if (act == 1) {
+        nnc_relu(&t, out);
+    } else if (act == 2) {
+        nnc_sigmoid(&t, out);
+    } else {
+        memcpy(out->data, tmp, (size_t)n * sizeof(float));
+    }
+    free(wt);
+    free(tmp);
+}

@@ -61,35 +61,69 @@ def test_o1_call_sequence_matches_reference_snapshot(model, pkg):
 
 def test_o3_fusion_and_prepack_on_resnet18(pkg):
     """O3: conv+relu fusion, each residual block's conv+add+relu as one call
-    (in place only over the residual), conv entry selection, constant FC
+    (in place only over the residual), every 3x3 conv with Ci % 32 == 0 on
+    tap-major packed weights, conv entry selection for the rest, constant FC
     weight as gemm_nt."""
     from nnc_py_amd.compiler import build_program, zoo
     prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
     ops = [c.op for c in prog.calls]
     assert len(ops) == 23  # Flatten is an alias of the pooled tensor: no call
     assert "nnc_flatten" not in ops and prog.plan.aliases
-    assert ops.count("nnc_hip_conv_add_relu") == 8
+    assert ops.count("nnc_hip_conv_packed") == 16
     assert "nnc_add_relu" not in ops and "nnc_relu" not in ops
-    assert ops.count("nnc_conv_relu3x3_s1") == 5  # conv1 of the five stride-1 blocks
     assert ops[0] == "nnc_conv_relu7x7_s2" and ops.count("nnc_conv1x1") == 3
     assert ops[-1] == "nnc_gemm_nt"
+    with_res = [c for c in prog.calls if c.op == "nnc_hip_conv_packed" and c.args[3][0] == "t"]
+    assert len(with_res) == 8
     for c in prog.calls:
-        if c.op == "nnc_hip_conv_add_relu":
+        if c.op != "nnc_hip_conv_packed":
+            continue
+        assert c.args[-1] == ("i", 1)  # relu after every 3x3 conv of ResNet-18
+        w = prog.graph.tensors[c.args[1][1]]
+        assert w.shape[1:3] == (3, 3) and w.shape[3] % 32 == 0  # [Co][kh][kw][Ci]
+        if c.args[3][0] == "t":
             res, out = c.args[3][1], c.args[4][1]
             assert prog.graph.tensors[res].shape == prog.graph.tensors[out].shape
             assert prog.plan.offsets[out] != prog.plan.offsets[c.args[0][1]]
 
 
-def test_residual_fusion_can_be_switched_off(pkg):
+def test_packed_conv_weights_are_the_transposed_constants(pkg):
+    from nnc_py_amd.compiler import build_program, zoo
+    ref = zoo.resnet18(batch=1, seed=0)
+    orig = {k: t.data.copy() for k, t in ref.tensors.items() if t.is_constant and t.data is not None
+            and t.data.ndim == 4}
+    prog = build_program(ref, opt_level=3)
+    n = 0
+    for c in prog.calls:
+        if c.op == "nnc_hip_conv_packed":
+            name = c.args[1][1]
+            np.testing.assert_array_equal(prog.graph.tensors[name].data, orig[name].transpose(0, 2, 3, 1))
+            n += 1
+    assert n == 16
+
+
+def test_target_rewrites_can_be_switched_off(pkg):
+    """Without weight packing the residual blocks use nnc_hip_conv_add_relu;
+    without residual fusion either, conv and add_relu are separate calls;
+    target_passes=False gives the reference's own O3 call sequence."""
     from nnc_py_amd.compiler import build_program, zoo
     from nnc_py_amd.compiler import executor as ex_mod
-    ex_mod.RESIDUAL_FUSION = False
+    ex_mod.PACK_CONV_WEIGHTS = False
     try:
         prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
+        ops = [c.op for c in prog.calls]
+        assert len(ops) == 23 and ops.count("nnc_hip_conv_add_relu") == 8
+        assert ops.count("nnc_conv_relu3x3_s1") == 5  # conv1 of the five stride-1 blocks
+        ex_mod.RESIDUAL_FUSION = False
+        prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
+        ops = [c.op for c in prog.calls]
+        assert len(ops) == 31 and ops.count("nnc_add_relu") == 8
     finally:
+        ex_mod.PACK_CONV_WEIGHTS = True
         ex_mod.RESIDUAL_FUSION = True
-    ops = [c.op for c in prog.calls]
-    assert len(ops) == 31 and ops.count("nnc_add_relu") == 8
+    ops = [c.op for c in build_program(zoo.resnet18(batch=2, seed=0), opt_level=3, target_passes=False).calls]
+    assert len(ops) == 32 and ops.count("nnc_add_relu") == 8 and "nnc_flatten" in ops
+    assert not any(o.startswith("nnc_hip_") for o in ops)
 
 
 def test_arena_plan_reuses_memory_and_keeps_invariants(pkg):

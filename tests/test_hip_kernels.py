@@ -1,8 +1,8 @@
 """Targeted GPU checks of the MFMA kernels at shapes the golden vectors are
 too small to reach: every conv tile configuration with stream-K splitting
 (tiles fewer than resident workgroups, K tails, 3-channel stem), the fused
-conv+add+relu of the mi355x target (also in place over its residual), and
-GEMM / MatMul layouts. Expected values come from the oracle on the host, the
+conv+add+relu of the mi355x target (also in place over its residual), the
+packed-weight direct-to-LDS convolution, and GEMM / MatMul layouts. Expected values come from the oracle on the host, the
 same seeded inputs; bar |got - ref| <= 1e-4 or <= 1e-3 * |ref|."""
 
 from __future__ import annotations
@@ -124,6 +124,93 @@ def test_conv_add_relu_rejects_bad_residual(hip, dmem, abi):
     runtime.clear_error()
     out = caserun.run_case(hip, case, abi, dmem)["out"]
     assert runtime.last_error()[0] != 0
+    assert not out.any()
+
+
+def _packed_case(rng, n, ci, h, co, k, s, p, act=1, bias=True, res=True, w_ref=None):
+    """nnc_hip_conv_packed case: weights drawn in the reference layout and
+    passed tap-major [Co][kh][kw][Ci]."""
+    ho = (h + 2 * p - k) // s + 1
+    x = rng.standard_normal((n, ci, h, h)).astype(np.float32)
+    w = (rng.standard_normal((co, ci, k, k)) / np.sqrt(ci * k * k)).astype(np.float32) if w_ref is None else w_ref
+    tensors = {"x": x, "w": np.ascontiguousarray(w.transpose(0, 2, 3, 1)),
+               "out": np.zeros((n, co, ho, ho), np.float32)}
+    if bias:
+        tensors["b"] = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    if res:
+        tensors["res"] = rng.standard_normal((n, co, ho, ho)).astype(np.float32)
+    args = [("t", "x"), ("t", "w"), ("t", "b") if bias else ("null",), ("t", "res") if res else ("null",),
+            ("t", "out")] + [("i", v) for v in (k, k, s, s, p, p, act)]
+    return {"name": f"packed_{n}x{ci}x{h}_{co}_k{k}s{s}p{p}_a{act}{'b' if bias else ''}{'r' if res else ''}",
+            "op": "nnc_hip_conv_packed", "tensors": tensors, "args": args, "outputs": ["out"], "bar": "fp"}
+
+
+# every tile configuration of the direct-to-LDS kernels, tails in Co and
+# pixels, stride 2, no padding, 1x1
+PACKED_SHAPES = [
+    (2, 64, 28, 64, 3, 1, 1),     # 64x64 tiles
+    (4, 64, 56, 64, 3, 1, 1),     # 64x128 tiles, stream-K
+    (8, 128, 28, 128, 3, 1, 1),   # 128x128 tiles, stream-K
+    (16, 256, 14, 256, 3, 1, 1),  # 128x128 with a partial last pixel tile
+    (2, 256, 14, 512, 3, 2, 1),   # stride 2, many M tiles
+    (4, 512, 7, 512, 3, 1, 1),    # K = 4608: many partials per tile
+    (3, 32, 13, 96, 3, 2, 1),     # odd image, Co and pixel tails
+    (2, 32, 9, 40, 3, 1, 1),      # Co < tile
+    (2, 64, 10, 64, 3, 1, 0),     # no padding
+    (4, 64, 14, 128, 1, 1, 0),    # 1x1
+    (4, 128, 28, 256, 1, 2, 0),   # 1x1 stride 2
+]
+
+
+@pytest.mark.parametrize("shape", PACKED_SHAPES, ids=[str(s) for s in PACKED_SHAPES])
+def test_conv_packed_shapes(shape, hip, dmem, abi, oracle_lib):
+    case = _packed_case(np.random.default_rng(13), *shape)
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    _check(got, exp, case["name"])
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("bias,res", [(True, False), (False, True), (False, False)])
+def test_conv_packed_epilogues(act, bias, res, hip, dmem, abi, oracle_lib):
+    for shape in ((2, 64, 12, 64, 3, 1, 1), (8, 128, 28, 128, 3, 1, 1)):
+        case = _packed_case(np.random.default_rng(17), *shape, act=act, bias=bias, res=res)
+        print(f"case {case['name']}", flush=True)
+        exp = caserun.run_case(oracle_lib, case, abi)["out"]
+        got = caserun.run_case(hip, case, abi, dmem)["out"]
+        _check(got, exp, case["name"])
+
+
+def test_conv_packed_matches_reference_layout_entry(hip, dmem, abi, oracle_lib):
+    """The packed entry on transposed weights agrees with nnc_conv_relu on
+    the original ones (both within the bar of the oracle's fp64 sums)."""
+    rng = np.random.default_rng(19)
+    packed = _packed_case(rng, 4, 128, 28, 128, 3, 1, 1, bias=True, res=False)
+    w = np.ascontiguousarray(packed["tensors"]["w"].transpose(0, 3, 1, 2))
+    plain = {"name": "plain", "op": "nnc_conv_relu",
+             "tensors": {"x": packed["tensors"]["x"], "w": w, "b": packed["tensors"]["b"],
+                         "out": np.zeros_like(packed["tensors"]["out"])},
+             "args": [("t", "x"), ("t", "w"), ("t", "b"), ("t", "out")] + [("i", v) for v in (3, 3, 1, 1, 1, 1)],
+             "outputs": ["out"], "bar": "fp"}
+    got = caserun.run_case(hip, packed, abi, dmem)["out"]
+    ref = caserun.run_case(hip, plain, abi, dmem)["out"]
+    _check(got, ref, "packed vs reference layout")
+
+
+@pytest.mark.parametrize("why,shape,wshape", [
+    ("Ci % 32", (1, 24, 8, 16, 3, 1, 1), (16, 3, 3, 24)),
+    ("5x5 kernel", (1, 32, 8, 16, 5, 1, 2), (16, 5, 5, 32)),
+    ("not tap-major", (1, 32, 8, 16, 3, 1, 1), (16, 32, 3, 3)),
+])
+def test_conv_packed_rejects(why, shape, wshape, hip, dmem, abi):
+    from nnc_py_amd import runtime
+    rng = np.random.default_rng(1)
+    case = _packed_case(rng, *shape)
+    case["tensors"]["w"] = np.zeros(wshape, np.float32)
+    runtime.clear_error()
+    out = caserun.run_case(hip, case, abi, dmem)["out"]
+    assert runtime.last_error()[0] != 0, why
     assert not out.any()
 
 

@@ -267,3 +267,71 @@ def test_oracle_binary_flat_modulo_rule(oracle_lib, abi):
                     "out": np.full(8, -1.0, F32)}
     got = caserun.run_case(oracle_lib, c, abi)["out"]
     assert got.tolist() == [0, 2, 4, -1, -1, -1, -1, -1]  # only min(3,5,8) written
+
+
+# ---------------------------------------------------------------------------
+# the mi355x target's entry points that have no reference counterpart are
+# compositions of pinned ones; check the composition against numpy so that a
+# wrong unpacking index, a dropped residual or a wrong activation fails
+# ---------------------------------------------------------------------------
+def _relu(x):
+    return np.where(x > 0, x, F32(0)).astype(F32)
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("res", [False, True])
+@pytest.mark.parametrize("kernel", [(3, 3, 1, 1, 1, 1), (3, 3, 2, 2, 1, 1), (1, 1, 2, 2, 0, 0)])
+def test_oracle_conv_packed_composition(act, res, kernel, oracle_lib, abi):
+    kh, kw, sh, sw, ph, pw = kernel
+    rng = np.random.default_rng(31 + act + 3 * res)
+    c = _conv_case(rng, "nnc_conv", 2, 32, 9, 9, 6, kh, kw, sh, sw, ph, pw)
+    conv = caserun.run_case(oracle_lib, c, abi)["out"]
+    t = dict(c["tensors"])
+    t["w"] = np.ascontiguousarray(t["w"].transpose(0, 2, 3, 1))
+    args = c["args"][:3] + [("t", "res") if res else ("null",)] + c["args"][3:] + [("i", act)]
+    t["res"] = rng.standard_normal(conv.shape).astype(F32)
+    got = caserun.run_case(oracle_lib, {"name": "packed", "op": "nnc_hip_conv_packed", "tensors": t,
+                                        "args": args, "outputs": ["out"]}, abi)["out"]
+    pre = (conv + t["res"]).astype(F32) if res else conv
+    if act == 0:
+        assert caserun.same_bits(got, pre)
+    elif act == 1:
+        assert caserun.same_bits(got, _relu(pre))
+    else:
+        np.testing.assert_allclose(got, 1.0 / (1.0 + np.exp(-pre.astype(np.float64))), rtol=1e-6, atol=1e-7)
+    # and the unpacked weights give the float64 convolution
+    ref = _np_conv_f64(c["tensors"]["x"], c["tensors"]["w"], c["tensors"]["b"], sh, sw, ph, pw,
+                       conv.shape[2], conv.shape[3])
+    np.testing.assert_allclose(conv, ref.astype(F32), rtol=2e-7, atol=1e-5)
+
+
+def test_oracle_conv_add_relu_composition(oracle_lib, abi):
+    rng = np.random.default_rng(41)
+    c = _conv_case(rng, "nnc_conv", 2, 5, 8, 8, 4, 3, 3, 1, 1, 1, 1)
+    conv = caserun.run_case(oracle_lib, c, abi)["out"]
+    t = dict(c["tensors"], res=rng.standard_normal(conv.shape).astype(F32))
+    args = c["args"][:3] + [("t", "res")] + c["args"][3:]
+    got = caserun.run_case(oracle_lib, {"name": "car", "op": "nnc_hip_conv_add_relu", "tensors": t,
+                                        "args": args, "outputs": ["out"]}, abi)["out"]
+    assert caserun.same_bits(got, _relu((conv + t["res"]).astype(F32)))
+
+
+@pytest.mark.parametrize("bias_shape", [None, (7,), (5, 7)])
+def test_oracle_matmul_relu_composition(bias_shape, oracle_lib, abi):
+    rng = np.random.default_rng(43)
+    a = rng.standard_normal((5, 6)).astype(F32)
+    b = rng.standard_normal((6, 7)).astype(F32)
+    t = {"a": a, "b": b, "out": np.zeros((5, 7), F32)}
+    mm = caserun.run_case(oracle_lib, {"name": "mm", "op": "nnc_matmul", "tensors": dict(t),
+                                       "args": [("t", "a"), ("t", "b"), ("t", "out")], "outputs": ["out"]},
+                          abi)["out"]
+    np.testing.assert_allclose(mm, a.astype(np.float64) @ b, rtol=1e-5, atol=1e-5)
+    args = [("t", "a"), ("t", "b"), ("null",), ("t", "out")]
+    want = mm
+    if bias_shape:
+        t["bias"] = rng.standard_normal(bias_shape).astype(F32)
+        args[2] = ("t", "bias")
+        want = (mm + t["bias"]).astype(F32)
+    got = caserun.run_case(oracle_lib, {"name": "mmr", "op": "nnc_matmul_relu", "tensors": t, "args": args,
+                                        "outputs": ["out"]}, abi)["out"]
+    assert caserun.same_bits(got, _relu(want))
