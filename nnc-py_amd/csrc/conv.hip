@@ -302,19 +302,29 @@ __global__ void __launch_bounds__(256, 2) conv_dma_k(ConvArgs a, StreamK sk) {
                     bmask |= (uint32_t)in << (r * KW + c);
                 }
         }
-        // issue slice (t, cb) into stage S
-        auto issue = [&](int t, int cb, float* S) {
+        // loads of slice (t, cb) into stage S; with `on` false every load gets
+        // an out-of-range offset (no memory access, zeros into the stage)
+        auto issue_a = [&](int t, int cb, float* S, bool on) {
+            const uint32_t sa = (uint32_t)(t * a.Ci + cb * 32) * 4u;
+#pragma unroll
+            for (int i = 0; i < D::A_LOADS; ++i)
+                dma_load16(rw, S + (wave + 4 * i) * 8 * 32, on ? avo[i] : kOutOfRange, sa);
+        };
+        // this lane's B offset for tap t: out of range (exactly kOutOfRange, so
+        // adding the SGPR offset cannot wrap) if the tap is outside the image
+        // or `on` is false; computed without branches
+        auto b_voff = [&](int t, bool on) {
             const int r = t / KW, c = t - r * KW;
-            const uint32_t bv = ((bmask >> t) & 1u) ? (uint32_t)(bpo + r * a.W + c) * 4u : kOutOfRange;
-            const int c0 = cb * 32;
-            const uint32_t sa = (uint32_t)(t * a.Ci + c0) * 4u;
+            const uint32_t addr = (uint32_t)(bpo + r * a.W + c) * 4u;
+            const uint32_t keep = 0u - (((bmask >> t) & 1u) & (uint32_t)on);
+            return (addr & keep) | (kOutOfRange & ~keep);
+        };
+        auto issue_b = [&](int cb, float* S, uint32_t bv, int i_begin, int i_end) {
+            const uint32_t s0 = (uint32_t)((cb * 32 + b_kr0) * HW) * 4u;
+            const uint32_t step = (uint32_t)(B_KSTEP * HW) * 4u;
+            float* d0 = S + D::A_FLOATS + b_kr0 * T::BN + b_grp * 64;
 #pragma unroll
-            for (int i = 0; i < D::A_LOADS; ++i) dma_load16(rw, S + (wave + 4 * i) * 8 * 32, avo[i], sa);
-#pragma unroll
-            for (int i = 0; i < D::B_LOADS; ++i) {
-                const int kr = b_kr0 + B_KSTEP * i;
-                dma_load4(rin, S + D::A_FLOATS + kr * T::BN + b_grp * 64, bv, (uint32_t)((c0 + kr) * HW) * 4u);
-            }
+            for (int i = i_begin; i < i_end; ++i) dma_load4(rin, d0 + i * B_KSTEP * T::BN, bv, s0 + i * step);
         };
 
         floatx16 sum[T::TM][T::TN];
@@ -327,44 +337,40 @@ __global__ void __launch_bounds__(256, 2) conv_dma_k(ConvArgs a, StreamK sk) {
 
         int t = seg.kb / CB;
         int cb = seg.kb - t * CB;
-        issue(t, cb, lds);
+        issue_a(t, cb, lds, true);
+        issue_b(cb, lds, b_voff(t, true), 0, D::B_LOADS);
         wait_dma();
         __syncthreads();
-        f32x4 av[T::TM], bw[T::TN];
-        read_quad_dma<T>(lds, a_row, a_sw, lds + b_off, 0, av, bw);
+        // operands of quads 0 and 2 in set 0, quads 1 and 3 in set 1: the
+        // registers carried from one slice to the next (quad 0) stay put
+        f32x4 a0[T::TM], b0[T::TN], a1[T::TM], b1[T::TN];
+        read_quad_dma<T>(lds, a_row, a_sw, lds + b_off, 0, a0, b0);
         int stage = 0;
         for (int it = seg.kb; it < seg.ke; ++it) {
+            // next slice; past the segment's end its loads are no-ops
             const bool more = it + 1 < seg.ke;
+            const int cb1 = cb + 1 == CB ? 0 : cb + 1;
+            const int t1 = cb + 1 == CB ? t + 1 : t;
+            t = more ? t1 : t;
+            cb = more ? cb1 : cb;
             float* next = lds + (stage ^ 1) * D::STAGE;
-            if (more) {
-                if (++cb == CB) {
-                    cb = 0;
-                    ++t;
-                }
-                issue(t, cb, next);
-            }
             const float* S = lds + stage * D::STAGE;
-#pragma unroll
-            for (int q = 0; q < 3; ++q) {
-                f32x4 an[T::TM], bn[T::TN];
-                read_quad_dma<T>(S, a_row, a_sw, S + b_off, q + 1, an, bn);
-                mfma_quad<T>(av, bw, sum);
-#pragma unroll
-                for (int tm = 0; tm < T::TM; ++tm) av[tm] = an[tm];
-#pragma unroll
-                for (int tn = 0; tn < T::TN; ++tn) bw[tn] = bn[tn];
-            }
+            // the loads issue in two halves ahead of quads 0 and 1; quad 2
+            // leaves them time to land before the barrier
+            const uint32_t bv = b_voff(t, more);
+            issue_a(t, cb, next, more);
+            issue_b(cb, next, bv, 0, D::B_LOADS / 2);
+            read_quad_dma<T>(S, a_row, a_sw, S + b_off, 1, a1, b1);
+            mfma_quad<T>(a0, b0, sum);
+            issue_b(cb, next, bv, D::B_LOADS / 2, D::B_LOADS);
+            read_quad_dma<T>(S, a_row, a_sw, S + b_off, 2, a0, b0);
+            mfma_quad<T>(a1, b1, sum);
+            read_quad_dma<T>(S, a_row, a_sw, S + b_off, 3, a1, b1);
+            mfma_quad<T>(a0, b0, sum);
             wait_dma();
             __syncthreads();
-            f32x4 an[T::TM], bn[T::TN];
-            if (more) read_quad_dma<T>(next, a_row, a_sw, next + b_off, 0, an, bn);
-            mfma_quad<T>(av, bw, sum);
-            if (more) {
-#pragma unroll
-                for (int tm = 0; tm < T::TM; ++tm) av[tm] = an[tm];
-#pragma unroll
-                for (int tn = 0; tn < T::TN; ++tn) bw[tn] = bn[tn];
-            }
+            read_quad_dma<T>(next, a_row, a_sw, next + b_off, 0, a0, b0);
+            mfma_quad<T>(a1, b1, sum);
             stage ^= 1;
         }
         conv_segment_out<T>(a, seg, g, i0, j0, sum);
