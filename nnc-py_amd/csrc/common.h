@@ -22,6 +22,10 @@ struct Context {
     // split-K partials and other per-call scratch; grown outside capture only
     float* workspace = nullptr;
     size_t workspace_bytes = 0;
+    // per-tile arrival counters of the stream-K kernels; zero between kernels
+    // (each kernel returns the counters it used to zero)
+    int* counters = nullptr;
+    size_t counters_n = 0;
     bool capturing = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -45,6 +49,10 @@ bool hip_ok(hipError_t e, const char* who, const char* what);
 // (inside graph capture the workspace cannot grow).
 float* workspace(size_t bytes);
 size_t workspace_capacity();
+
+// At least `n` zeroed tile counters, or nullptr if they cannot be provided
+// (inside graph capture the buffer cannot grow). Kernels leave them zero.
+int* tile_counters(size_t n);
 
 // ---------------------------------------------------------------------------
 // kernel launch with optional hipEvent timing (keyed by kernel name)

@@ -40,6 +40,7 @@ struct ConvArgs {
     const float* res;  // residual added before the activation (nullable)
     float* out;
     float* ws;  // stream-K partial tiles
+    int* cnt;   // stream-K tile arrival counters (nullptr: conv_fixup_k finishes shared tiles)
     int N, Ci, H, W, Co, Ho, Wo, kh, kw, sh, sw, ph, pw;
     int K, Npix, act;
     int tiles_m, tiles_n;
@@ -128,11 +129,101 @@ struct ConvGather {
     }
 };
 
+// Bias (+ residual) + act for 4 consecutive output pixels p0..p0+3 of
+// channel co (one row of a tile), float4 when they are in one image and the
+// output (and residual) are 16-byte aligned.
+__device__ __forceinline__ void fixup_store(const ConvArgs& a, int co, int p0, float4 v) {
+    const int hw = a.Ho * a.Wo;
+    const float b = a.bias ? a.bias[co] : 0.f;
+    const int n = p0 / hw;
+    const int64_t o = ((int64_t)n * a.Co + co) * hw + (p0 - n * hw);
+    if (a.vec_out && (hw & 3) == 0 && p0 + 3 < a.Npix) {
+        float4 x = make_float4(v.x + b, v.y + b, v.z + b, v.w + b);
+        if (a.res) {
+            const float4 r = *reinterpret_cast<const float4*>(a.res + o);
+            x.x += r.x;
+            x.y += r.y;
+            x.z += r.z;
+            x.w += r.w;
+        }
+        *reinterpret_cast<float4*>(a.out + o) =
+            make_float4(activate(x.x, a.act), activate(x.y, a.act), activate(x.z, a.act), activate(x.w, a.act));
+        return;
+    }
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int pix = p0 + q;
+        if (pix >= a.Npix) break;
+        const int nq = pix / hw;
+        const int64_t oq = ((int64_t)nq * a.Co + co) * hw + (pix - nq * hw);
+        float x = vals[q] + b;
+        if (a.res) x += a.res[oq];
+        a.out[oq] = activate(x, a.act);
+    }
+}
+
+// Partial tiles are written and read with device-scope coherence (the
+// buffer instructions' sc1 bit: stores write through the XCD's L2, loads do
+// not hit a stale L2 line), so the workgroup that finishes a tile on another
+// XCD sees them once their writers' stores have completed - without an L2
+// writeback or invalidate.
+static constexpr int kDeviceScope = 16;
+
+template <class T>
+__device__ __forceinline__ uint32_t slot_byte_offset(int g, int which) {
+    return (uint32_t)((g * 2 + which) * (T::BM * T::BN)) * 4u;
+}
+
+// Shared stream-K tile t finished inside the kernel by the workgroup whose
+// partial arrived last: partials summed in workgroup order g0..g1 (the
+// order of conv_fixup_k, so the result is the same to the bit), then bias
+// (+ residual) + act.
+template <class T>
+__device__ void conv_finish_tile(const ConvArgs& a, int t, int g0, int g1, int first_slot) {
+    constexpr int E = T::BM * T::BN / 1024;  // float4 per thread
+    constexpr int CH = E < 8 ? E : 8;         // float4 in flight per partial (register budget)
+    const __amdgpu_buffer_rsrc_t rws = make_rsrc(a.ws);
+    const int mt = t % a.tiles_m, nt = t / a.tiles_m;
+    const uint32_t first = slot_byte_offset<T>(g0, first_slot);
+    for (int e0 = 0; e0 < E; e0 += CH) {
+        // a chunk of one partial's loads in flight at once, partial after partial
+        f32x4 v[CH];
+#pragma unroll
+        for (int e = 0; e < CH; ++e)
+            v[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rws, (int)(first + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u), 0,
+                                                 kDeviceScope));
+        for (int g = g0 + 1; g <= g1; ++g) {
+            const uint32_t base = slot_byte_offset<T>(g, 0);
+            f32x4 p[CH];
+#pragma unroll
+            for (int e = 0; e < CH; ++e)
+                p[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rws, (int)(base + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u),
+                                                     0, kDeviceScope));
+#pragma unroll
+            for (int e = 0; e < CH; ++e) v[e] += p[e];
+        }
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            const int e4 = (e0 + e) * 256 + threadIdx.x;
+            const int co = mt * T::BM + (e4 * 4) / T::BN;
+            const int p0 = nt * T::BN + (e4 * 4) % T::BN;
+            if (co < a.Co && p0 < a.Npix) fixup_store(a, co, p0, make_float4(v[e].x, v[e].y, v[e].z, v[e].w));
+        }
+    }
+}
+
 // Writes a finished segment: a whole tile straight to the output with bias
 // (+ residual) + act, or a partial tile to the workgroup's stream-K slot.
-template <class T>
-__device__ __forceinline__ void conv_segment_out(const ConvArgs& a, const Segment& seg, int g, int i0, int j0,
-                                                 const floatx16 (&sum)[T::TM][T::TN]) {
+// With tile counters (a.cnt) each writer of a partial then counts itself in
+// on the tile, and the last to arrive finishes the tile (no spinning: no
+// workgroup ever waits for another); the last arriver also returns the
+// counter to zero for the next kernel.
+template <class T, bool FIN>
+__device__ __forceinline__ void conv_segment_out(const ConvArgs& a, const StreamK& sk, const Segment& seg, int g,
+                                                 int i0, int j0, const floatx16 (&sum)[T::TM][T::TN]) {
     const int hw = a.Ho * a.Wo;
     if (seg.slot < 0) {
 #pragma unroll
@@ -153,7 +244,9 @@ __device__ __forceinline__ void conv_segment_out(const ConvArgs& a, const Segmen
                     }
                 }
         }
-    } else {
+        return;
+    }
+    if (!FIN || !a.cnt) {  // the fixup kernel reads the partials after this kernel
         float* slot = partial_slot<T>(a.ws, g, seg.slot);
 #pragma unroll
         for (int tn = 0; tn < T::TN; ++tn)
@@ -161,6 +254,40 @@ __device__ __forceinline__ void conv_segment_out(const ConvArgs& a, const Segmen
             for (int tm = 0; tm < T::TM; ++tm)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) slot[acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)] = sum[tm][tn][r];
+        return;
+    }
+    if constexpr (FIN) {
+        const __amdgpu_buffer_rsrc_t rws = make_rsrc(a.ws);
+        const uint32_t base = slot_byte_offset<T>(g, seg.slot);
+    #pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn)
+    #pragma unroll
+            for (int tm = 0; tm < T::TM; ++tm)
+    #pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    // copy the element first: this compiler's __builtin_bit_cast of
+                    // an ext-vector element reads the wrong element
+                    const float x = sum[tm][tn][r];
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(x), rws,
+                        (int)(base + (uint32_t)(acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)) * 4u), 0, kDeviceScope);
+                }
+        __shared__ int last;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int g0, g1, first_slot;
+            tile_partials(sk, seg.tile, g0, g1, first_slot);
+            const int old = __hip_atomic_fetch_add(a.cnt + seg.tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = old == g1 - g0;
+            if (last) __hip_atomic_store(a.cnt + seg.tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (last) {
+            int g0, g1, first_slot;
+            tile_partials(sk, seg.tile, g0, g1, first_slot);
+            conv_finish_tile<T>(a, seg.tile, g0, g1, first_slot);
+        }
     }
 }
 
@@ -183,41 +310,37 @@ __global__ void __launch_bounds__(256, 2) conv_streamk_k(ConvArgs a, StreamK sk)
         floatx16 sum[T::TM][T::TN];
         mfma_mainloop<T, false>(la, lb, seg.kb * T::BK, min(a.K, seg.ke * T::BK), lds, sum);
 
-        conv_segment_out<T>(a, seg, g, i0, j0, sum);
+        conv_segment_out<T, false>(a, sk, seg, g, i0, j0, sum);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Direct-to-LDS variant for Ci % 32 == 0 with weights packed tap-major,
-// [Co][kh][kw][Ci] (for 1x1 kernels that is the reference layout). K is
-// walked tap-major too: slice s covers one tap t and 32 consecutive input
-// channels c0..c0+31 (k = t*Ci + c), so within a slice the tap - and with
-// it each pixel's in-image test and offset - is uniform, and channels
-// differ by a wave-uniform stride (an SGPR offset). Operands go from global
-// memory straight into LDS (`buffer_load ... lds`, which writes lane l's
-// data to LDS[M0 + size * l]): no VGPR staging and no LDS store
-// instructions.
-//   A stage: [BM rows][32 k], 16-byte chunks XOR-swizzled (chunk kc of row
-//     x sits at position kc ^ (x & 7)). One dwordx4 load covers 8 rows x
-//     128 contiguous bytes of the packed weights; lane l takes row l / 8,
-//     position l % 8. An MFMA lane reads its four k of a quad as one
-//     ds_read_b128; eight consecutive rows hit eight different positions,
-//     so the reads are free of bank conflicts.
-//   B stage: [32 k][BN pixels]. One dword load covers 64 consecutive pixels
-//     of one (tap, channel): the gather coalesces along image rows. An MFMA
-//     lane reads its k one ds_read_b32 at a time (consecutive lanes,
-//     consecutive floats).
-// Out-of-range lanes (co >= Co, pixel >= Npix, tap outside the image) get an
-// out-of-range offset, and the hardware writes 0 to LDS.
+// Direct-to-LDS convolution. Operands go from global memory straight into
+// LDS (`buffer_load ... lds`, which writes lane l's data to LDS[M0 + size *
+// l]): no VGPR staging and no LDS store instructions. Stage layout:
+//   A: [BM rows][32 k], 16-byte chunks XOR-swizzled: chunk kc of row x sits
+//     at position kc ^ (x & 7). An MFMA lane reads its four k of a quad as
+//     one ds_read_b128, and eight consecutive rows hit eight different
+//     positions, so the reads are free of bank conflicts.
+//   B: [32 k][BN pixels]. One dword load covers 64 consecutive pixels of one
+//     k (one channel and tap), so the gather coalesces along image rows; an
+//     MFMA lane reads its k one ds_read_b32 at a time.
+// Out-of-range lanes (co >= Co, pixel >= Npix, tap outside the image, k >=
+// K) get an out-of-range offset, and the hardware writes 0 to LDS. The
+// loader (DmaPacked) needs Ci % 32 == 0 and weights packed tap-major
+// [Co][kh][kw][Ci] (for 1x1 kernels the reference layout). K is walked
+// tap-major: slice s is one tap t and 32 consecutive channels, so the tap -
+// and each pixel's in-image test and offset - is uniform over the slice and
+// channels differ by an SGPR offset. A: one dwordx4 load per 8 rows (lane l:
+// row l / 8, 16 bytes of the packed row).
 // ---------------------------------------------------------------------------
 template <class T>
 struct DmaStage {
     static constexpr int A_FLOATS = T::BM * 32, B_FLOATS = T::BN * 32;
     static constexpr int STAGE = A_FLOATS + B_FLOATS;
     static constexpr int LDS_FLOATS = 2 * STAGE;
-    static constexpr int A_LOADS = T::BM / 32;        // dwordx4 loads per wave per slice (8 rows each)
     static constexpr int PX_GROUPS = T::BN / 64;      // 64-pixel groups of a B row
-    static constexpr int B_LOADS = 32 / (4 / PX_GROUPS);  // dword loads per wave per slice
+    static constexpr int B_LOADS = 32 * PX_GROUPS / 4;  // dword loads per wave per slice
     static_assert(T::BM % 32 == 0 && (T::BN == 64 || T::BN == 128) && T::BK == 32, "dma tile");
 };
 
@@ -231,6 +354,101 @@ __device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, float* lds_
 
 // s_waitcnt vmcnt(0): the direct-to-LDS loads of this wave have landed
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// `addr` if `keep`, else exactly kOutOfRange (adding an SGPR offset below
+// 2^31 cannot wrap it back into range); without branches
+__device__ __forceinline__ uint32_t keep_or_oob(uint32_t addr, bool keep) {
+    const uint32_t m = 0u - (uint32_t)keep;
+    return (addr & m) | (kOutOfRange & ~m);
+}
+
+// Per-tile pixel data of the B loaders: this lane's pixel (one per wave's
+// 64-pixel group), element offset of its tap (0, 0) at channel 0, and the
+// taps inside the image as a bit mask.
+template <int KH, int KW>
+struct PixelTaps {
+    typedef typename std::conditional<(KH * KW > 32), uint64_t, uint32_t>::type Mask;
+    int bpo;
+    Mask mask;
+    __device__ void init(const ConvArgs& a, int px) {
+        const bool valid = px < a.Npix;
+        const int hw = a.Ho * a.Wo;
+        const int p = valid ? px : 0;
+        const int n = p / hw;
+        const int rem = p - n * hw;
+        const int oh = rem / a.Wo;
+        const int ow = rem - oh * a.Wo;
+        const int h0 = oh * a.sh - a.ph, w0 = ow * a.sw - a.pw;
+        bpo = n * a.Ci * (a.H * a.W) + h0 * a.W + w0;
+        mask = 0;
+#pragma unroll
+        for (int r = 0; r < KH; ++r)
+#pragma unroll
+            for (int c = 0; c < KW; ++c) {
+                const bool in = valid && (unsigned)(h0 + r) < (unsigned)a.H && (unsigned)(w0 + c) < (unsigned)a.W;
+                mask |= (Mask)in << (r * KW + c);
+            }
+    }
+    __device__ bool inside(int tap) const { return ((mask >> tap) & 1u) != 0; }
+};
+
+template <class T, int KH, int KW>
+struct DmaPacked {
+    typedef DmaStage<T> D;
+    static constexpr int A_LOADS = T::BM / 32;  // dwordx4 loads per wave per slice, 8 rows each
+    __amdgpu_buffer_rsrc_t rin, rw;
+    int wave, b_grp, b_kr0, CB, HW, W, Ci;
+    uint32_t avo[A_LOADS];
+    PixelTaps<KH, KW> px;
+    int t, cb;       // slice cursor: tap, 32-channel block
+    uint32_t bv;     // B offset of the slice being issued
+
+    __device__ void init(const ConvArgs& a, int wave_, int lane) {
+        rin = make_rsrc(a.in);
+        rw = make_rsrc(a.w);
+        wave = wave_;
+        b_grp = wave % D::PX_GROUPS;
+        b_kr0 = (wave / D::PX_GROUPS) * D::B_LOADS;
+        CB = a.Ci >> 5;
+        HW = a.H * a.W;
+        W = a.W;
+        Ci = a.Ci;
+    }
+    __device__ void tile(const ConvArgs& a, int i0, int j0, int lane) {
+        const int a_kc = (lane & 7) ^ ((lane >> 3) & 7);
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) {
+            const int co = i0 + (wave + 4 * i) * 8 + (lane >> 3);
+            avo[i] = keep_or_oob((uint32_t)(co * a.K) * 4u + (uint32_t)a_kc * 16u, co < a.Co);
+        }
+        px.init(a, j0 + b_grp * 64 + lane);
+    }
+    __device__ void begin(int kb) {
+        t = kb / CB;
+        cb = kb - t * CB;
+    }
+    __device__ void step(bool more) {
+        const int cb1 = cb + 1 == CB ? 0 : cb + 1;
+        const int t1 = cb + 1 == CB ? t + 1 : t;
+        t = more ? t1 : t;
+        cb = more ? cb1 : cb;
+    }
+    // part 0: A and the first half of B; part 1: the rest of B
+    __device__ void issue(float* S, bool on, int part) {
+        if (part == 0) {
+            const uint32_t sa = (uint32_t)(t * Ci + cb * 32) * 4u;
+#pragma unroll
+            for (int i = 0; i < A_LOADS; ++i) dma_load16(rw, S + (wave + 4 * i) * 8 * 32, on ? avo[i] : kOutOfRange, sa);
+            const int r = t / KW, c = t - r * KW;
+            bv = keep_or_oob((uint32_t)(px.bpo + r * W + c) * 4u, on && px.inside(t));
+        }
+        const uint32_t s0 = (uint32_t)((cb * 32 + b_kr0) * HW) * 4u;
+        float* d0 = S + D::A_FLOATS + b_kr0 * T::BN + b_grp * 64;
+        constexpr int H = D::B_LOADS / 2;
+#pragma unroll
+        for (int i = part * H; i < (part + 1) * H; ++i) dma_load4(rin, d0 + i * T::BN, bv, s0 + (uint32_t)(i * HW) * 4u);
+    }
+};
 
 // MFMA operands of quad q from a direct-to-LDS stage: A as one 16-byte read
 // per 32-row block, B as four single floats per 32-column block.
@@ -246,86 +464,27 @@ __device__ __forceinline__ void read_quad_dma(const float* Sa, int a_row, int a_
         for (int s = 0; s < 4; ++s) b[tn][s] = Sb[(4 * q + s) * T::BN + tn * 32];
 }
 
-template <class T, int KH, int KW>
+template <class T, class L, bool FIN>
 __global__ void __launch_bounds__(256, 2) conv_dma_k(ConvArgs a, StreamK sk) {
     typedef DmaStage<T> D;
     extern __shared__ __align__(16) float lds[];
     const int g = xcd_remap(blockIdx.x, sk.G);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int hw = a.Ho * a.Wo;
-    const int HW = a.H * a.W;
-    const int CB = a.Ci >> 5;  // 32-channel blocks per tap
-    const __amdgpu_buffer_rsrc_t rin = make_rsrc(a.in), rw = make_rsrc(a.w);
     // MFMA read side: A row and swizzled chunk of quad 0 (kc = 4h), B column
     const int wi = (wave / T::WN) * T::WAVE_M, wj = (wave % T::WN) * T::WAVE_N;
     const int a_row = wi + (lane & 31);
     const int a_sw = (4 * (lane >> 5)) ^ (lane & 7);
     const int b_off = D::A_FLOATS + 16 * (lane >> 5) * T::BN + wj + (lane & 31);
-    // load side: A rows (wave + 4i) * 8 + lane / 8, chunk (lane % 8) ^ (lane / 8);
-    // B pixel group wave % PX_GROUPS, k rows wave / PX_GROUPS + (4 / PX_GROUPS) * i
-    const int a_kc = (lane & 7) ^ ((lane >> 3) & 7);
-    const int b_grp = wave % D::PX_GROUPS;
-    const int b_kr0 = wave / D::PX_GROUPS;
-    constexpr int B_KSTEP = 4 / D::PX_GROUPS;
+    L ld;
+    ld.init(a, wave, lane);
 
     SegmentWalker walk(sk, g);
     Segment seg;
     while (walk.next(sk, seg)) {
         const int mt = seg.tile % a.tiles_m, nt = seg.tile / a.tiles_m;
         const int i0 = mt * T::BM, j0 = nt * T::BN;
-        uint32_t avo[D::A_LOADS];
-#pragma unroll
-        for (int i = 0; i < D::A_LOADS; ++i) {
-            const int co = i0 + (wave + 4 * i) * 8 + (lane >> 3);
-            avo[i] = co < a.Co ? (uint32_t)(co * a.K) * 4u + (uint32_t)a_kc * 16u : kOutOfRange;
-        }
-        // this lane's pixel: element offset of tap (0, 0) at channel 0, and
-        // the taps that fall inside the image
-        const int px = j0 + b_grp * 64 + lane;
-        const bool valid = px < a.Npix;
-        int bpo;
-        uint32_t bmask = 0;
-        {
-            const int p = valid ? px : 0;
-            const int n = p / hw;
-            const int rem = p - n * hw;
-            const int oh = rem / a.Wo;
-            const int ow = rem - oh * a.Wo;
-            const int h0 = oh * a.sh - a.ph, w0 = ow * a.sw - a.pw;
-            bpo = n * a.Ci * HW + h0 * a.W + w0;
-#pragma unroll
-            for (int r = 0; r < KH; ++r)
-#pragma unroll
-                for (int c = 0; c < KW; ++c) {
-                    const bool in = valid && (unsigned)(h0 + r) < (unsigned)a.H && (unsigned)(w0 + c) < (unsigned)a.W;
-                    bmask |= (uint32_t)in << (r * KW + c);
-                }
-        }
-        // loads of slice (t, cb) into stage S; with `on` false every load gets
-        // an out-of-range offset (no memory access, zeros into the stage)
-        auto issue_a = [&](int t, int cb, float* S, bool on) {
-            const uint32_t sa = (uint32_t)(t * a.Ci + cb * 32) * 4u;
-#pragma unroll
-            for (int i = 0; i < D::A_LOADS; ++i)
-                dma_load16(rw, S + (wave + 4 * i) * 8 * 32, on ? avo[i] : kOutOfRange, sa);
-        };
-        // this lane's B offset for tap t: out of range (exactly kOutOfRange, so
-        // adding the SGPR offset cannot wrap) if the tap is outside the image
-        // or `on` is false; computed without branches
-        auto b_voff = [&](int t, bool on) {
-            const int r = t / KW, c = t - r * KW;
-            const uint32_t addr = (uint32_t)(bpo + r * a.W + c) * 4u;
-            const uint32_t keep = 0u - (((bmask >> t) & 1u) & (uint32_t)on);
-            return (addr & keep) | (kOutOfRange & ~keep);
-        };
-        auto issue_b = [&](int cb, float* S, uint32_t bv, int i_begin, int i_end) {
-            const uint32_t s0 = (uint32_t)((cb * 32 + b_kr0) * HW) * 4u;
-            const uint32_t step = (uint32_t)(B_KSTEP * HW) * 4u;
-            float* d0 = S + D::A_FLOATS + b_kr0 * T::BN + b_grp * 64;
-#pragma unroll
-            for (int i = i_begin; i < i_end; ++i) dma_load4(rin, d0 + i * B_KSTEP * T::BN, bv, s0 + i * step);
-        };
+        ld.tile(a, i0, j0, lane);
 
         floatx16 sum[T::TM][T::TN];
 #pragma unroll
@@ -335,10 +494,9 @@ __global__ void __launch_bounds__(256, 2) conv_dma_k(ConvArgs a, StreamK sk) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) sum[tm][tn][r] = 0.f;
 
-        int t = seg.kb / CB;
-        int cb = seg.kb - t * CB;
-        issue_a(t, cb, lds, true);
-        issue_b(cb, lds, b_voff(t, true), 0, D::B_LOADS);
+        ld.begin(seg.kb);
+        ld.issue(lds, true, 0);
+        ld.issue(lds, true, 1);
         wait_dma();
         __syncthreads();
         // operands of quads 0 and 2 in set 0, quads 1 and 3 in set 1: the
@@ -349,20 +507,15 @@ __global__ void __launch_bounds__(256, 2) conv_dma_k(ConvArgs a, StreamK sk) {
         for (int it = seg.kb; it < seg.ke; ++it) {
             // next slice; past the segment's end its loads are no-ops
             const bool more = it + 1 < seg.ke;
-            const int cb1 = cb + 1 == CB ? 0 : cb + 1;
-            const int t1 = cb + 1 == CB ? t + 1 : t;
-            t = more ? t1 : t;
-            cb = more ? cb1 : cb;
+            ld.step(more);
             float* next = lds + (stage ^ 1) * D::STAGE;
             const float* S = lds + stage * D::STAGE;
             // the loads issue in two halves ahead of quads 0 and 1; quad 2
             // leaves them time to land before the barrier
-            const uint32_t bv = b_voff(t, more);
-            issue_a(t, cb, next, more);
-            issue_b(cb, next, bv, 0, D::B_LOADS / 2);
+            ld.issue(next, more, 0);
             read_quad_dma<T>(S, a_row, a_sw, S + b_off, 1, a1, b1);
             mfma_quad<T>(a0, b0, sum);
-            issue_b(cb, next, bv, D::B_LOADS / 2, D::B_LOADS);
+            ld.issue(next, more, 1);
             read_quad_dma<T>(S, a_row, a_sw, S + b_off, 2, a0, b0);
             mfma_quad<T>(a1, b1, sum);
             read_quad_dma<T>(S, a_row, a_sw, S + b_off, 3, a1, b1);
@@ -373,7 +526,7 @@ __global__ void __launch_bounds__(256, 2) conv_dma_k(ConvArgs a, StreamK sk) {
             mfma_quad<T>(a1, b1, sum);
             stage ^= 1;
         }
-        conv_segment_out<T>(a, seg, g, i0, j0, sum);
+        conv_segment_out<T, FIN>(a, sk, seg, g, i0, j0, sum);
     }
 }
 
@@ -415,35 +568,13 @@ __global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
         v.z += p.z;
         v.w += p.w;
     }
-    const int hw = a.Ho * a.Wo;
-    const float b = a.bias ? a.bias[co] : 0.f;
-    const int n = p0 / hw;
-    const int64_t o = ((int64_t)n * a.Co + co) * hw + (p0 - n * hw);
-    if (a.vec_out && (hw & 3) == 0 && p0 + 3 < a.Npix) {
-        float4 x = make_float4(v.x + b, v.y + b, v.z + b, v.w + b);
-        if (a.res) {
-            const float4 r = *reinterpret_cast<const float4*>(a.res + o);
-            x.x += r.x;
-            x.y += r.y;
-            x.z += r.z;
-            x.w += r.w;
-        }
-        *reinterpret_cast<float4*>(a.out + o) =
-            make_float4(activate(x.x, a.act), activate(x.y, a.act), activate(x.z, a.act), activate(x.w, a.act));
-        return;
-    }
-    const float vals[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int pix = p0 + q;
-        if (pix >= a.Npix) break;
-        const int nq = pix / hw;
-        const int64_t oq = ((int64_t)nq * a.Co + co) * hw + (pix - nq * hw);
-        float x = vals[q] + b;
-        if (a.res) x += a.res[oq];
-        a.out[oq] = activate(x, a.act);
-    }
+    fixup_store(a, co, p0, v);
 }
+
+// direct-to-LDS kernels finish shared stream-K tiles themselves when a tile
+// has at most kMaxInKernelParts partials
+static constexpr bool kInKernelFixup = true;
+static constexpr int kMaxInKernelParts = 4;
 
 typedef Tile<128, 128, 32, 2, 2> ConvT128;  // Co >= 128: 2x2 blocks per wave
 typedef Tile<64, 128, 32, 1, 4> ConvT64;    // Co == 64, many pixels: 2x1 blocks per wave
@@ -484,9 +615,13 @@ static void launch_conv_t(ConvArgs& a, const char* entry) {
     }
 }
 
-template <class T, int KH, int KW>
-static void launch_conv_dma_t(ConvArgs& a, const char* entry) {
-    auto kernel = conv_dma_k<T, KH, KW>;
+template <class T, class L>
+static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) {
+    // the in-kernel finish only where it measured faster than the fixup
+    // kernel (64x128 tiles: ResNet's 64-channel layers); elsewhere its code
+    // costs the main loop registers
+    constexpr bool FIN = kInKernelFixup && T::BM == 64 && T::BN == 128;
+    auto kernel = conv_dma_k<T, L, FIN>;
     const size_t lds = (size_t)DmaStage<T>::LDS_FLOATS * sizeof(float);
     static bool configured = false;
     static int slots = 0;
@@ -498,31 +633,45 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry) {
         slots = resident_groups(kernel, lds);
         configured = true;
     }
-    const int iters = a.K / T::BK;  // Ci % 32 == 0: whole slices
+    // K == 0 (no input channels) still runs one empty slice so the epilogue
+    // writes act(bias)
+    const int iters = a.K > 0 ? (int)ceil_div(a.K, T::BK) : 1;
     const StreamK sk = plan_streamk(a.tiles_m * a.tiles_n, iters, slots, fixup_slices<T>());
     if (sk.G < 1) return;
     float* ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
     if (!ws) return fail(NNC_HIP_ENOMEM, entry, "no workspace for stream-K partials");
     a.ws = ws;
-    char name[64];
-    snprintf(name, sizeof name, "conv_igemm_%dx%d_k%dx%d_dma", T::BM, T::BN, KH, KW);
+    // shared tiles with at most kMaxInKernelParts contributors are finished
+    // inside the kernel by the last to arrive; tiles split further (short
+    // problems) by the fixup kernel, which spreads the sum over many
+    // workgroups; so also when no counters can be had (capture before growth)
+    const int64_t per = sk.total() / sk.G;  // slices per workgroup range (>= 1)
+    const bool in_kernel = FIN && sk.needs_fixup() && (sk.iters + per - 1) / per + 1 <= kMaxInKernelParts;
+    a.cnt = in_kernel ? tile_counters((size_t)sk.sk_tiles) : nullptr;
     set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
     launch(name, kernel, dim3(sk.G), dim3(256), lds, a, sk);
-    if (sk.needs_fixup()) {
+    if (sk.needs_fixup() && !a.cnt) {
         set_work(0.0, 0.0);
         launch("conv_streamk_fixup", conv_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, a, sk);
     }
 }
 
-// `dma`: weights are tap-major [Co][kh][kw][Ci] (or 1x1), Ci % 32 == 0, kernel
-// 1x1 or 3x3 and weights 16-byte aligned; checked by the caller.
+template <class T, int KH, int KW>
+static void launch_conv_dma(ConvArgs& a, const char* entry) {
+    char name[64];
+    snprintf(name, sizeof name, "conv_igemm_%dx%d_k%dx%d_dma", T::BM, T::BN, KH, KW);
+    launch_conv_dma_t<T, DmaPacked<T, KH, KW>>(a, entry, name);
+}
+
+// `dma`: weights tap-major [Co][kh][kw][Ci] (or 1x1), Ci % 32 == 0, kernel
+// 1x1 or 3x3, weights 16-byte aligned; checked by the caller.
 template <class T>
 static void launch_conv(ConvArgs& a, bool avec, bool dma, const char* entry) {
     a.tiles_m = (int)ceil_div(a.Co, T::BM);
     a.tiles_n = (int)ceil_div(a.Npix, T::BN);
     if (dma) {
-        if (a.kh == 3) return launch_conv_dma_t<T, 3, 3>(a, entry);
-        return launch_conv_dma_t<T, 1, 1>(a, entry);
+        if (a.kh == 3) return launch_conv_dma<T, 3, 3>(a, entry);
+        return launch_conv_dma<T, 1, 1>(a, entry);
     }
 #define NNC_CONV_KS(KH, KW)                                                 \
     if (avec) launch_conv_t<T, KH, KW, true>(a, entry);                     \

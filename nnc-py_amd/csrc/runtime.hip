@@ -68,6 +68,28 @@ float* workspace(size_t bytes) {
 
 size_t workspace_capacity() { return g_ctx.workspace_bytes; }
 
+static const size_t kDefaultCounters = 1u << 16;
+
+int* tile_counters(size_t n) {
+    if (n <= g_ctx.counters_n) return g_ctx.counters;
+    if (g_ctx.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(g_ctx.stream), "tile_counters", "hipStreamSynchronize")) return nullptr;
+    if (g_ctx.counters) (void)hipFree(g_ctx.counters);
+    g_ctx.counters = nullptr;
+    g_ctx.counters_n = 0;
+    const size_t want = n < kDefaultCounters ? kDefaultCounters : n;
+    void* p = nullptr;
+    if (!hip_ok(hipMalloc(&p, want * sizeof(int)), "tile_counters", "hipMalloc")) return nullptr;
+    if (!hip_ok(hipMemsetAsync(p, 0, want * sizeof(int), g_ctx.stream), "tile_counters", "hipMemsetAsync") ||
+        !hip_ok(hipStreamSynchronize(g_ctx.stream), "tile_counters", "hipStreamSynchronize")) {
+        (void)hipFree(p);
+        return nullptr;
+    }
+    g_ctx.counters = static_cast<int*>(p);
+    g_ctx.counters_n = want;
+    return g_ctx.counters;
+}
+
 // ---------------------------------------------------------------------------
 // per-kernel timing
 // ---------------------------------------------------------------------------
@@ -165,6 +187,7 @@ int nnc_hip_init(int device) {
         return NNC_HIP_EDEVICE;
     c.device = device;
     if (!workspace(kDefaultWorkspace)) return NNC_HIP_ENOMEM;
+    if (!tile_counters(kDefaultCounters)) return NNC_HIP_ENOMEM;
     return NNC_HIP_OK;
 }
 
@@ -182,6 +205,7 @@ void nnc_hip_shutdown(void) {
     g_event_pool.clear();
     if (c.arena) (void)hipFree(c.arena);
     if (c.workspace) (void)hipFree(c.workspace);
+    if (c.counters) (void)hipFree(c.counters);
     (void)hipStreamDestroy(c.stream);
     g_ctx = Context{};
 }
