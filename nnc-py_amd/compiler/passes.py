@@ -150,12 +150,13 @@ CONV_OPS = ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu")
 
 
 def pack_conv_weights(g: Graph) -> int:
-    """mi355x target, O3: 3x3 convolutions with Ci % 32 == 0 whose weight is
-    a constant used only there get the weight transposed at compile time
-    from [Co][Ci][kh][kw] to tap-major [Co][kh][kw][Ci] and are lowered to
-    nnc_hip_conv_packed, whose kernels stream that layout straight into LDS.
-    1x1 weights already have that layout and keep their reference entry
-    points (which take the same kernels)."""
+    """mi355x target, O3: convolutions whose weight is a constant used only
+    there get the weight transposed at compile time to tap-major order and
+    are lowered to nnc_hip_conv_packed, whose kernels stream that layout
+    straight into LDS: 3x3 kernels with Ci % 32 == 0 as [Co][kh][kw][Ci],
+    the 3-channel 7x7 stem as [Co][Kp] (rows of K = 147 tap-major values
+    zero-padded to 160). 1x1 weights already have the tap-major layout and
+    keep their reference entry points (which take the same kernels)."""
     packed = 0
     for node in g.nodes:
         if node.op_type not in CONV_OPS or len(node.inputs) < 2:
@@ -166,11 +167,20 @@ def pack_conv_weights(g: Graph) -> int:
         if not w.is_constant or w.data is None or w.data.ndim != 4 or len(g.consumers(wname)) != 1:
             continue
         co, ci, kh, kw = w.data.shape
-        if (kh, kw) != (3, 3) or ci % 32 or len(x.shape) != 4 or x.shape[1] != ci:
+        if len(x.shape) != 4 or x.shape[1] != ci:
             continue
         if int(node.attrs.get("group", 1)) != 1 or list(node.attrs.get("dilations", [1, 1])) != [1, 1]:
             continue
-        w.data = np.ascontiguousarray(w.data.transpose(0, 2, 3, 1))
+        tap_major = w.data.transpose(0, 2, 3, 1)
+        if (kh, kw) == (7, 7) and ci == 3:
+            k = kh * kw * ci
+            rows = np.zeros((co, (k + 31) // 32 * 32), w.data.dtype)
+            rows[:, :k] = tap_major.reshape(co, k)
+            w.data = rows
+        elif (kh, kw) == (3, 3) and ci % 32 == 0:
+            w.data = np.ascontiguousarray(tap_major)
+        else:
+            continue
         w.shape = tuple(w.data.shape)
         node.attrs["kernel_shape"] = [kh, kw]
         node.metadata.setdefault("lowering", {})["weight_pack"] = "tap_major"

@@ -43,6 +43,7 @@ struct ConvArgs {
     int* cnt;   // stream-K tile arrival counters (nullptr: conv_fixup_k finishes shared tiles)
     int N, Ci, H, W, Co, Ho, Wo, kh, kw, sh, sw, ph, pw;
     int K, Npix, act;
+    int ldw;  // weight row stride in floats (packed weights may pad K)
     int tiles_m, tiles_n;
     int vec_out;  // out (and res) 16-byte aligned: the fixup may store float4
 };
@@ -395,6 +396,7 @@ struct PixelTaps {
 template <class T, int KH, int KW>
 struct DmaPacked {
     typedef DmaStage<T> D;
+    static constexpr bool kFinishInKernel = true;
     static constexpr int A_LOADS = T::BM / 32;  // dwordx4 loads per wave per slice, 8 rows each
     __amdgpu_buffer_rsrc_t rin, rw;
     int wave, b_grp, b_kr0, CB, HW, W, Ci;
@@ -419,7 +421,7 @@ struct DmaPacked {
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
             const int co = i0 + (wave + 4 * i) * 8 + (lane >> 3);
-            avo[i] = keep_or_oob((uint32_t)(co * a.K) * 4u + (uint32_t)a_kc * 16u, co < a.Co);
+            avo[i] = keep_or_oob((uint32_t)(co * a.ldw) * 4u + (uint32_t)a_kc * 16u, co < a.Co);
         }
         px.init(a, j0 + b_grp * 64 + lane);
     }
@@ -447,6 +449,64 @@ struct DmaPacked {
         constexpr int H = D::B_LOADS / 2;
 #pragma unroll
         for (int i = part * H; i < (part + 1) * H; ++i) dma_load4(rin, d0 + i * T::BN, bv, s0 + (uint32_t)(i * HW) * 4u);
+    }
+};
+
+// Few input channels (the RGB stem): weights packed [Co][Kp], k = tap * CI +
+// ci tap-major, zero past K = kh*kw*CI up to Kp, a multiple of 32. A as in
+// DmaPacked; each B load is one k, whose tap and channel are uniform (the
+// divisions by compile-time constants run on the scalar unit), and each lane
+// applies its pixel's in-image test for that tap.
+template <class T, int KH, int KW, int CI>
+struct DmaSmallC {
+    typedef DmaStage<T> D;
+    // (the in-kernel finish's registers would cost this kernel occupancy)
+    static constexpr bool kFinishInKernel = false;
+    static constexpr int A_LOADS = T::BM / 32;
+    __amdgpu_buffer_rsrc_t rin, rw;
+    int wave, b_grp, b_kr0, HW, W, K;
+    uint32_t avo[A_LOADS];
+    PixelTaps<KH, KW> px;
+    int k0;  // slice cursor
+
+    __device__ void init(const ConvArgs& a, int wave_, int lane) {
+        rin = make_rsrc(a.in);
+        rw = make_rsrc(a.w);
+        wave = wave_;
+        b_grp = wave % D::PX_GROUPS;
+        b_kr0 = (wave / D::PX_GROUPS) * D::B_LOADS;
+        HW = a.H * a.W;
+        W = a.W;
+        K = a.K;
+    }
+    __device__ void tile(const ConvArgs& a, int i0, int j0, int lane) {
+        const int a_kc = (lane & 7) ^ ((lane >> 3) & 7);
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) {
+            const int co = i0 + (wave + 4 * i) * 8 + (lane >> 3);
+            avo[i] = keep_or_oob((uint32_t)(co * a.ldw) * 4u + (uint32_t)a_kc * 16u, co < a.Co);
+        }
+        px.init(a, j0 + b_grp * 64 + lane);
+    }
+    __device__ void begin(int kb) { k0 = kb * 32; }
+    __device__ void step(bool more) { k0 += more ? 32 : 0; }
+    __device__ void issue(float* S, bool on, int part) {
+        if (part == 0) {
+#pragma unroll
+            for (int i = 0; i < A_LOADS; ++i)
+                dma_load16(rw, S + (wave + 4 * i) * 8 * 32, on ? avo[i] : kOutOfRange, (uint32_t)k0 * 4u);
+        }
+        constexpr int H = D::B_LOADS / 2;
+        float* d0 = S + D::A_FLOATS + b_kr0 * T::BN + b_grp * 64;
+#pragma unroll
+        for (int i = part * H; i < (part + 1) * H; ++i) {
+            const int k = k0 + b_kr0 + i;  // uniform
+            const bool kin = k < K;
+            const int tap = k / CI, ci = k - tap * CI;
+            const int r = tap / KW, c = tap - r * KW;
+            const uint32_t v = keep_or_oob((uint32_t)(px.bpo + r * W + c) * 4u, on && kin && px.inside(tap));
+            dma_load4(rin, d0 + i * T::BN, v, kin ? (uint32_t)(ci * HW) * 4u : 0u);
+        }
     }
 };
 
@@ -620,7 +680,7 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
     // the in-kernel finish only where it measured faster than the fixup
     // kernel (64x128 tiles: ResNet's 64-channel layers); elsewhere its code
     // costs the main loop registers
-    constexpr bool FIN = kInKernelFixup && T::BM == 64 && T::BN == 128;
+    constexpr bool FIN = kInKernelFixup && T::BM == 64 && T::BN == 128 && L::kFinishInKernel;
     auto kernel = conv_dma_k<T, L, FIN>;
     const size_t lds = (size_t)DmaStage<T>::LDS_FLOATS * sizeof(float);
     static bool configured = false;
@@ -663,6 +723,15 @@ static void launch_conv_dma(ConvArgs& a, const char* entry) {
     launch_conv_dma_t<T, DmaPacked<T, KH, KW>>(a, entry, name);
 }
 
+template <class T>
+static void launch_conv_stem(ConvArgs& a, const char* entry) {
+    a.tiles_m = (int)ceil_div(a.Co, T::BM);
+    a.tiles_n = (int)ceil_div(a.Npix, T::BN);
+    char name[64];
+    snprintf(name, sizeof name, "conv_igemm_%dx%d_k7x7c3_dma", T::BM, T::BN);
+    launch_conv_dma_t<T, DmaSmallC<T, 7, 7, 3>>(a, entry, name);
+}
+
 // `dma`: weights tap-major [Co][kh][kw][Ci] (or 1x1), Ci % 32 == 0, kernel
 // 1x1 or 3x3, weights 16-byte aligned; checked by the caller.
 template <class T>
@@ -703,6 +772,18 @@ static bool conv_check(Tensor* in, Tensor* w, Tensor* out, const char* name) {
         return false;
     }
     return true;
+}
+
+// nnc_hip_conv_packed: weights [Co][kh][kw][Ci] or [Co][Kp]
+static bool conv_check_packed(Tensor* in, Tensor* w, Tensor* out, const char* name) {
+    if (w && w->shape && w->ndim == 2) {
+        int64_t shape4[4] = {w->shape[0], w->shape[1], 1, 1};
+        Tensor w4 = *w;
+        w4.ndim = 4;
+        w4.shape = shape4;
+        return conv_check(in, &w4, out, name);
+    }
+    return conv_check(in, w, out, name);
 }
 
 // `packed`: the weights are [Co][kh][kw][Ci] (nnc_hip_conv_packed)
@@ -748,11 +829,22 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     if (K >= (1 << 30) || npix >= (1 << 30) || in_bytes >= ((int64_t)1 << 31) || w_bytes >= ((int64_t)1 << 31))
         return fail(NNC_HIP_EUNSUPP, name, "input or weights of 2 GiB or more");
     a.K = (int)K;
+    a.ldw = (int)K;
     a.Npix = (int)npix;
     a.vec_out = aligned16(a.out) && (!a.res || aligned16(a.res));
     // direct-to-LDS kernels: tap-major weights (1x1 weights already are)
     const bool dma_ok = a.Ci % 32 == 0 && aligned16(a.w) && ((kh == 3 && kw == 3) || (kh == 1 && kw == 1));
-    if (packed) {
+    bool stem = false;
+    if (packed && w->ndim == 2) {
+        // [Co][Kp], K padded with zeros to a multiple of 32: the RGB 7x7 stem
+        const int64_t kp = (K + 31) / 32 * 32;
+        if (w->shape[1] != kp) return fail(NNC_HIP_EINVAL, name, "packed weight row is not K rounded up to 32");
+        if (!(kh == 7 && kw == 7 && a.Ci == 3 && aligned16(a.w)))
+            return fail(NNC_HIP_EUNSUPP, name, "[Co][Kp] packed weights need a 7x7 kernel, 3 channels, alignment");
+        if (a.Co * kp * 4 >= ((int64_t)1 << 31)) return fail(NNC_HIP_EUNSUPP, name, "weights of 2 GiB or more");
+        a.ldw = (int)kp;
+        stem = true;
+    } else if (packed) {
         if (w->shape[1] != kh || w->shape[2] != kw || w->shape[3] != a.Ci)
             return fail(NNC_HIP_EINVAL, name, "packed weight shape is not [Co][kh][kw][Ci]");
         if (!dma_ok)
@@ -761,6 +853,11 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     }
     const bool dma = dma_ok && (packed || (kh == 1 && kw == 1));
     if (a.N == 0 || a.Co == 0 || a.Ho <= 0 || a.Wo <= 0) return;
+    if (stem) {
+        if (a.Co <= 64 && a.Npix >= 4096)
+            return launch_conv_stem<ConvT64>(a, name);
+        return launch_conv_stem<ConvTSmall>(a, name);
+    }
     const bool avec = (a.K % 4 == 0) && aligned16(a.w);
     // Tile choice (measured on ResNet-18 layers at batch 1 and 32): big tiles
     // pay off only for long contractions with enough output tiles; short
@@ -833,15 +930,16 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
 }
 
 // No reference counterpart: convolution with weights packed tap-major,
-// [Co][kh][kw][Ci], emitted by the mi355x target at O3 (the compiler packs
-// the constant). out = act(conv(in, w) + bias (+ res)), act 0 none, 1 relu,
-// 2 sigmoid; `b` and `res` may be NULL, `res` may be the same buffer as
-// `out`. Needs Ci % 32 == 0, a 1x1 or 3x3 kernel and 16-byte aligned
-// weights (NNC_HIP_EUNSUPP otherwise).
+// emitted by the mi355x target at O3 (the compiler packs the constant):
+// [Co][kh][kw][Ci] with Ci % 32 == 0 and a 1x1 or 3x3 kernel, or [Co][Kp]
+// for the 3-channel 7x7 stem (k = tap * Ci + ci, zero up to Kp = K rounded
+// up to 32). out = act(conv(in, w) + bias (+ res)), act 0 none, 1 relu, 2
+// sigmoid; `b` and `res` may be NULL, `res` may be the same buffer as `out`.
+// Weights 16-byte aligned; other shapes give NNC_HIP_EUNSUPP.
 void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh, int sw,
                          int ph, int pw, int act) {
     const char* name = "nnc_hip_conv_packed";
-    if (!conv_check(in, w, out, name)) return;
+    if (!conv_check_packed(in, w, out, name)) return;
     if (res && (!res->data || !res->shape)) return fail(NNC_HIP_EINVAL, name, "NULL residual data");
     if (act < kActNone || act > kActSigmoid) return fail(NNC_HIP_EINVAL, name, "act must be 0, 1 or 2");
     conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, act, name, res, true);

@@ -952,7 +952,8 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
 
 /* ------------------------------------------------------------------------
  * Packed-weight convolution of the mi355x target (include/nnc_hip.h), no
- * reference counterpart: the weights [Co][kh][kw][Ci] are unpacked to the
+ * reference counterpart: the weights, [Co][kh][kw][Ci] or [Co][Kp] (rows of
+ * K = kh*kw*Ci tap-major values padded to Kp), are unpacked to the
  * reference layout [Co][Ci][kh][kw], then nnc_conv into a temporary
  * (ops.c:720-1050) followed by the element-wise op that applies residual and
  * activation: nnc_add / nnc_add_relu / nnc_add_sigmoid with `res`
@@ -961,8 +962,9 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
  * ---------------------------------------------------------------------- */
 void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,
                          int sw, int ph, int pw, int act) {
-    if (!in || !w || !out || w->ndim != 4 || in->ndim != 4) return;
+    if (!in || !w || !out || (w->ndim != 4 && w->ndim != 2) || in->ndim != 4) return;
     const int64_t co = w->shape[0], ci = in->shape[1], taps = (int64_t)kh * kw;
+    const int64_t row = w->ndim == 2 ? w->shape[1] : taps * ci;
     const int64_t n = numel(out);
     float* wt = (float*)malloc((size_t)(co * ci * taps > 0 ? co * ci * taps : 1) * sizeof(float));
     float* tmp = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
@@ -974,7 +976,7 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
     const float* wp = (const float*)w->data;
     for (int64_t o = 0; o < co; ++o)
         for (int64_t t = 0; t < taps; ++t)
-            for (int64_t c = 0; c < ci; ++c) wt[(o * ci + c) * taps + t] = wp[(o * taps + t) * ci + c];
+            for (int64_t c = 0; c < ci; ++c) wt[(o * ci + c) * taps + t] = wp[o * row + t * ci + c];
     int64_t wshape[4] = {co, ci, kh, kw};
     Tensor wu = *w;
     wu.data = wt;

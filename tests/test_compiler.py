@@ -69,18 +69,21 @@ def test_o3_fusion_and_prepack_on_resnet18(pkg):
     ops = [c.op for c in prog.calls]
     assert len(ops) == 23  # Flatten is an alias of the pooled tensor: no call
     assert "nnc_flatten" not in ops and prog.plan.aliases
-    assert ops.count("nnc_hip_conv_packed") == 16
+    assert ops.count("nnc_hip_conv_packed") == 17  # the stem and every 3x3 conv
     assert "nnc_add_relu" not in ops and "nnc_relu" not in ops
-    assert ops[0] == "nnc_conv_relu7x7_s2" and ops.count("nnc_conv1x1") == 3
+    assert ops[0] == "nnc_hip_conv_packed" and ops.count("nnc_conv1x1") == 3
     assert ops[-1] == "nnc_gemm_nt"
     with_res = [c for c in prog.calls if c.op == "nnc_hip_conv_packed" and c.args[3][0] == "t"]
     assert len(with_res) == 8
     for c in prog.calls:
         if c.op != "nnc_hip_conv_packed":
             continue
-        assert c.args[-1] == ("i", 1)  # relu after every 3x3 conv of ResNet-18
+        assert c.args[-1] == ("i", 1)  # relu after every conv of ResNet-18 but the 1x1
         w = prog.graph.tensors[c.args[1][1]]
-        assert w.shape[1:3] == (3, 3) and w.shape[3] % 32 == 0  # [Co][kh][kw][Ci]
+        if c.args[5] == ("i", 7):
+            assert w.shape == (64, 160)  # [Co][Kp]: 7*7*3 = 147 padded to 160
+        else:
+            assert w.shape[1:3] == (3, 3) and w.shape[3] % 32 == 0  # [Co][kh][kw][Ci]
         if c.args[3][0] == "t":
             res, out = c.args[3][1], c.args[4][1]
             assert prog.graph.tensors[res].shape == prog.graph.tensors[out].shape
@@ -97,9 +100,15 @@ def test_packed_conv_weights_are_the_transposed_constants(pkg):
     for c in prog.calls:
         if c.op == "nnc_hip_conv_packed":
             name = c.args[1][1]
-            np.testing.assert_array_equal(prog.graph.tensors[name].data, orig[name].transpose(0, 2, 3, 1))
+            packed, w = prog.graph.tensors[name].data, orig[name]
+            if packed.ndim == 2:  # [Co][Kp]: tap-major rows, zero past K
+                k = w[0].size
+                np.testing.assert_array_equal(packed[:, :k], w.transpose(0, 2, 3, 1).reshape(w.shape[0], k))
+                assert not packed[:, k:].any() and packed.shape[1] % 32 == 0
+            else:
+                np.testing.assert_array_equal(packed, w.transpose(0, 2, 3, 1))
             n += 1
-    assert n == 16
+    assert n == 17
 
 
 def test_target_rewrites_can_be_switched_off(pkg):
@@ -114,6 +123,7 @@ def test_target_rewrites_can_be_switched_off(pkg):
         ops = [c.op for c in prog.calls]
         assert len(ops) == 23 and ops.count("nnc_hip_conv_add_relu") == 8
         assert ops.count("nnc_conv_relu3x3_s1") == 5  # conv1 of the five stride-1 blocks
+        assert ops[0] == "nnc_conv_relu7x7_s2"
         ex_mod.RESIDUAL_FUSION = False
         prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
         ops = [c.op for c in prog.calls]

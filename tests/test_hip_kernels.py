@@ -171,6 +171,22 @@ def test_conv_packed_shapes(shape, hip, dmem, abi, oracle_lib):
     _check(got, exp, case["name"])
 
 
+@pytest.mark.parametrize("n,h", [(2, 64), (1, 224), (3, 37)])
+def test_conv_packed_stem(n, h, hip, dmem, abi, oracle_lib):
+    """3-channel 7x7 stride-2 stem on [Co][Kp] rows (K = 147 padded to 160):
+    64x128 tiles from 4096 output pixels, 64x64 below."""
+    rng = np.random.default_rng(23)
+    case = _packed_case(rng, n, 3, h, 64, 7, 2, 3, res=False)
+    w = case["tensors"]["w"]  # [Co][7][7][3]
+    rows = np.zeros((64, 160), np.float32)
+    rows[:, :147] = w.reshape(64, 147)
+    case["tensors"]["w"] = rows
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    _check(got, exp, case["name"])
+
+
 @pytest.mark.parametrize("act", [0, 1, 2])
 @pytest.mark.parametrize("bias,res", [(True, False), (False, True), (False, False)])
 def test_conv_packed_epilogues(act, bias, res, hip, dmem, abi, oracle_lib):
@@ -202,6 +218,8 @@ def test_conv_packed_matches_reference_layout_entry(hip, dmem, abi, oracle_lib):
     ("Ci % 32", (1, 24, 8, 16, 3, 1, 1), (16, 3, 3, 24)),
     ("5x5 kernel", (1, 32, 8, 16, 5, 1, 2), (16, 5, 5, 32)),
     ("not tap-major", (1, 32, 8, 16, 3, 1, 1), (16, 32, 3, 3)),
+    ("rows not padded to 32", (1, 3, 16, 16, 7, 2, 3), (16, 147)),
+    ("rows for a 3x3 kernel", (1, 3, 16, 16, 3, 1, 1), (16, 32)),
 ])
 def test_conv_packed_rejects(why, shape, wshape, hip, dmem, abi):
     from nnc_py_amd import runtime

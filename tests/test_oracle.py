@@ -305,6 +305,24 @@ def test_oracle_conv_packed_composition(act, res, kernel, oracle_lib, abi):
     np.testing.assert_allclose(conv, ref.astype(F32), rtol=2e-7, atol=1e-5)
 
 
+def test_oracle_conv_packed_rows_stem(oracle_lib, abi):
+    """[Co][Kp] packing (3-channel 7x7 stem): rows of tap-major weights with
+    zeros past K give the reference convolution."""
+    rng = np.random.default_rng(37)
+    c = _conv_case(rng, "nnc_conv_relu", 2, 3, 23, 23, 5, 7, 7, 2, 2, 3, 3)
+    ref = caserun.run_case(oracle_lib, c, abi)["out"]
+    t = dict(c["tensors"])
+    w = t["w"]
+    rows = np.zeros((w.shape[0], 160), F32)
+    rows[:, :147] = w.transpose(0, 2, 3, 1).reshape(w.shape[0], 147)
+    rows[:, 147:] = 1e30  # padding is ignored
+    t["w"] = rows
+    args = c["args"][:3] + [("null",)] + c["args"][3:] + [("i", 1)]
+    got = caserun.run_case(oracle_lib, {"name": "stem", "op": "nnc_hip_conv_packed", "tensors": t, "args": args,
+                                        "outputs": ["out"]}, abi)["out"]
+    assert caserun.same_bits(got, ref)
+
+
 def test_oracle_conv_add_relu_composition(oracle_lib, abi):
     rng = np.random.default_rng(41)
     c = _conv_case(rng, "nnc_conv", 2, 5, 8, 8, 4, 3, 3, 1, 1, 1, 1)
