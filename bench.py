@@ -156,11 +156,12 @@ COPY_PROBE_BYTES = 256 << 20
 def conv_symbol_pattern(name: str) -> re.Pattern | None:
     """Kernel-table name -> regex over the HIP kernel symbol rocprofv3 reports,
     e.g. conv_igemm_128x128_k3x3_v4 -> conv_streamk_k<nnc::Tile<128, 128, ...>, 3, 3, true>,
-    conv_igemm_128x128_k3x3_dma -> conv_dma_k<nnc::Tile<128, 128, ...>, 3, 3>."""
-    m = re.fullmatch(r"conv_igemm_(\d+)x(\d+)_k(\d+)x(\d+)_dma", name)
+    conv_igemm_128x128_k3x3_dma -> conv_dma_k<nnc::Tile<128, 128, ...>, nnc::DmaPacked<..., 3, 3>, ...>."""
+    m = re.fullmatch(r"conv_igemm_(\d+)x(\d+)_k(\d+)x(\d+)(c3)?_dma", name)
     if m:
-        bm, bn, kh, kw = m.groups()
-        return re.compile(rf"conv_dma_k<nnc::Tile<{bm}, {bn},[^>]*>, {kh}, {kw}>")
+        bm, bn, kh, kw, c3 = m.groups()
+        loader = rf"DmaSmallC<nnc::Tile<[^>]*>, {kh}, {kw}, 3>" if c3 else rf"DmaPacked<nnc::Tile<[^>]*>, {kh}, {kw}>"
+        return re.compile(rf"conv_dma_k<nnc::Tile<{bm}, {bn},[^>]*>, nnc::{loader}")
     m = re.fullmatch(r"conv_igemm_(\d+)x(\d+)_k(\d+|any)(?:x(\d+))?_(v4|s1)", name)
     if m:
         bm, bn, kh, kw, vec = m.groups()

@@ -340,8 +340,9 @@ struct DmaStage {
     static constexpr int A_FLOATS = T::BM * 32, B_FLOATS = T::BN * 32;
     static constexpr int STAGE = A_FLOATS + B_FLOATS;
     static constexpr int LDS_FLOATS = 2 * STAGE;
-    static constexpr int PX_GROUPS = T::BN / 64;      // 64-pixel groups of a B row
-    static constexpr int B_LOADS = 32 * PX_GROUPS / 4;  // dword loads per wave per slice
+    static constexpr int PX_GROUPS = T::BN / 64;             // 64-pixel groups of a B row
+    static constexpr int B_LOADS = 32 * PX_GROUPS / T::NW;  // dword loads per wave per slice
+    static_assert(T::NW % PX_GROUPS == 0 && B_LOADS % 2 == 0, "B rows split evenly over the waves");
     static_assert(T::BM % 32 == 0 && (T::BN == 64 || T::BN == 128) && T::BK == 32, "dma tile");
 };
 
@@ -397,7 +398,8 @@ template <class T, int KH, int KW>
 struct DmaPacked {
     typedef DmaStage<T> D;
     static constexpr bool kFinishInKernel = true;
-    static constexpr int A_LOADS = T::BM / 32;  // dwordx4 loads per wave per slice, 8 rows each
+    static constexpr int A_LOADS = T::BM / (8 * T::NW);  // dwordx4 loads per wave per slice, 8 rows each
+    static_assert(T::BM % (8 * T::NW) == 0, "A rows split evenly over the waves");
     __amdgpu_buffer_rsrc_t rin, rw;
     int wave, b_grp, b_kr0, CB, HW, W, Ci;
     uint32_t avo[A_LOADS];
@@ -420,7 +422,7 @@ struct DmaPacked {
         const int a_kc = (lane & 7) ^ ((lane >> 3) & 7);
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
-            const int co = i0 + (wave + 4 * i) * 8 + (lane >> 3);
+            const int co = i0 + (wave + T::NW * i) * 8 + (lane >> 3);
             avo[i] = keep_or_oob((uint32_t)(co * a.ldw) * 4u + (uint32_t)a_kc * 16u, co < a.Co);
         }
         px.init(a, j0 + b_grp * 64 + lane);
@@ -440,7 +442,8 @@ struct DmaPacked {
         if (part == 0) {
             const uint32_t sa = (uint32_t)(t * Ci + cb * 32) * 4u;
 #pragma unroll
-            for (int i = 0; i < A_LOADS; ++i) dma_load16(rw, S + (wave + 4 * i) * 8 * 32, on ? avo[i] : kOutOfRange, sa);
+            for (int i = 0; i < A_LOADS; ++i)
+                dma_load16(rw, S + (wave + T::NW * i) * 8 * 32, on ? avo[i] : kOutOfRange, sa);
             const int r = t / KW, c = t - r * KW;
             bv = keep_or_oob((uint32_t)(px.bpo + r * W + c) * 4u, on && px.inside(t));
         }
@@ -462,7 +465,7 @@ struct DmaSmallC {
     typedef DmaStage<T> D;
     // (the in-kernel finish's registers would cost this kernel occupancy)
     static constexpr bool kFinishInKernel = false;
-    static constexpr int A_LOADS = T::BM / 32;
+    static constexpr int A_LOADS = T::BM / (8 * T::NW);
     __amdgpu_buffer_rsrc_t rin, rw;
     int wave, b_grp, b_kr0, HW, W, K;
     uint32_t avo[A_LOADS];
@@ -483,7 +486,7 @@ struct DmaSmallC {
         const int a_kc = (lane & 7) ^ ((lane >> 3) & 7);
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
-            const int co = i0 + (wave + 4 * i) * 8 + (lane >> 3);
+            const int co = i0 + (wave + T::NW * i) * 8 + (lane >> 3);
             avo[i] = keep_or_oob((uint32_t)(co * a.ldw) * 4u + (uint32_t)a_kc * 16u, co < a.Co);
         }
         px.init(a, j0 + b_grp * 64 + lane);
@@ -494,7 +497,7 @@ struct DmaSmallC {
         if (part == 0) {
 #pragma unroll
             for (int i = 0; i < A_LOADS; ++i)
-                dma_load16(rw, S + (wave + 4 * i) * 8 * 32, on ? avo[i] : kOutOfRange, (uint32_t)k0 * 4u);
+                dma_load16(rw, S + (wave + T::NW * i) * 8 * 32, on ? avo[i] : kOutOfRange, (uint32_t)k0 * 4u);
         }
         constexpr int H = D::B_LOADS / 2;
         float* d0 = S + D::A_FLOATS + b_kr0 * T::BN + b_grp * 64;
@@ -525,7 +528,7 @@ __device__ __forceinline__ void read_quad_dma(const float* Sa, int a_row, int a_
 }
 
 template <class T, class L, bool FIN>
-__global__ void __launch_bounds__(256, 2) conv_dma_k(ConvArgs a, StreamK sk) {
+__global__ void __launch_bounds__(T::THREADS, 2) conv_dma_k(ConvArgs a, StreamK sk) {
     typedef DmaStage<T> D;
     extern __shared__ __align__(16) float lds[];
     const int g = xcd_remap(blockIdx.x, sk.G);
@@ -609,6 +612,19 @@ __global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
     if (co >= a.Co || p0 >= a.Npix) return;
     float4 v = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g0, first_slot))[e4];
     int g = g0 + 1;
+    // many partials per tile (short problems): 16 loads in flight per thread
+    for (; g + 15 <= g1; g += 16) {
+        float4 p[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) p[q] = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g + q, 0))[e4];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            v.x += p[q].x;
+            v.y += p[q].y;
+            v.z += p[q].z;
+            v.w += p[q].w;
+        }
+    }
     for (; g + 3 <= g1; g += 4) {
         float4 p[4];
 #pragma unroll
@@ -680,7 +696,7 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
     // the in-kernel finish only where it measured faster than the fixup
     // kernel (64x128 tiles: ResNet's 64-channel layers); elsewhere its code
     // costs the main loop registers
-    constexpr bool FIN = kInKernelFixup && T::BM == 64 && T::BN == 128 && L::kFinishInKernel;
+    constexpr bool FIN = kInKernelFixup && T::BM == 64 && T::BN == 128 && T::NW == 4 && L::kFinishInKernel;
     auto kernel = conv_dma_k<T, L, FIN>;
     const size_t lds = (size_t)DmaStage<T>::LDS_FLOATS * sizeof(float);
     static bool configured = false;
@@ -690,7 +706,7 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
                                         (int)lds),
                     entry, "hipFuncSetAttribute"))
             return;
-        slots = resident_groups(kernel, lds);
+        slots = resident_groups(kernel, lds, T::THREADS);
         configured = true;
     }
     // K == 0 (no input channels) still runs one empty slice so the epilogue
@@ -709,7 +725,7 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
     const bool in_kernel = FIN && sk.needs_fixup() && (sk.iters + per - 1) / per + 1 <= kMaxInKernelParts;
     a.cnt = in_kernel ? tile_counters((size_t)sk.sk_tiles) : nullptr;
     set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
-    launch(name, kernel, dim3(sk.G), dim3(256), lds, a, sk);
+    launch(name, kernel, dim3(sk.G), dim3(T::THREADS), lds, a, sk);
     if (sk.needs_fixup() && !a.cnt) {
         set_work(0.0, 0.0);
         launch("conv_streamk_fixup", conv_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, a, sk);
@@ -853,8 +869,8 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     }
     const bool dma = dma_ok && (packed || (kh == 1 && kw == 1));
     if (a.N == 0 || a.Co == 0 || a.Ho <= 0 || a.Wo <= 0) return;
-    if (stem) {
-        if (a.Co <= 64 && a.Npix >= 4096)
+    if (stem) {  // 64x128 tiles only once there are plenty of them (batch 32: 3136)
+        if (a.Co <= 64 && a.Npix >= 65536)
             return launch_conv_stem<ConvT64>(a, name);
         return launch_conv_stem<ConvTSmall>(a, name);
     }

@@ -67,11 +67,12 @@ __device__ __forceinline__ f32x4 load_f32x4(__amdgpu_buffer_rsrc_t r, uint32_t b
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
 }
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int NW_ = 4>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
-    static constexpr int THREADS = 256;
-    static_assert(WM * WN == 4, "four waves per workgroup");
+    static constexpr int NW = NW_;  // waves per workgroup (the staging loaders take 4)
+    static constexpr int THREADS = 64 * NW;
+    static_assert(WM * WN == NW, "one wave per (WM, WN) cell");
     static constexpr int WAVE_M = BM / WM, WAVE_N = BN / WN;
     static constexpr int TM = WAVE_M / 32, TN = WAVE_N / 32;
     static_assert(TM >= 1 && TN >= 1 && WAVE_M % 32 == 0 && WAVE_N % 32 == 0, "32x32 blocks");
@@ -518,9 +519,9 @@ constexpr int fixup_slices() {
 
 // Persistent-grid size: workgroups of `kernel` resident on the device at once.
 template <typename K>
-static int resident_groups(K kernel, size_t lds_bytes) {
+static int resident_groups(K kernel, size_t lds_bytes, int threads = 256) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds_bytes) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds_bytes) != hipSuccess ||
         per_cu < 1)
         per_cu = 1;
     return per_cu * ctx().cu_count;
