@@ -366,6 +366,8 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--no-b1", action="store_true", help="measure batch 32 only (profiling runs)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="skip the reference's own O3 call sequence on the HIP library")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--suite", action="store_true",
                     help="instead of the ResNet-18 line: GEMM sweep, bandwidth ops and transformer encoder, "
@@ -410,6 +412,20 @@ def main() -> int:
             f"{results[batch]['images_per_s']:.1f} images/s")
         if batch == args.batch:
             tables[batch] = kernel_table(ex, runtime, args.profile_steps)
+        ex.close()
+
+    # the drop-in path: the call sequence the reference's own O3 pipeline
+    # emits (reference entry points only) on this library, same batch
+    dropin = None
+    if not args.no_dropin:
+        prog = build_program(zoo.resnet18(batch=args.batch, seed=1), opt_level=3, target_passes=False)
+        ex = Executor(prog, device=True)
+        ex.set_input("input", np.random.default_rng(0).standard_normal((args.batch, 3, 224, 224)).astype(np.float32))
+        steps = max(10, args.steps // 2)
+        log(f"drop-in (reference O3 call sequence, {len(prog.calls)} calls): {steps} timed steps")
+        dt = timed_steps(ex, steps, args.warmup, graph, runtime)
+        dropin = {"images_per_s": round(args.batch * steps / dt, 2), "ms_per_step": round(dt / steps * 1e3, 4),
+                  "calls": len(prog.calls), "batch": args.batch}
         ex.close()
 
     table = tables[args.batch]
@@ -462,6 +478,7 @@ def main() -> int:
         "per_kernel": [{k: r[k] for k in ("kernel", "launches_per_step", "avg_us", "bound", "achieved", "unit", "frac")}
                        for r in table],
         "cpu_baseline": cpu,
+        "dropin": dropin,
         "host": platform.node(),
     }
     print(json.dumps(line), flush=True)

@@ -26,6 +26,9 @@ struct Context {
     // (each kernel returns the counters it used to zero)
     int* counters = nullptr;
     size_t counters_n = 0;
+    // tap-major copies of reference-layout conv weights (grown outside capture)
+    float* repack = nullptr;
+    size_t repack_bytes = 0;
     bool capturing = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -53,6 +56,10 @@ size_t workspace_capacity();
 // At least `n` zeroed tile counters, or nullptr if they cannot be provided
 // (inside graph capture the buffer cannot grow). Kernels leave them zero.
 int* tile_counters(size_t n);
+
+// At least `bytes` of scratch for a repacked weight tensor, or nullptr if it
+// cannot be provided (inside graph capture the buffer cannot grow).
+float* repack_buffer(size_t bytes);
 
 // ---------------------------------------------------------------------------
 // kernel launch with optional hipEvent timing (keyed by kernel name)

@@ -647,9 +647,24 @@ __global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
     fixup_store(a, co, p0, v);
 }
 
+// Reference-layout weights [Co][Ci][T] to tap-major [Co][T][Ci] (T = kh*kw),
+// so that reference-layout 3x3 calls reach the direct-to-LDS kernel. One
+// thread per output element: writes coalesce, reads stride T (cached).
+__global__ void __launch_bounds__(256) repack_taps_k(const float* w, float* wp, int Ci, int T, int64_t n) {
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (o >= n) return;
+    const int ci = (int)(o % Ci);
+    const int64_t rest = o / Ci;  // co * T + t
+    const int t = (int)(rest % T);
+    const int64_t co = rest / T;
+    wp[o] = w[(co * Ci + ci) * T + t];
+}
+
 // direct-to-LDS kernels finish shared stream-K tiles themselves when a tile
 // has at most kMaxInKernelParts partials
 static constexpr bool kInKernelFixup = true;
+// reference-layout 3x3 convolutions from this much work on are repacked
+static constexpr double kRepackMinFlops = 1e9;
 static constexpr int kMaxInKernelParts = 4;
 
 typedef Tile<128, 128, 32, 2, 2> ConvT128;  // Co >= 128: 2x2 blocks per wave
@@ -867,8 +882,21 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
             return fail(NNC_HIP_EUNSUPP, name,
                         "packed weights need Ci % 32 == 0, a 1x1 or 3x3 kernel and 16-byte alignment");
     }
-    const bool dma = dma_ok && (packed || (kh == 1 && kw == 1));
+    bool dma = dma_ok && (packed || (kh == 1 && kw == 1));
     if (a.N == 0 || a.Co == 0 || a.Ho <= 0 || a.Wo <= 0) return;
+    // reference-layout 3x3 weights of a large convolution: a tap-major copy
+    // (one small transpose kernel) pays for itself on the direct-to-LDS path
+    if (dma_ok && !packed && kh == 3 && 2.0 * a.Co * (double)a.Npix * a.K >= kRepackMinFlops) {
+        float* wp = repack_buffer((size_t)a.Co * a.K * sizeof(float));
+        if (wp) {
+            const int64_t n = (int64_t)a.Co * a.K;
+            set_work(0.0, 8.0 * (double)n);
+            launch("conv_repack_taps", repack_taps_k, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, a.w, wp, a.Ci,
+                   kh * kw, n);
+            a.w = wp;
+            dma = true;
+        }
+    }
     if (stem) {  // 64x128 tiles only once there are plenty of them (batch 32: 3136)
         if (a.Co <= 64 && a.Npix >= 65536)
             return launch_conv_stem<ConvT64>(a, name);

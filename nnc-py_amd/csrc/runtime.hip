@@ -50,12 +50,19 @@ bool ready(const char* who) {
 // 128x128 floats for 512 workgroups = 64 MiB) with room; grows outside capture.
 static const size_t kDefaultWorkspace = 128u << 20;
 
+// Scratch buffers replaced by larger ones stay allocated until shutdown: a
+// hipGraph captured earlier still holds their addresses.
+static std::vector<void*> g_retired;
+static void retire(void* p) {
+    if (p) g_retired.push_back(p);
+}
+
 float* workspace(size_t bytes) {
     if (bytes <= g_ctx.workspace_bytes) return g_ctx.workspace;
     if (g_ctx.capturing) return nullptr;
     if (!hip_ok(hipStreamSynchronize(g_ctx.stream), "workspace", "hipStreamSynchronize"))
         return nullptr;
-    if (g_ctx.workspace) (void)hipFree(g_ctx.workspace);
+    retire(g_ctx.workspace);
     g_ctx.workspace = nullptr;
     g_ctx.workspace_bytes = 0;
     size_t want = bytes < kDefaultWorkspace ? kDefaultWorkspace : bytes;
@@ -68,13 +75,28 @@ float* workspace(size_t bytes) {
 
 size_t workspace_capacity() { return g_ctx.workspace_bytes; }
 
+float* repack_buffer(size_t bytes) {
+    if (bytes <= g_ctx.repack_bytes) return g_ctx.repack;
+    if (g_ctx.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(g_ctx.stream), "repack_buffer", "hipStreamSynchronize")) return nullptr;
+    retire(g_ctx.repack);
+    g_ctx.repack = nullptr;
+    g_ctx.repack_bytes = 0;
+    const size_t want = bytes < (16u << 20) ? (16u << 20) : bytes;
+    void* p = nullptr;
+    if (!hip_ok(hipMalloc(&p, want), "repack_buffer", "hipMalloc")) return nullptr;
+    g_ctx.repack = static_cast<float*>(p);
+    g_ctx.repack_bytes = want;
+    return g_ctx.repack;
+}
+
 static const size_t kDefaultCounters = 1u << 16;
 
 int* tile_counters(size_t n) {
     if (n <= g_ctx.counters_n) return g_ctx.counters;
     if (g_ctx.capturing) return nullptr;
     if (!hip_ok(hipStreamSynchronize(g_ctx.stream), "tile_counters", "hipStreamSynchronize")) return nullptr;
-    if (g_ctx.counters) (void)hipFree(g_ctx.counters);
+    retire(g_ctx.counters);
     g_ctx.counters = nullptr;
     g_ctx.counters_n = 0;
     const size_t want = n < kDefaultCounters ? kDefaultCounters : n;
@@ -206,6 +228,9 @@ void nnc_hip_shutdown(void) {
     if (c.arena) (void)hipFree(c.arena);
     if (c.workspace) (void)hipFree(c.workspace);
     if (c.counters) (void)hipFree(c.counters);
+    if (c.repack) (void)hipFree(c.repack);
+    for (void* p : g_retired) (void)hipFree(p);
+    g_retired.clear();
     (void)hipStreamDestroy(c.stream);
     g_ctx = Context{};
 }
