@@ -183,7 +183,7 @@ __device__ __forceinline__ uint32_t slot_byte_offset(int g, int which) {
 template <class T>
 __device__ void conv_finish_tile(const ConvArgs& a, int t, int g0, int g1, int first_slot) {
     constexpr int E = T::BM * T::BN / 1024;  // float4 per thread
-    constexpr int CH = E < 8 ? E : 8;         // float4 in flight per partial (register budget)
+    constexpr int CH = E < 4 ? E : 4;         // float4 in flight per partial (register budget)
     const __amdgpu_buffer_rsrc_t rws = make_rsrc(a.ws);
     const int mt = t % a.tiles_m, nt = t / a.tiles_m;
     const uint32_t first = slot_byte_offset<T>(g0, first_slot);
@@ -340,6 +340,10 @@ struct DmaStage {
     static constexpr int A_FLOATS = T::BM * 32, B_FLOATS = T::BN * 32;
     static constexpr int STAGE = A_FLOATS + B_FLOATS;
     static constexpr int LDS_FLOATS = 2 * STAGE;
+    // waves per SIMD that the LDS stages allow (160 KB per CU): the register
+    // budget the kernel is compiled for, so registers never lower occupancy
+    static constexpr int LDS_WAVES = (160 * 1024 / (LDS_FLOATS * 4)) * T::NW / 4;
+    static constexpr int MIN_WAVES = LDS_WAVES < 2 ? 2 : (LDS_WAVES > 4 ? 4 : LDS_WAVES);
     static constexpr int PX_GROUPS = T::BN / 64;             // 64-pixel groups of a B row
     static constexpr int B_LOADS = 32 * PX_GROUPS / T::NW;  // dword loads per wave per slice
     static_assert(T::NW % PX_GROUPS == 0 && B_LOADS % 2 == 0, "B rows split evenly over the waves");
@@ -528,7 +532,7 @@ __device__ __forceinline__ void read_quad_dma(const float* Sa, int a_row, int a_
 }
 
 template <class T, class L, bool FIN>
-__global__ void __launch_bounds__(T::THREADS, 2) conv_dma_k(ConvArgs a, StreamK sk) {
+__global__ void __launch_bounds__(T::THREADS, DmaStage<T>::MIN_WAVES) conv_dma_k(ConvArgs a, StreamK sk) {
     typedef DmaStage<T> D;
     extern __shared__ __align__(16) float lds[];
     const int g = xcd_remap(blockIdx.x, sk.G);
@@ -544,11 +548,28 @@ __global__ void __launch_bounds__(T::THREADS, 2) conv_dma_k(ConvArgs a, StreamK 
 
     SegmentWalker walk(sk, g);
     Segment seg;
-    while (walk.next(sk, seg)) {
+    // The slice loop runs on across segment boundaries: during a segment's
+    // last slice the loads of the next segment's first slice are issued, so
+    // a new tile starts with its operands already in LDS (short-K
+    // convolutions - the stem, 1x1 - have only a few slices per tile).
+    if (!walk.next(sk, seg)) return;
+    {
+        const int mt = seg.tile % a.tiles_m, nt = seg.tile / a.tiles_m;
+        ld.tile(a, mt * T::BM, nt * T::BN, lane);
+        ld.begin(seg.kb);
+        ld.issue(lds, true, 0);
+        ld.issue(lds, true, 1);
+        wait_dma();
+        __syncthreads();
+    }
+    // operands of quads 0 and 2 in set 0, quads 1 and 3 in set 1: the
+    // registers carried from one slice to the next (quad 0) stay put
+    f32x4 a0[T::TM], b0[T::TN], a1[T::TM], b1[T::TN];
+    read_quad_dma<T>(lds, a_row, a_sw, lds + b_off, 0, a0, b0);
+    int stage = 0;
+    while (true) {
         const int mt = seg.tile % a.tiles_m, nt = seg.tile / a.tiles_m;
         const int i0 = mt * T::BM, j0 = nt * T::BN;
-        ld.tile(a, i0, j0, lane);
-
         floatx16 sum[T::TM][T::TN];
 #pragma unroll
         for (int tm = 0; tm < T::TM; ++tm)
@@ -556,21 +577,24 @@ __global__ void __launch_bounds__(T::THREADS, 2) conv_dma_k(ConvArgs a, StreamK 
             for (int tn = 0; tn < T::TN; ++tn)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) sum[tm][tn][r] = 0.f;
-
-        ld.begin(seg.kb);
-        ld.issue(lds, true, 0);
-        ld.issue(lds, true, 1);
-        wait_dma();
-        __syncthreads();
-        // operands of quads 0 and 2 in set 0, quads 1 and 3 in set 1: the
-        // registers carried from one slice to the next (quad 0) stay put
-        f32x4 a0[T::TM], b0[T::TN], a1[T::TM], b1[T::TN];
-        read_quad_dma<T>(lds, a_row, a_sw, lds + b_off, 0, a0, b0);
-        int stage = 0;
+        Segment nxt;
+        bool have_next = false;
         for (int it = seg.kb; it < seg.ke; ++it) {
-            // next slice; past the segment's end its loads are no-ops
-            const bool more = it + 1 < seg.ke;
-            ld.step(more);
+            // next slice: this segment's, or the first of the next segment
+            // (the loader switches tiles once this tile's loads are all issued);
+            // past the walk's end its loads are no-ops
+            const bool last = it + 1 == seg.ke;
+            if (last) {
+                have_next = walk.next(sk, nxt);
+                if (have_next) {
+                    const int nmt = nxt.tile % a.tiles_m, nnt = nxt.tile / a.tiles_m;
+                    ld.tile(a, nmt * T::BM, nnt * T::BN, lane);
+                    ld.begin(nxt.kb);
+                }
+            } else {
+                ld.step(true);
+            }
+            const bool more = !last || have_next;
             float* next = lds + (stage ^ 1) * D::STAGE;
             const float* S = lds + stage * D::STAGE;
             // the loads issue in two halves ahead of quads 0 and 1; quad 2
@@ -590,6 +614,8 @@ __global__ void __launch_bounds__(T::THREADS, 2) conv_dma_k(ConvArgs a, StreamK 
             stage ^= 1;
         }
         conv_segment_out<T, FIN>(a, sk, seg, g, i0, j0, sum);
+        if (!have_next) break;
+        seg = nxt;
     }
 }
 
@@ -665,7 +691,16 @@ __global__ void __launch_bounds__(256) repack_taps_k(const float* w, float* wp, 
 static constexpr bool kInKernelFixup = true;
 // reference-layout 3x3 convolutions from this much work on are repacked
 static constexpr double kRepackMinFlops = 1e9;
-static constexpr int kMaxInKernelParts = 4;
+#ifndef NNC_CONV_FIN_MAX_PARTS
+#define NNC_CONV_FIN_MAX_PARTS 4
+#endif
+static constexpr int kMaxInKernelParts = NNC_CONV_FIN_MAX_PARTS;
+// 128x128 direct-to-LDS tiles finish shared tiles in-kernel too (off: on
+// ResNet-18's batch-32 layers it measured 62.0 -> 69.0 us per launch, the
+// finishing workgroups' partial reads sit on the kernel's critical path)
+#ifndef NNC_CONV_FIN128
+#define NNC_CONV_FIN128 0
+#endif
 
 typedef Tile<128, 128, 32, 2, 2> ConvT128;  // Co >= 128: 2x2 blocks per wave
 typedef Tile<64, 128, 32, 1, 4> ConvT64;    // Co == 64, many pixels: 2x1 blocks per wave
@@ -711,7 +746,8 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
     // the in-kernel finish only where it measured faster than the fixup
     // kernel (64x128 tiles: ResNet's 64-channel layers); elsewhere its code
     // costs the main loop registers
-    constexpr bool FIN = kInKernelFixup && T::BM == 64 && T::BN == 128 && T::NW == 4 && L::kFinishInKernel;
+    constexpr bool FIN = kInKernelFixup && L::kFinishInKernel && T::NW == 4 &&
+                         ((T::BM == 64 && T::BN == 128) || (NNC_CONV_FIN128 && T::BM == 128 && T::BN == 128));
     auto kernel = conv_dma_k<T, L, FIN>;
     const size_t lds = (size_t)DmaStage<T>::LDS_FLOATS * sizeof(float);
     static bool configured = false;
