@@ -12,6 +12,7 @@
 //            count (padding excluded, ops.c:442-456); empty window -> 0.
 // N and C come from the input and Ho/Wo from the output, as in the reference.
 #include "common.h"
+#include "mfma_tile.h"
 
 namespace nnc {
 
@@ -160,6 +161,76 @@ __global__ void __launch_bounds__(256) pool2d_lds_k(PoolArgs a) {
     }
 }
 
+// 3x3 stride-2 max pooling with one row and one column of padding (the
+// ResNet stem's pool), straight from HBM: one wave per (plane, band of R
+// output rows, 64 output columns). Lane l owns output column ow = ow0 + l
+// and loads input columns 2ow and 2ow+1 of every input row of the band as
+// one 8-byte load; column 2ow-1 is its left neighbour's second element (a
+// lane shuffle; lane 0 of a later chunk loads it itself). All 2R+1 rows of
+// the band are loaded up front (the row two vertically adjacent windows
+// share stays in registers), so the input is read once plus one halo row
+// per band. Each window is scanned in the reference's order - rows top to
+// bottom, columns left to right, the first in-bounds element taken, then
+// strict > - so the result is bit-exact with pool2d_k. Needs an even W and
+// an input below 2 GiB (buffer offsets), checked by the caller.
+template <int R>
+__global__ void __launch_bounds__(256) maxpool3s2_k(PoolArgs a, int nbands, int nchunks) {
+    const int lane = threadIdx.x & 63;
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int chunk = wid % nchunks;
+    const int rest = wid / nchunks;
+    const int band = rest % nbands;
+    const int nc = rest / nbands;
+    if (nc >= a.NC) return;  // wave-uniform
+    const int ow = chunk * 64 + lane;
+    const int oh0 = band * R;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.in);
+    // in-bounds columns of this lane's window: 2ow-1, 2ow, 2ow+1 (W even:
+    // 2ow < W implies 2ow+1 < W)
+    const bool c0 = ow >= 1 && 2 * ow - 1 < a.W;
+    const bool c1 = 2 * ow < a.W;
+    const int hbase = 2 * oh0 - 1;
+    float x0[2 * R + 1], x1[2 * R + 1], x2[2 * R + 1];
+#pragma unroll
+    for (int i = 0; i < 2 * R + 1; ++i) {
+        const int h = hbase + i;
+        const bool row_in = h >= 0 && h < a.H;
+        const uint32_t rowoff = row_in ? (uint32_t)((nc * a.H + h) * a.W) * 4u : 0u;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(row_in && c1 ? rowoff + (uint32_t)ow * 8u : kOutOfRange),
+                                                            0, 0);
+        // element copies first: bit_cast of an ext-vector element is miscompiled
+        const uint32_t lo = v[0], hi = v[1];
+        x1[i] = __uint_as_float(lo);
+        x2[i] = __uint_as_float(hi);
+        float left = __shfl_up(x2[i], 1);
+        if (lane == 0 && c0)
+            left = load_f32(rs, row_in ? rowoff + (uint32_t)(2 * ow - 1) * 4u : kOutOfRange);
+        x0[i] = left;
+    }
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int oh = oh0 + j;
+        if (oh >= a.Ho) break;
+        float best = -3.402823e38f;
+        bool seen = false;
+#pragma unroll
+        for (int r = 0; r < 3; ++r) {
+            const int h = hbase + 2 * j + r;
+            if (h < 0 || h >= a.H) continue;
+            const float v3[3] = {x0[2 * j + r], x1[2 * j + r], x2[2 * j + r]};
+            const bool ok3[3] = {c0, c1, c1};
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                if (ok3[c] && (!seen || v3[c] > best)) {
+                    best = v3[c];
+                    seen = true;
+                }
+            }
+        }
+        if (ow < a.Wo) a.out[((int64_t)nc * a.Ho + oh) * a.Wo + ow] = best;
+    }
+}
+
 __global__ void fill_value_k(float* out, int64_t n, float v) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = v;
@@ -207,6 +278,16 @@ static void pool_entry(const char* name, Tensor* in, Tensor* out, int kh, int kw
         return;
     }
     if ((int64_t)a.Ho * a.Wo >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "output plane too large");
+    if (MAX && kh == 3 && kw == 3 && sh == 2 && sw == 2 && ph == 1 && pw == 1 && a.W % 2 == 0 && a.H > 0 &&
+        a.Ho > 0 && a.Wo > 0 && nc > 0 && numel(in) * 4 < ((int64_t)1 << 31)) {
+        constexpr int R = 8;
+        const int nbands = (int)ceil_div(a.Ho, R), nchunks = (int)ceil_div(a.Wo, 64);
+        const int64_t waves = nc * nbands * nchunks;
+        if (waves < ((int64_t)1 << 31) - 4) {
+            launch(name, maxpool3s2_k<R>, dim3((unsigned)ceil_div(waves, 4)), dim3(256), 0, a, nbands, nchunks);
+            return;
+        }
+    }
     if (hw <= 16384 && hw > 0 && a.Ho > 0 && a.Wo > 0 && nc > 0) {
         // whole plane in LDS (at most 64 KB): the input is read once
         const int64_t cap = (int64_t)ctx().cu_count * 8;

@@ -278,3 +278,41 @@ def test_batched_matmul_streamk(hip, dmem, abi, oracle_lib):
               "tensors": {"a": a[q].copy(), "b": b[q].copy(), "out": np.zeros((128, 128), np.float32)},
               "args": [("t", "a"), ("t", "b"), ("t", "out")], "outputs": ["out"], "bar": "fp"}
         _check(got[q], caserun.run_case(oracle_lib, c2, abi)["out"], f"batch {q}")
+
+
+def _maxpool_case(x, ho, wo, k=3, s=2, p=1):
+    n, c = x.shape[:2]
+    out = np.full((n, c, ho, wo), 7.0, np.float32)
+    return {"name": f"maxpool_{'x'.join(map(str, x.shape))}_to_{ho}x{wo}", "op": "nnc_maxpool2d",
+            "tensors": {"x": x, "out": out},
+            "args": [("t", "x"), ("t", "out")] + [("i", v) for v in (k, k, s, s, p, p)],
+            "outputs": ["out"], "bar": "exact"}
+
+
+# (N, C, H, W, Ho, Wo): the ResNet stem pool, two column chunks (Wo > 64),
+# odd H, and outputs past the natural size (clamped and empty windows)
+MAXPOOL_SHAPES = [
+    (2, 64, 112, 112, 56, 56),
+    (1, 3, 130, 130, 65, 65),
+    (2, 5, 7, 8, 4, 4),
+    (1, 2, 8, 8, 6, 6),
+    (1, 1, 2, 2, 1, 1),
+]
+
+
+@pytest.mark.parametrize("shape", MAXPOOL_SHAPES, ids=[str(s) for s in MAXPOOL_SHAPES])
+def test_maxpool_3x3s2_bit_exact(shape, hip, dmem, abi, oracle_lib):
+    n, c, h, w, ho, wo = shape
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((n, c, h, w)).astype(np.float32)
+    # the first-element rule: NaN first in a window stays, later NaN is
+    # skipped; signed zeros keep the first one seen
+    flat = x.reshape(-1)
+    flat[rng.integers(0, flat.size, 8)] = np.nan
+    x[0, 0, :2, :] = -0.0
+    x[0, 0, 0, ::2] = 0.0
+    case = _maxpool_case(x, ho, wo)
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    assert caserun.same_bits(got, exp), f"{case['name']}: {np.sum(got.view(np.uint32) != exp.view(np.uint32))} differ"
