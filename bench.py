@@ -247,8 +247,12 @@ def measure_traffic(kernel: str, batch: int) -> dict | None:
     return out
 
 
-def _op_roofline(runtime, fn, reps: int = 10, warmup: int = 3) -> list[dict]:
-    """Per-kernel table of `fn()` (one or more nnc_* calls) over `reps` calls."""
+def _op_roofline(runtime, fn, reps: int = 10, warmup: int = 3) -> dict:
+    """Per-kernel table of `fn()` (one or more nnc_* calls) over `reps` calls,
+    each launch bracketed by its own hipEvent pair, and the same `reps` calls
+    captured as one hipGraph and replayed back to back: `op_us` is the graph's
+    time per call (no per-launch event overhead), `op_achieved` the call's
+    algorithmic work over it."""
     for _ in range(warmup):
         fn()
     runtime.sync()
@@ -260,14 +264,55 @@ def _op_roofline(runtime, fn, reps: int = 10, warmup: int = 3) -> list[dict]:
     table = runtime.profile_table()
     runtime.profile_enable(False)
     rows = []
+    flops = sum(r["flops"] for r in table) / reps
+    nbytes = sum(r["bytes"] for r in table) / reps
+    mfma = False
     for r in table:
         if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma")):
             achieved, unit, peak = r["flops"] / (r["ms"] * 1e-3) / 1e12, "TFLOP/s", PEAK_FP32_MFMA_TF
+            mfma = True
         else:
             achieved, unit, peak = (r["bytes"] / (r["ms"] * 1e-3) / 1e9 if r["ms"] > 0 else 0.0), "GB/s", PEAK_HBM_GBS
         rows.append({"kernel": r["name"], "launches": r["launches"] // reps, "avg_us": round(r["ms"] / r["launches"] * 1e3, 2),
                      "achieved": round(achieved, 2), "unit": unit, "frac": round(achieved / peak, 4)})
-    return rows
+    lib = runtime.load()
+    runtime.check(lib.nnc_hip_graph_begin(), "graph_begin")
+    for _ in range(reps):
+        fn()
+    runtime.check(lib.nnc_hip_graph_end(), "graph_end")
+    runtime.check(lib.nnc_hip_graph_launch(), "graph_launch")
+    runtime.sync()
+    launches = 5
+    runtime.profile_reset()
+    runtime.profile_enable(True)
+    for _ in range(launches):
+        runtime.check(lib.nnc_hip_graph_launch(), "graph_launch")
+    runtime.sync()
+    graph_ms = sum(r["ms"] for r in runtime.profile_table() if r["name"] == "graph")
+    runtime.profile_enable(False)
+    lib.nnc_hip_graph_destroy()
+    op_us = graph_ms / (launches * reps) * 1e3
+    if mfma:
+        op_ach, unit, peak = flops / (op_us * 1e-6) / 1e12, "TFLOP/s", PEAK_FP32_MFMA_TF
+    else:
+        op_ach, unit, peak = nbytes / (op_us * 1e-6) / 1e9, "GB/s", PEAK_HBM_GBS
+    return {"kernels": rows, "op_us": round(op_us, 2), "op_achieved": round(op_ach, 2), "op_unit": unit,
+            "op_frac": round(op_ach / peak, 4)}
+
+
+def _copy_ceiling(runtime, nbytes: int) -> dict:
+    """A plain device copy (copy16_k) that reads and writes `nbytes` each,
+    timed like an op: the bandwidth a read-once/write-once kernel of this
+    size reaches, ramp-up and tail included."""
+    n = max(4, nbytes // 4)
+    src = runtime.DeviceBuffer.empty((n,))
+    dst = runtime.DeviceBuffer.empty((n,))
+    ts, td = src.tensor(), dst.tensor()
+    lib = runtime.load()
+    res = _op_roofline(runtime, lambda: lib.nnc_identity(ctypes.byref(ts[0]), ctypes.byref(td[0])))
+    src.free()
+    dst.free()
+    return {"bytes": 8 * n, "us": res["op_us"], "GB/s": res["op_achieved"], "frac": res["op_frac"]}
 
 
 def run_suite() -> int:
@@ -292,8 +337,10 @@ def run_suite() -> int:
         keep.append((buf, t))
         return ctypes.pointer(t[0])
 
-    def emit(suite, workload, rows, **extra):
-        print(json.dumps({"suite": suite, "workload": workload, **extra, "kernels": rows}), flush=True)
+    def emit(suite, workload, res, copy_bytes=None, **extra):
+        if copy_bytes:
+            res["copy_ceiling"] = _copy_ceiling(runtime, copy_bytes)
+        print(json.dumps({"suite": suite, "workload": workload, **extra, **res}), flush=True)
 
     for n in (1024, 2048, 4096):
         a, b, c = (rng.uniform(-1, 1, s).astype(np.float32) for s in ((n, n), (n, n), (n,)))
@@ -318,21 +365,24 @@ def run_suite() -> int:
     for op in ("nnc_add", "nnc_mul", "nnc_add_relu"):
         emit("bandwidth", f"{op} [32,256,56,56]", _op_roofline(runtime, lambda op=op: getattr(lib, op)(tx, ty, to)))
     for op in ("nnc_relu", "nnc_sigmoid", "nnc_tanh"):
-        emit("bandwidth", f"{op} [32,256,56,56]", _op_roofline(runtime, lambda op=op: getattr(lib, op)(tx, to)))
+        emit("bandwidth", f"{op} [32,256,56,56]", _op_roofline(runtime, lambda op=op: getattr(lib, op)(tx, to)),
+             copy_bytes=4 * 32 * 256 * 56 * 56 if op == "nnc_relu" else None)
     emit("bandwidth", "nnc_clip(-6,6) [32,256,56,56]", _op_roofline(runtime, lambda: lib.nnc_clip(tx, to, -6.0, 6.0)))
     tcat = dev(np.zeros((32, 512, 56, 56), np.float32))
     pair = (abi.TP * 2)(tx, ty)
     emit("bandwidth", "nnc_concat axis 1: 2 x [32,256,56,56]",
-         _op_roofline(runtime, lambda: lib.nnc_concat(ctypes.cast(pair, abi.TPP), tcat, 2, 1)))
+         _op_roofline(runtime, lambda: lib.nnc_concat(ctypes.cast(pair, abi.TPP), tcat, 2, 1)),
+         copy_bytes=4 * 32 * 512 * 56 * 56)
     emit("bandwidth", "nnc_split axis 1: [32,512,56,56] -> 2",
          _op_roofline(runtime, lambda: lib.nnc_split(tcat, ctypes.cast(pair, abi.TPP), 2, 1)))
     keep.clear()
     ts, tso = dev(rng.standard_normal((4096, 1024)).astype(np.float32)), dev(np.zeros((4096, 1024), np.float32))
-    emit("bandwidth", "nnc_softmax [4096,1024] axis -1", _op_roofline(runtime, lambda: lib.nnc_softmax(ts, tso, -1)))
+    emit("bandwidth", "nnc_softmax [4096,1024] axis -1", _op_roofline(runtime, lambda: lib.nnc_softmax(ts, tso, -1)),
+         copy_bytes=4 * 4096 * 1024)
     tl, tg, tb0 = dev(rng.standard_normal((8192, 768)).astype(np.float32)), dev(np.ones(768, np.float32)), dev(np.zeros(768, np.float32))
     tlo = dev(np.zeros((8192, 768), np.float32))
     emit("bandwidth", "nnc_layernorm [8192,768] eps 1e-5",
-         _op_roofline(runtime, lambda: lib.nnc_layernorm(tl, tg, tb0, tlo, -1, 1e-5)))
+         _op_roofline(runtime, lambda: lib.nnc_layernorm(tl, tg, tb0, tlo, -1, 1e-5)), copy_bytes=4 * 8192 * 768)
     r = rng.standard_normal((32, 512, 28, 28)).astype(np.float32)
     tr, tro = dev(r, (32, 512, 784)), dev(np.zeros((32, 512, 1), np.float32))
     for op in ("nnc_reducemean", "nnc_reducesum"):
@@ -347,7 +397,7 @@ def run_suite() -> int:
     dt = timed_steps(ex, steps, 10, True, runtime)
     ms = dt / steps * 1e3
     flops = zoo.transformer_flops()
-    emit("transformer", "encoder 2 layers, B8 S128 D256 H4 FFN1024, O3, hipGraph", kernel_table(ex, runtime, 5),
+    emit("transformer", "encoder 2 layers, B8 S128 D256 H4 FFN1024, O3, hipGraph", {"kernels": kernel_table(ex, runtime, 5)},
          ms_per_step=round(ms, 4), gflops_per_s=round(flops / (ms * 1e-3) / 1e9, 1),
          mfma_frac_whole_step=round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TF, 4))
     ex.close()

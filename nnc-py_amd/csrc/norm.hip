@@ -18,7 +18,11 @@
 // with max by strict '>' from -inf; layernorm y = g[i] * ((x - mean) / std) +
 // b[i], std = sqrtf(var + eps), var the mean of squared deviations. Parallel
 // sums change the summation order, so these are tolerance parity
-// (1e-4 abs / 1e-3 rel), except the strided reduction.
+// (1e-4 abs / 1e-3 rel), except the strided reduction. The row kernels take
+// exp from the hardware exp2 (__expf, a few ulp for the arguments x - max
+// <= 0) and divide by the row's sum / std through one reciprocal per row:
+// both within the bar, and per-element divisions with full-range expf made
+// the row kernels VALU-bound (softmax [4096,1024] 8.9 -> 7.2 us).
 #include <math.h>
 
 #include "common.h"
@@ -44,21 +48,42 @@ __device__ __forceinline__ float wave_max(float v) {
 // softmax
 // ---------------------------------------------------------------------------
 // PER float4 per lane: rows up to 256*PER floats, dim % 4 == 0, aligned.
+// Each wave walks its rows with the next row's loads issued before the
+// current row's reductions, so reads of one row overlap the arithmetic and
+// the stores of the previous one.
+// the next row is prefetched while its registers fit (rows up to 2048 floats)
+template <int PER>
+constexpr bool kPrefetch = PER <= 8;
+
+template <int PER>
+__device__ __forceinline__ void load_row4(float4 (&v)[PER], const float* base, int n4, int lane, float fill) {
+    const float4* x = reinterpret_cast<const float4*>(base);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int idx = lane + 64 * q;
+        v[q] = idx < n4 ? x[idx] : make_float4(fill, fill, fill, fill);
+    }
+}
+
 template <int PER>
 __global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, float* out, int64_t rows,
                                                          int dim) {
     const int lane = threadIdx.x & 63;
     const int64_t wstride = (int64_t)gridDim.x * 4;
     const int d4 = dim / 4;
-    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += wstride) {
-        const float4* x = reinterpret_cast<const float4*>(in + row * dim);
-        float4 v[PER];
+    int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float4 v[PER];
+    load_row4<PER>(v, in + row * dim, d4, lane, -INFINITY);
+    while (true) {
+        const int64_t nrow = row + wstride;
+        const bool more = nrow < rows;
+        float4 nx[PER];
+        if (kPrefetch<PER> && more) load_row4<PER>(nx, in + nrow * dim, d4, lane, -INFINITY);
         float m = -INFINITY;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-            const int idx = lane + 64 * q;
-            v[q] = idx < d4 ? x[idx] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-            if (idx < d4) {
+            if (lane + 64 * q < d4) {
                 if (v[q].x > m) m = v[q].x;
                 if (v[q].y > m) m = v[q].y;
                 if (v[q].z > m) m = v[q].z;
@@ -70,20 +95,26 @@ __global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, float*
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             if (lane + 64 * q < d4) {
-                v[q].x = expf(v[q].x - m);
-                v[q].y = expf(v[q].y - m);
-                v[q].z = expf(v[q].z - m);
-                v[q].w = expf(v[q].w - m);
+                v[q].x = __expf(v[q].x - m);
+                v[q].y = __expf(v[q].y - m);
+                v[q].z = __expf(v[q].z - m);
+                v[q].w = __expf(v[q].w - m);
                 s += (v[q].x + v[q].y) + (v[q].z + v[q].w);
             }
         }
         s = wave_sum(s);
         float4* y = reinterpret_cast<float4*>(out + row * dim);
+        const float rs = 1.0f / s;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             const int idx = lane + 64 * q;
-            if (idx < d4) y[idx] = make_float4(v[q].x / s, v[q].y / s, v[q].z / s, v[q].w / s);
+            if (idx < d4) y[idx] = make_float4(v[q].x * rs, v[q].y * rs, v[q].z * rs, v[q].w * rs);
         }
+        if (!more) break;
+        if (!kPrefetch<PER>) load_row4<PER>(nx, in + nrow * dim, d4, lane, -INFINITY);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) v[q] = nx[q];
+        row = nrow;
     }
 }
 
@@ -134,16 +165,18 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
     const int lane = threadIdx.x & 63;
     const int64_t wstride = (int64_t)gridDim.x * 4;
     const int s4 = span / 4;
-    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += wstride) {
-        const float4* x = reinterpret_cast<const float4*>(in + row * span);
-        float4 v[PER];
+    int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float4 v[PER];
+    load_row4<PER>(v, in + row * span, s4, lane, 0.f);
+    while (true) {
+        const int64_t nrow = row + wstride;
+        const bool more = nrow < rows;
+        float4 nx[PER];
+        if (kPrefetch<PER> && more) load_row4<PER>(nx, in + nrow * span, s4, lane, 0.f);
         float acc = 0.f;
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int idx = lane + 64 * q;
-            v[q] = idx < s4 ? x[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
-            acc += (v[q].x + v[q].y) + (v[q].z + v[q].w);
-        }
+        for (int q = 0; q < PER; ++q) acc += (v[q].x + v[q].y) + (v[q].z + v[q].w);
         const float mean = wave_sum(acc) / (float)span;
         float sq = 0.f;
 #pragma unroll
@@ -156,6 +189,7 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
         }
         const float var = wave_sum(sq) / (float)span;
         const float sd = sqrtf(var + eps);
+        const float rsd = 1.0f / sd;
         float4* y = reinterpret_cast<float4*>(out + row * span);
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
@@ -183,10 +217,15 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
                     }
                 }
 #pragma unroll
-                for (int c = 0; c < 4; ++c) r[c] = gv[c] * ((r[c] - mean) / sd) + bv[c];
+                for (int c = 0; c < 4; ++c) r[c] = gv[c] * ((r[c] - mean) * rsd) + bv[c];
                 y[idx] = make_float4(r[0], r[1], r[2], r[3]);
             }
         }
+        if (!more) break;
+        if (!kPrefetch<PER>) load_row4<PER>(nx, in + nrow * span, s4, lane, 0.f);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) v[q] = nx[q];
+        row = nrow;
     }
 }
 
@@ -256,14 +295,15 @@ __global__ void __launch_bounds__(256) reduce_rows_v4_k(const float* in, float* 
     const int lane = threadIdx.x & 63;
     const int64_t wstride = (int64_t)gridDim.x * 4;
     const int l4 = len / 4;
-    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += wstride) {
-        const float4* x = reinterpret_cast<const float4*>(in + row * len);
-        float4 v[PER];
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int idx = lane + 64 * q;
-            v[q] = idx < l4 ? x[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+    int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float4 v[PER];
+    load_row4<PER>(v, in + row * len, l4, lane, 0.f);
+    while (true) {
+        const int64_t nrow = row + wstride;
+        const bool more = nrow < rows;
+        float4 nx[PER];
+        if (kPrefetch<PER> && more) load_row4<PER>(nx, in + nrow * len, l4, lane, 0.f);
         float s = 0.f, c = 0.f;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
@@ -278,6 +318,11 @@ __global__ void __launch_bounds__(256) reduce_rows_v4_k(const float* in, float* 
         }
         s = wave_sum(s);
         if (lane == 0) out[row] = MEAN ? s / (float)len : s;
+        if (!more) break;
+        if (!kPrefetch<PER>) load_row4<PER>(nx, in + nrow * len, l4, lane, 0.f);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) v[q] = nx[q];
+        row = nrow;
     }
 }
 
@@ -315,9 +360,13 @@ static bool split_axis(const char* name, Tensor* in, int& axis, int64_t& outer, 
     return true;
 }
 
+// one row per wave (measured fastest: every row's loads in flight at once);
+// past the grid cap a wave walks several rows, prefetching the next
+static unsigned row_grid(int64_t rows) { return grid_for(rows, 4, 1); }
+
 template <int PER>
 static void softmax_v4(const float* x, float* y, int64_t rows, int dim, const char* name) {
-    launch(name, softmax_rows_v4_k<PER>, dim3(grid_for(rows, 4, 1) * 1), dim3(256), 0, x, y, rows, dim);
+    launch(name, softmax_rows_v4_k<PER>, dim3(row_grid(rows)), dim3(256), 0, x, y, rows, dim);
 }
 
 template <int PER>
@@ -325,10 +374,10 @@ static void layernorm_v4(const float* x, const float* g, const float* b, float* 
                          int span, int inner, float eps, const char* name) {
     // inner == 1 with 16-byte aligned scale/bias: vector loads of those too
     if (inner == 1 && (!g || aligned16(g)) && (!b || aligned16(b)))
-        launch(name, layernorm_rows_v4_k<PER, true>, dim3(grid_for(rows, 4, 1)), dim3(256), 0, x, g, b, y,
+        launch(name, layernorm_rows_v4_k<PER, true>, dim3(row_grid(rows)), dim3(256), 0, x, g, b, y,
                rows, span, inner, eps);
     else
-        launch(name, layernorm_rows_v4_k<PER, false>, dim3(grid_for(rows, 4, 1)), dim3(256), 0, x, g, b, y,
+        launch(name, layernorm_rows_v4_k<PER, false>, dim3(row_grid(rows)), dim3(256), 0, x, g, b, y,
                rows, span, inner, eps);
 }
 
@@ -402,11 +451,12 @@ static void reduce_entry(const char* name, Tensor* in, Tensor* out, int axis, bo
     set_work(0.0, 4.0 * (double)(outer * len * inner + outer * inner));
     if (inner == 1) {
         const dim3 grid(grid_for(outer, 4, 1));
+        const dim3 grid_v4(row_grid(outer));
         if (len % 4 == 0 && len <= 4096 && aligned16(x)) {
 #define NNC_REDUCE_V4(PER)                                                                             \
     if (len <= 256 * PER) {                                                                            \
-        if (mean) launch(name, reduce_rows_v4_k<true, PER>, grid, dim3(256), 0, x, y, outer, (int)len);  \
-        else launch(name, reduce_rows_v4_k<false, PER>, grid, dim3(256), 0, x, y, outer, (int)len);      \
+        if (mean) launch(name, reduce_rows_v4_k<true, PER>, grid_v4, dim3(256), 0, x, y, outer, (int)len); \
+        else launch(name, reduce_rows_v4_k<false, PER>, grid_v4, dim3(256), 0, x, y, outer, (int)len); \
         return;                                                                                        \
     }
             NNC_REDUCE_V4(1)

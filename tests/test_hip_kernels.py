@@ -316,3 +316,33 @@ def test_maxpool_3x3s2_bit_exact(shape, hip, dmem, abi, oracle_lib):
     exp = caserun.run_case(oracle_lib, case, abi)["out"]
     got = caserun.run_case(hip, case, abi, dmem)["out"]
     assert caserun.same_bits(got, exp), f"{case['name']}: {np.sum(got.view(np.uint32) != exp.view(np.uint32))} differ"
+
+
+# Row kernels past the grid cap (more than 16384 rows: each wave walks
+# several rows, loading the next while it reduces the current), and a row of
+# the largest register-resident length (4096 floats, no prefetch)
+ROW_SHAPES = [(40000, 64), (20000, 260), (17, 4096)]
+
+
+@pytest.mark.parametrize("shape", ROW_SHAPES, ids=[str(s) for s in ROW_SHAPES])
+def test_row_kernels_many_rows(shape, hip, dmem, abi, oracle_lib):
+    rows, dim = shape
+    rng = np.random.default_rng(17)
+    x = (rng.standard_normal((rows, dim)) * 3).astype(np.float32)
+    cases = [
+        {"name": "softmax", "op": "nnc_softmax", "tensors": {"x": x, "out": np.zeros_like(x)},
+         "args": [("t", "x"), ("t", "out"), ("i", -1)], "outputs": ["out"], "bar": "fp"},
+        {"name": "layernorm", "op": "nnc_layernorm",
+         "tensors": {"x": x, "g": rng.standard_normal(dim).astype(np.float32),
+                     "b": rng.standard_normal(dim).astype(np.float32), "out": np.zeros_like(x)},
+         "args": [("t", "x"), ("t", "g"), ("t", "b"), ("t", "out"), ("i", -1), ("f", 1e-5)],
+         "outputs": ["out"], "bar": "fp"},
+        {"name": "reducemean", "op": "nnc_reducemean",
+         "tensors": {"x": x, "out": np.zeros((rows, 1), np.float32)},
+         "args": [("t", "x"), ("t", "out"), ("i", 1), ("i", 1)], "outputs": ["out"], "bar": "fp"},
+    ]
+    for case in cases:
+        print(f"case {case['name']} {shape}", flush=True)
+        exp = caserun.run_case(oracle_lib, case, abi)["out"]
+        got = caserun.run_case(hip, case, abi, dmem)["out"]
+        _check(got, exp, f"{case['name']} {shape}")
