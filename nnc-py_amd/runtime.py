@@ -13,6 +13,7 @@ There is no CPU fallback: every nnc_* call goes to the gfx950 kernels.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
@@ -64,11 +65,12 @@ class HipError(RuntimeError):
 
 
 def load(path: Path | str | None = None) -> ctypes.CDLL:
-    """Load (once) and bind libnnc_hip.so. Raises if it is missing."""
+    """Load (once) and bind libnnc_hip.so (`path`, else $NNC_HIP_LIB, else
+    the in-tree build). Raises if it is missing."""
     global _lib
     if _lib is not None:
         return _lib
-    p = Path(path) if path else LIB_PATH
+    p = Path(path or os.environ.get("NNC_HIP_LIB") or LIB_PATH)
     if not p.exists():
         raise HipError(f"{p} is not built; run `python nnc-py_amd/build.py` (or __graft_entry__.build())")
     # RTLD_LOCAL: the library's nnc_* names must not interpose on another
