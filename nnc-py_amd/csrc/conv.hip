@@ -46,6 +46,7 @@ struct ConvArgs {
     int ldw;  // weight row stride in floats (packed weights may pad K)
     int tiles_m, tiles_n;
     int vec_out;  // out (and res) 16-byte aligned: the fixup may store float4
+    int out32;    // output (and residual) below 2 GiB: whole tiles use 32-bit buffer offsets
 };
 
 // B operand: gathers input taps for X consecutive output pixels; each thread
@@ -222,10 +223,76 @@ __device__ void conv_finish_tile(const ConvArgs& a, int t, int g0, int g1, int f
 // on the tile, and the last to arrive finishes the tile (no spinning: no
 // workgroup ever waits for another); the last arriver also returns the
 // counter to zero for the next kernel.
-template <class T, bool FIN>
+// A whole tile straight to the output: bias (+ residual) + act per element
+// in the order of the per-element path below (same bits). The tile goes out
+// one 32-row block (tm) at a time, every bias and residual load of a block
+// issued before its first store: one memory round trip per block (loads
+// interleaved with stores made the compiler wait for each element's load -
+// and, counting in order, for every earlier store). Out-of-range rows and
+// pixels get an out-of-range buffer offset: loads read 0, stores are
+// dropped. Needs output (and residual) below 2 GiB.
+template <class T, bool RES>
+__device__ __forceinline__ void store_tile(const ConvArgs& a, int i0, int j0, const floatx16 (&sum)[T::TM][T::TN]) {
+    const int hw = a.Ho * a.Wo;
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias), rr = make_rsrc(a.res), ro = make_rsrc(a.out);
+    uint32_t pbase[T::TN];  // element offset of (pixel, channel 0), or kOutOfRange
+#pragma unroll
+    for (int tn = 0; tn < T::TN; ++tn) {
+        const int pix = j0 + acc_col<T>(tn);
+        const int n = pix / hw;
+        pbase[tn] = pix < a.Npix ? (uint32_t)(n * a.Co * hw + (pix - n * hw)) : kOutOfRange;
+    }
+    const int co0 = i0 + acc_row<T>(0, 0);  // this lane's first row; row (tm, r) adds a wave-uniform step
+    const int act = a.act;
+#pragma unroll
+    for (int tm = 0; tm < T::TM; ++tm) {
+        float bv[16];
+        float rv[T::TN][16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int co = co0 + tm * 32 + 8 * (r >> 2) + (r & 3);
+            bv[r] = a.bias ? load_f32(rb, co < a.Co ? (uint32_t)co * 4u : kOutOfRange) : 0.f;
+        }
+        if (RES) {
+#pragma unroll
+            for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int co = co0 + tm * 32 + 8 * (r >> 2) + (r & 3);
+                    const bool ok = pbase[tn] != kOutOfRange && co < a.Co;
+                    rv[tn][r] = load_f32(rr, ok ? (pbase[tn] + (uint32_t)(co * hw)) * 4u : kOutOfRange);
+                }
+        }
+#pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int co = co0 + tm * 32 + 8 * (r >> 2) + (r & 3);
+                const bool ok = pbase[tn] != kOutOfRange && co < a.Co;
+                float v = sum[tm][tn][r] + bv[r];
+                if (RES) v += rv[tn][r];
+                v = activate(v, act);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ro,
+                                                      (int)(ok ? (pbase[tn] + (uint32_t)(co * hw)) * 4u : kOutOfRange),
+                                                      0, 0);
+            }
+    }
+}
+
+// BATCHED: whole tiles through store_tile. 128x128 tiles keep the
+// per-element path: their kernels are at the register limit, and the
+// block's loads held live made the 3x3 kernel's main loop 3x slower.
+template <class T, bool FIN, bool BATCHED = (T::BM * T::BN < 128 * 128)>
 __device__ __forceinline__ void conv_segment_out(const ConvArgs& a, const StreamK& sk, const Segment& seg, int g,
                                                  int i0, int j0, const floatx16 (&sum)[T::TM][T::TN]) {
     const int hw = a.Ho * a.Wo;
+    if (BATCHED && seg.slot < 0 && a.out32) {
+        if (a.res)
+            store_tile<T, true>(a, i0, j0, sum);
+        else
+            store_tile<T, false>(a, i0, j0, sum);
+        return;
+    }
     if (seg.slot < 0) {
 #pragma unroll
         for (int tn = 0; tn < T::TN; ++tn) {
@@ -899,6 +966,7 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     a.ldw = (int)K;
     a.Npix = (int)npix;
     a.vec_out = aligned16(a.out) && (!a.res || aligned16(a.res));
+    a.out32 = (int64_t)a.N * a.Co * a.Ho * a.Wo * 4 < ((int64_t)1 << 31);
     // direct-to-LDS kernels: tap-major weights (1x1 weights already are)
     const bool dma_ok = a.Ci % 32 == 0 && aligned16(a.w) && ((kh == 3 && kw == 3) || (kh == 1 && kw == 1));
     bool stem = false;
@@ -944,6 +1012,12 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     // ones (1x1, the 3-channel stem) and small images run best on 64x64
     // tiles, whose shorter per-tile latency and larger tile count fill the
     // GPU.
+#ifdef NNC_1X1_TILE
+    if (kh == 1 && kw == 1 && dma) {
+        if (NNC_1X1_TILE == 2) return launch_conv<ConvT128>(a, avec, dma, name);
+        if (NNC_1X1_TILE == 1) return launch_conv<ConvT64>(a, avec, dma, name);
+    }
+#endif
     if (a.K >= 512 && a.Co >= 128 && a.Npix >= 1024)
         launch_conv<ConvT128>(a, avec, dma, name);
     else if (a.K >= 512 && a.Co <= 64 && a.Npix >= 4096)

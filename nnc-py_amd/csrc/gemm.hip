@@ -34,6 +34,7 @@ struct GemmArgs {
     int c_mode;  // 0 none, 1 C[j], 2 C[i*N + j]
     int relu;
     int tiles_m, tiles_n, splits;  // splits: K-split count of the GEMV path
+    int out32;  // one batch of out (and C) below 2 GiB: whole tiles use 32-bit buffer offsets
 };
 
 __device__ __forceinline__ float gemm_finish(const GemmArgs& g, int i, int j, float v) {
@@ -42,6 +43,54 @@ __device__ __forceinline__ float gemm_finish(const GemmArgs& g, int i, int j, fl
     else if (g.c_mode == 2) o += g.beta * g.C[(int64_t)i * g.N + j];
     if (g.relu) o = o > 0.0f ? o : 0.0f;
     return o;
+}
+
+// A whole output tile: alpha*v (+ beta*C) (+ relu) per element as
+// gemm_finish, one 32-row block (tm) at a time with the block's C loads
+// issued before its first store - one memory round trip per block (C may
+// alias out as far as the compiler knows, so per-element loads after stores
+// were serialised, each waiting for the earlier stores). Out-of-range rows
+// and columns get an out-of-range buffer offset: loads read 0, stores are
+// dropped.
+template <class T>
+__device__ __forceinline__ void gemm_store_tile(const GemmArgs& g, int batch, int i0, int j0,
+                                                const floatx16 (&sum)[T::TM][T::TN]) {
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(g.out + batch * g.so), rc = make_rsrc(g.C);
+    int jj[T::TN];
+    float cj[T::TN];  // C[j] (c_mode 1)
+#pragma unroll
+    for (int tn = 0; tn < T::TN; ++tn) {
+        jj[tn] = j0 + acc_col<T>(tn);
+        cj[tn] = g.c_mode == 1 ? load_f32(rc, jj[tn] < g.N ? (uint32_t)jj[tn] * 4u : kOutOfRange) : 0.f;
+    }
+    const int ib = i0 + acc_row<T>(0, 0);  // this lane's first row; row (tm, r) adds a wave-uniform step
+#pragma unroll
+    for (int tm = 0; tm < T::TM; ++tm) {
+        float cv[T::TN][16];
+        if (g.c_mode == 2) {
+#pragma unroll
+            for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int i = ib + tm * 32 + 8 * (r >> 2) + (r & 3);
+                    const bool ok = i < g.M && jj[tn] < g.N;
+                    cv[tn][r] = load_f32(rc, ok ? (uint32_t)(i * g.N + jj[tn]) * 4u : kOutOfRange);
+                }
+        }
+#pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = ib + tm * 32 + 8 * (r >> 2) + (r & 3);
+                const bool ok = i < g.M && jj[tn] < g.N;
+                float o = g.alpha * sum[tm][tn][r];
+                if (g.c_mode == 1) o += g.beta * cj[tn];
+                else if (g.c_mode == 2) o += g.beta * cv[tn][r];
+                if (g.relu) o = o > 0.0f ? o : 0.0f;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), ro,
+                                                      (int)(ok ? (uint32_t)(i * g.N + jj[tn]) * 4u : kOutOfRange), 0, 0);
+            }
+    }
 }
 
 // Loader kinds: element (x, k) at base[x*ld + k] (K*) or base[k*ld + x] (X*)
@@ -89,7 +138,10 @@ __global__ void __launch_bounds__(256, 2) gemm_streamk_k(GemmArgs g, StreamK sk)
         lb.init(g.B + batch * g.sb + PB::offset(j0, g.ldb), g.ldb, g.N - j0, g.K);
         floatx16 sum[T::TM][T::TN];
         mfma_mainloop<T, true>(la, lb, seg.kb * T::BK, min(g.K, seg.ke * T::BK), lds, sum);
-        if (seg.slot < 0) {
+        // (128x128 tiles keep the per-element path: their kernels are at the register limit)
+        if (T::BM * T::BN < 128 * 128 && seg.slot < 0 && g.out32) {
+            gemm_store_tile<T>(g, batch, i0, j0, sum);
+        } else if (seg.slot < 0) {
 #pragma unroll
             for (int tn = 0; tn < T::TN; ++tn) {
                 const int j = j0 + acc_col<T>(tn);
@@ -334,6 +386,7 @@ static void gemm_run(const GemmProblem& p, const char* name) {
     g.c_mode = p.c_mode;
     g.relu = p.relu;
     g.splits = 1;
+    g.out32 = (int64_t)p.M * p.N * 4 < ((int64_t)1 << 31);
     if (p.K <= 0) {
         // empty contraction: out = beta*C (alpha*0)
         GemmArgs z = g;
