@@ -133,26 +133,61 @@ struct ConvGather {
 
 // Bias (+ residual) + act for 4 consecutive output pixels p0..p0+3 of
 // channel co (one row of a tile), float4 when they are in one image and the
-// output (and residual) are 16-byte aligned.
-__device__ __forceinline__ void fixup_store(const ConvArgs& a, int co, int p0, float4 v) {
+// output (and residual) are 16-byte aligned. Split into the loads
+// (fixup_load) and the arithmetic and stores (fixup_apply), so a thread
+// finishing several rows issues all its loads before its first store: the
+// compiler cannot move a load above a store that may alias it.
+struct FixupIn {
+    float b;
+    float4 r;
+};
+
+__device__ __forceinline__ bool fixup_vec(const ConvArgs& a, int p0) {
+    return a.vec_out && ((a.Ho * a.Wo) & 3) == 0 && p0 + 3 < a.Npix;
+}
+
+__device__ __forceinline__ FixupIn fixup_load(const ConvArgs& a, int co, int p0) {
     const int hw = a.Ho * a.Wo;
-    const float b = a.bias ? a.bias[co] : 0.f;
-    const int n = p0 / hw;
-    const int64_t o = ((int64_t)n * a.Co + co) * hw + (p0 - n * hw);
-    if (a.vec_out && (hw & 3) == 0 && p0 + 3 < a.Npix) {
+    FixupIn f;
+    f.b = a.bias ? a.bias[co] : 0.f;
+    f.r = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!a.res) return f;
+    if (fixup_vec(a, p0)) {
+        const int n = p0 / hw;
+        f.r = *reinterpret_cast<const float4*>(a.res + ((int64_t)n * a.Co + co) * hw + (p0 - n * hw));
+        return f;
+    }
+    float r[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int pix = p0 + q;
+        if (pix >= a.Npix) break;
+        const int nq = pix / hw;
+        r[q] = a.res[((int64_t)nq * a.Co + co) * hw + (pix - nq * hw)];
+    }
+    f.r = make_float4(r[0], r[1], r[2], r[3]);
+    return f;
+}
+
+__device__ __forceinline__ void fixup_apply(const ConvArgs& a, int co, int p0, float4 v, const FixupIn& f) {
+    const int hw = a.Ho * a.Wo;
+    const float b = f.b;
+    if (fixup_vec(a, p0)) {
+        const int n = p0 / hw;
+        const int64_t o = ((int64_t)n * a.Co + co) * hw + (p0 - n * hw);
         float4 x = make_float4(v.x + b, v.y + b, v.z + b, v.w + b);
         if (a.res) {
-            const float4 r = *reinterpret_cast<const float4*>(a.res + o);
-            x.x += r.x;
-            x.y += r.y;
-            x.z += r.z;
-            x.w += r.w;
+            x.x += f.r.x;
+            x.y += f.r.y;
+            x.z += f.r.z;
+            x.w += f.r.w;
         }
         *reinterpret_cast<float4*>(a.out + o) =
             make_float4(activate(x.x, a.act), activate(x.y, a.act), activate(x.z, a.act), activate(x.w, a.act));
         return;
     }
     const float vals[4] = {v.x, v.y, v.z, v.w};
+    const float rs[4] = {f.r.x, f.r.y, f.r.z, f.r.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int pix = p0 + q;
@@ -160,9 +195,13 @@ __device__ __forceinline__ void fixup_store(const ConvArgs& a, int co, int p0, f
         const int nq = pix / hw;
         const int64_t oq = ((int64_t)nq * a.Co + co) * hw + (pix - nq * hw);
         float x = vals[q] + b;
-        if (a.res) x += a.res[oq];
+        if (a.res) x += rs[q];
         a.out[oq] = activate(x, a.act);
     }
+}
+
+__device__ __forceinline__ void fixup_store(const ConvArgs& a, int co, int p0, float4 v) {
+    fixup_apply(a, co, p0, v, fixup_load(a, co, p0));
 }
 
 // Partial tiles are written and read with device-scope coherence (the
@@ -207,12 +246,21 @@ __device__ void conv_finish_tile(const ConvArgs& a, int t, int g0, int g1, int f
 #pragma unroll
             for (int e = 0; e < CH; ++e) v[e] += p[e];
         }
+        // the chunk's bias / residual loads, then its stores
+        FixupIn fin[CH];
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
             const int e4 = (e0 + e) * 256 + threadIdx.x;
             const int co = mt * T::BM + (e4 * 4) / T::BN;
             const int p0 = nt * T::BN + (e4 * 4) % T::BN;
-            if (co < a.Co && p0 < a.Npix) fixup_store(a, co, p0, make_float4(v[e].x, v[e].y, v[e].z, v[e].w));
+            if (co < a.Co && p0 < a.Npix) fin[e] = fixup_load(a, co, p0);
+        }
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            const int e4 = (e0 + e) * 256 + threadIdx.x;
+            const int co = mt * T::BM + (e4 * 4) / T::BN;
+            const int p0 = nt * T::BN + (e4 * 4) % T::BN;
+            if (co < a.Co && p0 < a.Npix) fixup_apply(a, co, p0, make_float4(v[e].x, v[e].y, v[e].z, v[e].w), fin[e]);
         }
     }
 }
