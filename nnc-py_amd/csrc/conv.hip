@@ -511,12 +511,15 @@ struct PixelTaps {
             }
     }
     __device__ bool inside(int tap) const { return ((mask >> tap) & 1u) != 0; }
+    __device__ uint32_t bit(int tap) const { return (uint32_t)(mask >> tap) & 1u; }
 };
 
 template <class T, int KH, int KW>
 struct DmaPacked {
     typedef DmaStage<T> D;
     static constexpr bool kFinishInKernel = true;
+    static constexpr int EXTRA_LDS_FLOATS = 0;
+    __device__ void prepare(float*, const ConvArgs&) {}
     static constexpr int A_LOADS = T::BM / (8 * T::NW);  // dwordx4 loads per wave per slice, 8 rows each
     static_assert(T::BM % (8 * T::NW) == 0, "A rows split evenly over the waves");
     __amdgpu_buffer_rsrc_t rin, rw;
@@ -585,10 +588,17 @@ struct DmaSmallC {
     // (the in-kernel finish's registers would cost this kernel occupancy)
     static constexpr bool kFinishInKernel = false;
     static constexpr int A_LOADS = T::BM / (8 * T::NW);
+    static constexpr int KMAX = 256;  // table entries (Kp <= KMAX, checked on the host)
+    static_assert(KH * KW < 64, "tap 63 marks k >= K");
+    // per k of the packed rows, filled once per workgroup: the byte offset of
+    // (channel, tap) from the pixel's (0, 0) tap at channel 0, and the tap
+    // index for the in-image bit (63 past K: never inside)
+    static constexpr int EXTRA_LDS_FLOATS = 2 * KMAX;
     __amdgpu_buffer_rsrc_t rin, rw;
-    int wave, b_grp, b_kr0, HW, W, K;
+    int wave, b_grp, b_kr0;
     uint32_t avo[A_LOADS];
     PixelTaps<KH, KW> px;
+    const int* tab;
     int k0;  // slice cursor
 
     __device__ void init(const ConvArgs& a, int wave_, int lane) {
@@ -597,9 +607,18 @@ struct DmaSmallC {
         wave = wave_;
         b_grp = wave % D::PX_GROUPS;
         b_kr0 = (wave / D::PX_GROUPS) * D::B_LOADS;
-        HW = a.H * a.W;
-        W = a.W;
-        K = a.K;
+    }
+    // fills the table (the caller's barrier publishes it)
+    __device__ void prepare(float* extra, const ConvArgs& a) {
+        int* t = reinterpret_cast<int*>(extra);
+        for (int k = threadIdx.x; k < KMAX; k += T::THREADS) {
+            const int tap = k / CI, ci = k - tap * CI;
+            const int r = tap / KW, c = tap - r * KW;
+            const bool in = k < a.K;
+            t[2 * k] = in ? (ci * (a.H * a.W) + r * a.W + c) * 4 : 0;
+            t[2 * k + 1] = in ? tap : 63;
+        }
+        tab = t;
     }
     __device__ void tile(const ConvArgs& a, int i0, int j0, int lane) {
         const int a_kc = (lane & 7) ^ ((lane >> 3) & 7);
@@ -620,14 +639,21 @@ struct DmaSmallC {
         }
         constexpr int H = D::B_LOADS / 2;
         float* d0 = S + D::A_FLOATS + b_kr0 * T::BN + b_grp * 64;
+        // this half's H table entries (broadcast LDS reads), then per load
+        // one add and a bit select: no per-load division or branch
+        const int kstart = k0 + b_kr0 + part * H;
+        int e[2 * H];
 #pragma unroll
-        for (int i = part * H; i < (part + 1) * H; ++i) {
-            const int k = k0 + b_kr0 + i;  // uniform
-            const bool kin = k < K;
-            const int tap = k / CI, ci = k - tap * CI;
-            const int r = tap / KW, c = tap - r * KW;
-            const uint32_t v = keep_or_oob((uint32_t)(px.bpo + r * W + c) * 4u, on && kin && px.inside(tap));
-            dma_load4(rin, d0 + i * T::BN, v, kin ? (uint32_t)(ci * HW) * 4u : 0u);
+        for (int q = 0; q < 2 * H; q += 4) {
+            const int4 v = *reinterpret_cast<const int4*>(tab + 2 * kstart + q);
+            e[q] = v.x, e[q + 1] = v.y, e[q + 2] = v.z, e[q + 3] = v.w;
+        }
+        const uint32_t base = (uint32_t)px.bpo * 4u;
+        const uint32_t onm = 0u - (uint32_t)on;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const uint32_t m = (0u - px.bit(e[2 * i + 1])) & onm;
+            dma_load4(rin, d0 + (part * H + i) * T::BN, ((base + (uint32_t)e[2 * i]) & m) | (kOutOfRange & ~m), 0u);
         }
     }
 };
@@ -660,6 +686,10 @@ __global__ void __launch_bounds__(T::THREADS, DmaStage<T>::MIN_WAVES) conv_dma_k
     const int b_off = D::A_FLOATS + 16 * (lane >> 5) * T::BN + wj + (lane & 31);
     L ld;
     ld.init(a, wave, lane);
+    if (L::EXTRA_LDS_FLOATS) {
+        ld.prepare(lds + 2 * D::STAGE, a);
+        __syncthreads();
+    }
 
     SegmentWalker walk(sk, g);
     Segment seg;
@@ -864,7 +894,7 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
     constexpr bool FIN = kInKernelFixup && L::kFinishInKernel && T::NW == 4 &&
                          ((T::BM == 64 && T::BN == 128) || (NNC_CONV_FIN128 && T::BM == 128 && T::BN == 128));
     auto kernel = conv_dma_k<T, L, FIN>;
-    const size_t lds = (size_t)DmaStage<T>::LDS_FLOATS * sizeof(float);
+    const size_t lds = (size_t)(DmaStage<T>::LDS_FLOATS + L::EXTRA_LDS_FLOATS) * sizeof(float);
     static bool configured = false;
     static int slots = 0;
     if (!configured) {
@@ -1025,6 +1055,7 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
         if (!(kh == 7 && kw == 7 && a.Ci == 3 && aligned16(a.w)))
             return fail(NNC_HIP_EUNSUPP, name, "[Co][Kp] packed weights need a 7x7 kernel, 3 channels, alignment");
         if (a.Co * kp * 4 >= ((int64_t)1 << 31)) return fail(NNC_HIP_EUNSUPP, name, "weights of 2 GiB or more");
+        if (kp > 256) return fail(NNC_HIP_EUNSUPP, name, "[Co][Kp] packed rows longer than 256");
         a.ldw = (int)kp;
         stem = true;
     } else if (packed) {
