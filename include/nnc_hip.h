@@ -99,6 +99,25 @@ int nnc_hip_graph_end(void);
 int nnc_hip_graph_launch(void);
 void nnc_hip_graph_destroy(void);
 
+/* ---- per-tensor debug dump ------------------------------------------------
+ * Replaces the dump code the reference emits into nnc_run() in debug mode
+ * (src/nnc_py/codegen/x86_emitters/model_source.py:136-184, 297-428): waits
+ * for the library stream, copies the tensor to the host and writes it in the
+ * reference's text format,
+ *   DEBUG_TENSOR_START <name> <node_idx>
+ *   SHAPE <ndim>
+ *   DIM <i> <extent>                      (one line per dimension)
+ *   DATA_START
+ *   <value printed with %f>               (one line per element)
+ *   DATA_END
+ *   DEBUG_TENSOR_END <name>               (then an empty line)
+ * to `file` (a FILE*; NULL: stdout), so the reference's parser
+ * (src/nnc_py/tools/debug_compare.py:17-106) reads it unchanged. Float32
+ * elements print as themselves, bool/uint8/int8 and int32/int64 as their
+ * value converted to float. Not while a graph is being captured
+ * (NNC_HIP_ESTATE). */
+int nnc_hip_debug_dump(const Tensor* t, const char* name, int node_idx, void* file);
+
 /* ---- fused operators of the mi355x target --------------------------------
  * No counterpart in the reference ABI (runtime/include/nnc_ops.h); emitted by
  * the mi355x compiler target at O3.

@@ -86,7 +86,7 @@ class Compiler:
         prog = build_program(graph, self.opt_level, strategy, parse_memory_size(max_memory))
         out = Path(output_dir)
         out.mkdir(parents=True, exist_ok=True)
-        for art in codegen.generate(prog, entry_point, str(REPO_ROOT)):
+        for art in codegen.generate(prog, entry_point, str(REPO_ROOT), debug_mode=self.debug_mode):
             path = out / art.filename
             if art.file_type == "binary":
                 path.write_bytes(art.content)

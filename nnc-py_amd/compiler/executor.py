@@ -162,6 +162,28 @@ class Executor:
         for fn, args in self._calls:
             fn(*args)
 
+    def run_debug(self, path) -> None:
+        """One nnc_run() node by node, writing every node's outputs after it
+        runs to `path` in the debug dump format (nnc_py_amd.tools.
+        debug_compare): the counterpart of the generated program's debug
+        mode. Node indices count the non-constant nodes in topological order,
+        as the reference's dump injection (model_source.py:398-428)."""
+        from ..tools.debug_compare import write_tensor
+        by_node: dict[str, list] = {}
+        for call, fn_args in zip(self.prog.calls, self._calls):
+            by_node.setdefault(call.node, []).append(fn_args)
+        consts = self.prog.graph.constants
+        with open(path, "w") as f:
+            idx = 0
+            for node in self.prog.order:
+                for fn, args in by_node.get(node.name, []):
+                    fn(*args)
+                for out in node.outputs:
+                    if out in consts or out not in self.prog.plan.offsets:
+                        continue
+                    write_tensor(f, out, idx, self.get(out))
+                idx += 1
+
     def capture(self) -> None:
         """Record run() into a hipGraph (device only); replay() launches it."""
         self.rt.check(self.lib.nnc_hip_graph_begin(), "nnc_hip_graph_begin")

@@ -372,6 +372,52 @@ int nnc_hip_profile_work(int i, double* flops, double* bytes) {
     return NNC_HIP_OK;
 }
 
+int nnc_hip_debug_dump(const Tensor* t, const char* name, int node_idx, void* file) {
+    const char* fn = "nnc_hip_debug_dump";
+    if (!ready(fn)) return NNC_HIP_ESTATE;
+    if (g_ctx.capturing) {
+        fail(NNC_HIP_ESTATE, fn, "cannot dump while a graph is being captured");
+        return NNC_HIP_ESTATE;
+    }
+    if (!t || !t->data || !name || (t->ndim > 0 && !t->shape) || t->nbytes < 0) {
+        fail(NNC_HIP_EINVAL, fn, "NULL tensor, data, shape or name");
+        return NNC_HIP_EINVAL;
+    }
+    int64_t n = 1;
+    for (int d = 0; d < t->ndim; ++d) n *= t->shape[d];
+    size_t esize = 4;
+    switch (t->dtype) {
+        case NNC_DTYPE_BOOL: case NNC_DTYPE_INT8: case NNC_DTYPE_UINT8: esize = 1; break;
+        case NNC_DTYPE_FLOAT16: esize = 2; break;
+        case NNC_DTYPE_INT64: esize = 8; break;
+        default: esize = 4; break;
+    }
+    if (n < 0 || (size_t)n * esize > (size_t)t->nbytes) n = (int64_t)((size_t)t->nbytes / esize);
+    std::vector<unsigned char> host((size_t)t->nbytes);
+    if (!host.empty() && nnc_hip_memcpy_d2h(host.data(), t->data, host.size()) != NNC_HIP_OK) return NNC_HIP_EDEVICE;
+    FILE* f = file ? static_cast<FILE*>(file) : stdout;
+    fprintf(f, "DEBUG_TENSOR_START %s %d\n", name, node_idx);
+    fprintf(f, "SHAPE %d\n", t->ndim);
+    for (int d = 0; d < t->ndim; ++d) fprintf(f, "DIM %d %d\n", d, (int)t->shape[d]);
+    fprintf(f, "DATA_START\n");
+    const unsigned char* b = host.data();
+    for (int64_t i = 0; i < n; ++i) {
+        float v;
+        switch (t->dtype) {
+            case NNC_DTYPE_BOOL: case NNC_DTYPE_UINT8: v = (float)b[i]; break;
+            case NNC_DTYPE_INT8: v = (float)reinterpret_cast<const int8_t*>(b)[i]; break;
+            case NNC_DTYPE_INT32: v = (float)reinterpret_cast<const int32_t*>(b)[i]; break;
+            case NNC_DTYPE_INT64: v = (float)reinterpret_cast<const int64_t*>(b)[i]; break;
+            case NNC_DTYPE_FLOAT16: v = (float)reinterpret_cast<const _Float16*>(b)[i]; break;
+            default: v = reinterpret_cast<const float*>(b)[i]; break;
+        }
+        fprintf(f, "%f\n", (double)v);
+    }
+    fprintf(f, "DATA_END\n");
+    fprintf(f, "DEBUG_TENSOR_END %s\n\n", name);
+    return ferror(f) ? NNC_HIP_EINVAL : NNC_HIP_OK;
+}
+
 int nnc_hip_graph_begin(void) {
     if (!ready("nnc_hip_graph_begin")) return NNC_HIP_ESTATE;
     nnc_hip_graph_destroy();

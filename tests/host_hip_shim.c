@@ -6,6 +6,8 @@
  * memcpy; graph capture reports "unsupported" so generated code takes its
  * node-by-node path. Never linked into the product.
  */
+#include <stdint.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -53,3 +55,23 @@ int nnc_hip_graph_begin(void) { return NNC_HIP_EUNSUPP; }
 int nnc_hip_graph_end(void) { return NNC_HIP_EUNSUPP; }
 int nnc_hip_graph_launch(void) { return NNC_HIP_EUNSUPP; }
 void nnc_hip_graph_destroy(void) {}
+/* the dump format of nnc_hip_debug_dump, for float32 / uint8 / int64 tensors in host memory */
+int nnc_hip_debug_dump(const Tensor* t, const char* name, int node_idx, void* file) {
+    FILE* f = file ? (FILE*)file : stdout;
+    int64_t n = 1;
+    for (int d = 0; d < t->ndim; ++d) n *= t->shape[d];
+    fprintf(f, "DEBUG_TENSOR_START %s %d\n", name, node_idx);
+    fprintf(f, "SHAPE %d\n", t->ndim);
+    for (int d = 0; d < t->ndim; ++d) fprintf(f, "DIM %d %d\n", d, (int)t->shape[d]);
+    fprintf(f, "DATA_START\n");
+    for (int64_t i = 0; i < n; ++i) {
+        float v;
+        if (t->dtype == NNC_DTYPE_BOOL || t->dtype == NNC_DTYPE_UINT8) v = (float)((const uint8_t*)t->data)[i];
+        else if (t->dtype == NNC_DTYPE_INT64) v = (float)((const int64_t*)t->data)[i];
+        else v = ((const float*)t->data)[i];
+        fprintf(f, "%f\n", (double)v);
+    }
+    fprintf(f, "DATA_END\n");
+    fprintf(f, "DEBUG_TENSOR_END %s\n\n", name);
+    return 0;
+}
