@@ -67,12 +67,31 @@ int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int nnc_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
 
 /* ---- synchronisation and errors ---------------------------------------- */
-int nnc_hip_sync(void);             /* waits for the library stream */
-void* nnc_hip_stream(void);         /* the hipStream_t, for callers that
-                                       order their own work after ours */
+int nnc_hip_sync(void);             /* waits for the library streams */
+void* nnc_hip_stream(void);         /* stream 0's hipStream_t, for callers
+                                       that order their own work after ours */
 int nnc_hip_last_error(void);       /* last non-zero code since reset */
 const char* nnc_hip_last_error_message(void);
 void nnc_hip_clear_error(void);
+
+/* ---- a second stream for independent branches ---------------------------
+ * Calls go to stream 0 unless stream 1 is selected. The compiler's O3
+ * schedule (mi355x target) runs a branch that only depends on the fork
+ * point - a residual block's 1x1 downsample convolution - on stream 1 while
+ * the main branch continues on stream 0:
+ *   nnc_hip_stream_fork();       stream 1 waits for stream 0's work so far
+ *   nnc_hip_stream_select(1); ...branch calls...; nnc_hip_stream_select(0);
+ *   ...main calls...
+ *   nnc_hip_stream_join();       stream 0 waits for stream 1's work so far
+ * Both streams have default priority and their own scratch (stream-K
+ * partials, counters), so concurrent calls never share it; nnc_hip_sync and
+ * the host copies wait for both. A graph capture starts and ends on stream
+ * 0 and records forked branches as parallel graph branches. No counterpart
+ * in the reference, whose O3 executor runs its resource queues on host
+ * threads (codegen/x86_emitters/model_source.py:502-735). */
+int nnc_hip_stream_fork(void);
+int nnc_hip_stream_select(int slot);
+int nnc_hip_stream_join(void);
 
 /* ---- per-kernel timing --------------------------------------------------
  * While enabled, every kernel launch is bracketed by hipEvents recorded on

@@ -15,15 +15,16 @@ implementation of the ABI and runs nnc_run()'s call sequence through ctypes:
 from __future__ import annotations
 
 import ctypes
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 
 from .. import abi
 from .ir import Graph, Node
 from .lower import Call, lower
-from .passes import (MemoryPlan, check_plan, eliminate_dead_code, eliminate_identity, fuse_matmul_bias, fuse_patterns,
-                     fuse_residual, pack_conv_weights, plan_memory, prepack_lowering)
+from .passes import (Branch, MemoryPlan, branch_calls, check_plan, eliminate_dead_code, eliminate_identity,
+                     find_branches, fuse_matmul_bias, fuse_patterns, fuse_residual, pack_conv_weights, plan_memory,
+                     prepack_lowering)
 
 
 @dataclass
@@ -33,21 +34,34 @@ class Program:
     plan: MemoryPlan
     calls: list[Call]
     opt_level: int
+    branches: list[Branch] = field(default_factory=list)  # side branches on stream 1 (O3)
 
 
 # Conv -> Add -> Relu fusion into nnc_hip_conv_add_relu at O3 (mi355x target).
 RESIDUAL_FUSION = True
 # tap-major 3x3 conv weights and nnc_hip_conv_packed at O3 (mi355x target).
 PACK_CONV_WEIGHTS = True
+# independent side branches (ResNet's downsample convolutions) on the second
+# library stream at O3 (mi355x target), while the main branch's convolutions
+# total at most BRANCH_MAX_FLOPS: two kernels overlap only while neither fills
+# the GPU. Off by default: on ResNet-18 the overlap measured 3% slower at
+# batch 1 (3261 vs 3374 img/s), +0.4% at batch 8 and -0.4% at batch 32; the
+# overlapped 1x1 convolution slows from 10.8 to 14.2 us and the cross-stream
+# edges of the captured graph cost more than the overlap saves.
+BRANCH_STREAMS = False
+BRANCH_MAX_FLOPS = 1e9
 
 
 def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None = None,
-                  max_memory: int | None = None, target_passes: bool = True) -> Program:
+                  max_memory: int | None = None, target_passes: bool = True,
+                  branch_streams: bool | None = None) -> Program:
     """Pass pipeline per optimisation level (passes/base.py:67-161 of the
     reference), arena plan, lowering. Mutates `graph`. `target_passes`
     False leaves out the mi355x target's own O3 rewrites (residual fusion,
     MatMul+bias fusion, packed conv weights, view aliasing), giving the call
-    sequence of the reference's own O3 pipeline for the reference runtime."""
+    sequence of the reference's own O3 pipeline for the reference runtime.
+    `branch_streams` (default BRANCH_STREAMS) runs independent side branches
+    on the second library stream at O3."""
     if opt_level >= 1:
         eliminate_identity(graph)
         eliminate_dead_code(graph)
@@ -61,10 +75,16 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
                 pack_conv_weights(graph)
         prepack_lowering(graph)
     order = graph.topological_sort()
+    branches = (find_branches(graph, order, BRANCH_MAX_FLOPS)
+                if opt_level >= 3 and target_passes and (BRANCH_STREAMS if branch_streams is None else branch_streams)
+                else [])
+    groups = [[b.side] + b.main for b in branches]
     strategy = memory_strategy or ("basic" if opt_level == 0 else "cost_aware")
-    plan = plan_memory(graph, order, strategy, max_memory, alias_views=opt_level >= 3 and target_passes)
-    check_plan(graph, order, plan)
-    return Program(graph, order, plan, lower(graph, order, plan.aliases), opt_level)
+    plan = plan_memory(graph, order, strategy, max_memory, alias_views=opt_level >= 3 and target_passes,
+                       concurrent=groups)
+    check_plan(graph, order, plan, groups)
+    calls = branch_calls(lower(graph, order, plan.aliases), branches, lambda op, args: Call(op, args, ""))
+    return Program(graph, order, plan, calls, opt_level, branches)
 
 
 class Executor:
@@ -95,7 +115,7 @@ class Executor:
             self.tensors[name] = ten
         for name, t in g.constants.items():
             self._write(name, t.data)
-        self._calls = [(getattr(self.lib, c.op), self._args(c)) for c in prog.calls]
+        self._calls = [(self._fn(c.op), self._args(c)) for c in prog.calls]
 
     # -- memory --------------------------------------------------------------
     def _addr(self, name: str) -> int:
@@ -128,6 +148,14 @@ class Executor:
         return self._read(name)
 
     # -- calls ---------------------------------------------------------------
+    def _fn(self, op: str):
+        """The library's entry point; the stream fork/select/join calls are
+        no-ops on an implementation without them (a host library runs every
+        call in order anyway)."""
+        if op.startswith("nnc_hip_stream_") and not hasattr(self.lib, op):
+            return lambda *args: 0
+        return getattr(self.lib, op)
+
     def _args(self, call: Call) -> tuple:
         out = []
         for spec in call.args:

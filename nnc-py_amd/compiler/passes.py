@@ -275,10 +275,12 @@ class Liveness:
     is_output: bool = False
 
 
-def liveness(g: Graph, order: list[Node]) -> dict[str, Liveness]:
+def liveness(g: Graph, order: list[Node], concurrent: list[list[str]] | None = None) -> dict[str, Liveness]:
     """[first definition, last use] per non-constant tensor over `order`
     (passes/liveness.py:23-132). Graph inputs are live from step 0, graph
-    outputs to the end."""
+    outputs to the end. Every tensor a node of a `concurrent` group reads or
+    writes stays live to the group's last step, so nothing one member touches
+    is freed (and reused, or written in place) while another may still run."""
     live: dict[str, Liveness] = {}
     last = len(order)
     for name in g.inputs:
@@ -296,6 +298,16 @@ def liveness(g: Graph, order: list[Node]) -> dict[str, Liveness]:
             live[name].is_output = True
     for name in g.inputs:  # inputs stay resident across repeated runs
         live[name].end = last
+    pos = {n.name: i for i, n in enumerate(order)}
+    for group in concurrent or []:
+        members = [order[pos[n]] for n in group if n in pos]
+        if not members:
+            continue
+        end = max(pos[n.name] for n in members)
+        for n in members:
+            for t in list(n.inputs) + list(n.outputs):
+                if t in live:
+                    live[t].end = max(live[t].end, end)
     return live
 
 
@@ -319,7 +331,8 @@ VIEW_OPS = {"Flatten", "Reshape", "Squeeze", "Unsqueeze", "Identity"}
 
 
 def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
-                max_memory: int | None = None, alias_views: bool = False) -> MemoryPlan:
+                max_memory: int | None = None, alias_views: bool = False,
+                concurrent: list[list[str]] | None = None) -> MemoryPlan:
     """Greedy offset assignment over the execution order.
 
     alias_views (mi355x O3): a view op whose input dies there gets the
@@ -331,7 +344,7 @@ def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
     Raises ValueError when the activations exceed max_memory (the reference
     raises the same way when the budget is below the peak node demand,
     cost_aware_allocator.py:88-102)."""
-    live = liveness(g, order)
+    live = liveness(g, order, concurrent)
     sizes = {n: _align(g.tensors[n].nbytes) for n in live}
     plan = MemoryPlan()
     free: list[tuple[int, int]] = []  # (offset, size)
@@ -424,11 +437,11 @@ def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
     return plan
 
 
-def check_plan(g: Graph, order: list[Node], plan: MemoryPlan) -> None:
+def check_plan(g: Graph, order: list[Node], plan: MemoryPlan, concurrent: list[list[str]] | None = None) -> None:
     """Invariants: simultaneously live tensors never overlap (except an
     in-place output and the input it replaces), every offset aligned, every
     tensor inside the arena."""
-    live = liveness(g, order)
+    live = liveness(g, order, concurrent)
     names = list(live)
     for n in plan.offsets:
         assert plan.offsets[n] % ALIGN == 0, n
@@ -443,3 +456,109 @@ def check_plan(g: Graph, order: list[Node], plan: MemoryPlan) -> None:
                 pair = plan.inplace.get(a) == b or plan.inplace.get(b) == a
                 if not pair:
                     raise AssertionError(f"{a} and {b} overlap in time and memory")
+
+
+# ---------------------------------------------------------------------------
+# independent branches on the second library stream (mi355x O3)
+# ---------------------------------------------------------------------------
+CONV_OPS = ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu")
+
+
+def conv_flops(g: Graph, node: Node) -> float:
+    """2 * Co * (N * Ho * Wo) * (Ci * kh * kw) of a convolution node (weights
+    [Co][Ci][kh][kw] or tap-major packed; the output shape gives N*Ho*Wo)."""
+    w = g.tensors[node.inputs[1]]
+    out = g.tensors[node.outputs[0]].shape
+    k = 1
+    for d in w.shape[1:]:
+        k *= int(d)
+    return 2.0 * int(w.shape[0]) * (int(out[0]) * int(out[2]) * int(out[3])) * k
+
+
+@dataclass
+class Branch:
+    """`side` runs on stream 1 from the fork until the join before `join`;
+    `main` are the nodes stream 0 runs meanwhile (between the fork and the
+    join in execution order)."""
+    side: str
+    main: list[str]
+    join: str
+
+
+def find_branches(g: Graph, order: list[Node], max_flops: float) -> list[Branch]:
+    """Side branches for the second stream: a convolution D whose only
+    activation input X has exactly one other consumer A, and whose output
+    has exactly one consumer J - ResNet's 1x1 downsample next to the
+    block's first 3x3 convolution, joined by the residual add (either of
+    the two can be D). The main branch is every node from A (or D, if
+    earlier) up to J; taken only while D and the main branch's convolutions
+    each stay within `max_flops` (two concurrent kernels pay off while
+    neither fills the GPU)."""
+    pos = {n.name: i for i, n in enumerate(order)}
+    consumers: dict[str, list[Node]] = {}
+    for n in order:
+        for t in n.inputs:
+            consumers.setdefault(t, []).append(n)
+    taken: set[str] = set()
+    out: list[Branch] = []
+    for d in order:
+        if d.op_type not in CONV_OPS or d.name in taken:
+            continue
+        acts = [t for t in d.inputs if t and t in g.tensors and not g.tensors[t].is_constant]
+        if len(acts) != 1 or len(d.outputs) != 1:
+            continue
+        others = [c for c in consumers.get(acts[0], []) if c.name != d.name]
+        readers = consumers.get(d.outputs[0], [])
+        if len(others) != 1 or len(readers) != 1 or d.outputs[0] in g.outputs:
+            continue
+        a, j = others[0], readers[0]
+        lo, hi = min(pos[a.name], pos[d.name]), pos[j.name]
+        if pos[a.name] >= hi or pos[d.name] >= hi:
+            continue
+        main = [order[i] for i in range(lo, hi) if order[i].name != d.name]
+        if not main or any(n.name in taken for n in main + [j]):
+            continue
+        # the join must read what the main branch produced
+        made = {t for n in main for t in n.outputs}
+        if not any(t in made for t in j.inputs):
+            continue
+        flops = sum(conv_flops(g, n) for n in main if n.op_type in CONV_OPS)
+        if max(flops, conv_flops(g, d)) > max_flops:
+            continue
+        out.append(Branch(d.name, [n.name for n in main], j.name))
+        taken.update([d.name, j.name] + [n.name for n in main])
+    return out
+
+
+def branch_calls(calls: list, branches: list[Branch], make_call) -> list:
+    """The call list with each branch's side call moved to a fork placed
+    before the branch's first main call (or before its join, if the main
+    nodes made no call), on stream 1, and a join before the join node's call.
+    `make_call(op, args)` builds a call."""
+    if not branches:
+        return calls
+    side_calls = {c.node: c for c in calls}
+    main_of = {n: b for b in branches for n in b.main}
+    join_of = {b.join: b for b in branches}
+    side_nodes = {b.side for b in branches}
+    forked: set[str] = set()
+
+    def fork(b: Branch) -> list:
+        forked.add(b.side)
+        return [make_call("nnc_hip_stream_fork", []), make_call("nnc_hip_stream_select", [("i", 1)]),
+                side_calls[b.side], make_call("nnc_hip_stream_select", [("i", 0)])]
+
+    out = []
+    for c in calls:
+        if c.node in side_nodes:
+            continue  # emitted at its fork
+        b = main_of.get(c.node)
+        if b is not None and b.side not in forked:
+            out += fork(b)
+        b = join_of.get(c.node)
+        if b is not None:
+            if b.side not in forked:
+                out += fork(b)
+            out.append(make_call("nnc_hip_stream_join", []))
+        out.append(c)
+    return out

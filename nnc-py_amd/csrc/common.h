@@ -14,21 +14,30 @@ namespace nnc {
 // ---------------------------------------------------------------------------
 // device context (one per process; the generated code drives one device)
 // ---------------------------------------------------------------------------
+// Library streams: 0 carries every call unless the caller selects 1, the
+// side stream of a forked branch (nnc_hip_stream_fork/select/join). Each
+// stream has its own scratch, so calls running concurrently on the two never
+// share partial tiles, counters or repacked weights.
+static constexpr int kStreams = 2;
+
 struct Context {
     int device = -1;
-    hipStream_t stream = nullptr;
+    hipStream_t stream = nullptr;  // the selected stream (streams[cur])
+    hipStream_t streams[kStreams] = {};
+    int cur = 0;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     char* arena = nullptr;
     size_t arena_bytes = 0;
-    // split-K partials and other per-call scratch; grown outside capture only
-    float* workspace = nullptr;
-    size_t workspace_bytes = 0;
-    // per-tile arrival counters of the stream-K kernels; zero between kernels
-    // (each kernel returns the counters it used to zero)
-    int* counters = nullptr;
-    size_t counters_n = 0;
-    // tap-major copies of reference-layout conv weights (grown outside capture)
-    float* repack = nullptr;
-    size_t repack_bytes = 0;
+    // per stream: split-K partials and other per-call scratch; grown outside capture only
+    float* workspace[kStreams] = {};
+    size_t workspace_bytes[kStreams] = {};
+    // per stream: per-tile arrival counters of the stream-K kernels; zero
+    // between kernels (each kernel returns the counters it used to zero)
+    int* counters[kStreams] = {};
+    size_t counters_n[kStreams] = {};
+    // per stream: tap-major copies of reference-layout conv weights (grown outside capture)
+    float* repack[kStreams] = {};
+    size_t repack_bytes[kStreams] = {};
     bool capturing = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -48,8 +57,8 @@ void fail(int code, const char* who, const char* fmt, ...);
 // Check a HIP runtime call; on failure record NNC_HIP_EDEVICE.
 bool hip_ok(hipError_t e, const char* who, const char* what);
 
-// Ensure the workspace holds at least `bytes`; returns nullptr if it cannot
-// (inside graph capture the workspace cannot grow).
+// Ensure the selected stream's workspace holds at least `bytes`; returns
+// nullptr if it cannot (inside graph capture the workspace cannot grow).
 float* workspace(size_t bytes);
 size_t workspace_capacity();
 

@@ -22,6 +22,13 @@ static char g_last_msg[512] = "";
 
 Context& ctx() { return g_ctx; }
 
+static bool sync_all(const char* who) {
+    for (int k = 0; k < kStreams; ++k)
+        if (g_ctx.streams[k] && !hip_ok(hipStreamSynchronize(g_ctx.streams[k]), who, "hipStreamSynchronize"))
+            return false;
+    return true;
+}
+
 void fail(int code, const char* who, const char* fmt, ...) {
     char body[384];
     va_list ap;
@@ -58,58 +65,63 @@ static void retire(void* p) {
 }
 
 float* workspace(size_t bytes) {
-    if (bytes <= g_ctx.workspace_bytes) return g_ctx.workspace;
-    if (g_ctx.capturing) return nullptr;
-    if (!hip_ok(hipStreamSynchronize(g_ctx.stream), "workspace", "hipStreamSynchronize"))
-        return nullptr;
-    retire(g_ctx.workspace);
-    g_ctx.workspace = nullptr;
-    g_ctx.workspace_bytes = 0;
+    Context& c = g_ctx;
+    const int k = c.cur;
+    if (bytes <= c.workspace_bytes[k]) return c.workspace[k];
+    if (c.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(c.stream), "workspace", "hipStreamSynchronize")) return nullptr;
+    retire(c.workspace[k]);
+    c.workspace[k] = nullptr;
+    c.workspace_bytes[k] = 0;
     size_t want = bytes < kDefaultWorkspace ? kDefaultWorkspace : bytes;
     void* p = nullptr;
     if (!hip_ok(hipMalloc(&p, want), "workspace", "hipMalloc")) return nullptr;
-    g_ctx.workspace = static_cast<float*>(p);
-    g_ctx.workspace_bytes = want;
-    return g_ctx.workspace;
+    c.workspace[k] = static_cast<float*>(p);
+    c.workspace_bytes[k] = want;
+    return c.workspace[k];
 }
 
-size_t workspace_capacity() { return g_ctx.workspace_bytes; }
+size_t workspace_capacity() { return g_ctx.workspace_bytes[g_ctx.cur]; }
 
 float* repack_buffer(size_t bytes) {
-    if (bytes <= g_ctx.repack_bytes) return g_ctx.repack;
-    if (g_ctx.capturing) return nullptr;
-    if (!hip_ok(hipStreamSynchronize(g_ctx.stream), "repack_buffer", "hipStreamSynchronize")) return nullptr;
-    retire(g_ctx.repack);
-    g_ctx.repack = nullptr;
-    g_ctx.repack_bytes = 0;
+    Context& c = g_ctx;
+    const int k = c.cur;
+    if (bytes <= c.repack_bytes[k]) return c.repack[k];
+    if (c.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(c.stream), "repack_buffer", "hipStreamSynchronize")) return nullptr;
+    retire(c.repack[k]);
+    c.repack[k] = nullptr;
+    c.repack_bytes[k] = 0;
     const size_t want = bytes < (16u << 20) ? (16u << 20) : bytes;
     void* p = nullptr;
     if (!hip_ok(hipMalloc(&p, want), "repack_buffer", "hipMalloc")) return nullptr;
-    g_ctx.repack = static_cast<float*>(p);
-    g_ctx.repack_bytes = want;
-    return g_ctx.repack;
+    c.repack[k] = static_cast<float*>(p);
+    c.repack_bytes[k] = want;
+    return c.repack[k];
 }
 
 static const size_t kDefaultCounters = 1u << 16;
 
 int* tile_counters(size_t n) {
-    if (n <= g_ctx.counters_n) return g_ctx.counters;
-    if (g_ctx.capturing) return nullptr;
-    if (!hip_ok(hipStreamSynchronize(g_ctx.stream), "tile_counters", "hipStreamSynchronize")) return nullptr;
-    retire(g_ctx.counters);
-    g_ctx.counters = nullptr;
-    g_ctx.counters_n = 0;
+    Context& c = g_ctx;
+    const int k = c.cur;
+    if (n <= c.counters_n[k]) return c.counters[k];
+    if (c.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(c.stream), "tile_counters", "hipStreamSynchronize")) return nullptr;
+    retire(c.counters[k]);
+    c.counters[k] = nullptr;
+    c.counters_n[k] = 0;
     const size_t want = n < kDefaultCounters ? kDefaultCounters : n;
     void* p = nullptr;
     if (!hip_ok(hipMalloc(&p, want * sizeof(int)), "tile_counters", "hipMalloc")) return nullptr;
-    if (!hip_ok(hipMemsetAsync(p, 0, want * sizeof(int), g_ctx.stream), "tile_counters", "hipMemsetAsync") ||
-        !hip_ok(hipStreamSynchronize(g_ctx.stream), "tile_counters", "hipStreamSynchronize")) {
+    if (!hip_ok(hipMemsetAsync(p, 0, want * sizeof(int), c.stream), "tile_counters", "hipMemsetAsync") ||
+        !hip_ok(hipStreamSynchronize(c.stream), "tile_counters", "hipStreamSynchronize")) {
         (void)hipFree(p);
         return nullptr;
     }
-    g_ctx.counters = static_cast<int*>(p);
-    g_ctx.counters_n = want;
-    return g_ctx.counters;
+    c.counters[k] = static_cast<int*>(p);
+    c.counters_n[k] = want;
+    return c.counters[k];
 }
 
 // ---------------------------------------------------------------------------
@@ -162,7 +174,7 @@ TimedScope::~TimedScope() {
 
 static void resolve_pending() {
     if (g_pending.empty()) return;
-    (void)hipStreamSynchronize(g_ctx.stream);
+    (void)sync_all("profile");
     for (auto& p : g_pending) {
         float ms = 0.f;
         (void)hipEventElapsedTime(&ms, p.start, p.stop);
@@ -204,19 +216,34 @@ int nnc_hip_init(int device) {
     hipDeviceProp_t prop;
     if (hip_ok(hipGetDeviceProperties(&prop, device), "nnc_hip_init", "hipGetDeviceProperties"))
         c.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-    if (!hip_ok(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking), "nnc_hip_init",
-                "hipStreamCreate"))
+    // default priority for every stream (streams of different priorities
+    // are not used anywhere in this library)
+    for (int k = 0; k < kStreams; ++k)
+        if (!hip_ok(hipStreamCreateWithFlags(&c.streams[k], hipStreamNonBlocking), "nnc_hip_init",
+                    "hipStreamCreate"))
+            return NNC_HIP_EDEVICE;
+    if (!hip_ok(hipEventCreateWithFlags(&c.fork_ev, hipEventDisableTiming), "nnc_hip_init", "hipEventCreate") ||
+        !hip_ok(hipEventCreateWithFlags(&c.join_ev, hipEventDisableTiming), "nnc_hip_init", "hipEventCreate"))
         return NNC_HIP_EDEVICE;
+    c.cur = 0;
+    c.stream = c.streams[0];
     c.device = device;
-    if (!workspace(kDefaultWorkspace)) return NNC_HIP_ENOMEM;
-    if (!tile_counters(kDefaultCounters)) return NNC_HIP_ENOMEM;
+    for (int k = 0; k < kStreams; ++k) {
+        c.cur = k;
+        c.stream = c.streams[k];
+        if (!workspace(kDefaultWorkspace)) return NNC_HIP_ENOMEM;
+        if (!tile_counters(kDefaultCounters)) return NNC_HIP_ENOMEM;
+    }
+    c.cur = 0;
+    c.stream = c.streams[0];
     return NNC_HIP_OK;
 }
 
 void nnc_hip_shutdown(void) {
     Context& c = g_ctx;
     if (!c.stream) return;
-    (void)hipStreamSynchronize(c.stream);
+    for (int k = 0; k < kStreams; ++k)
+        if (c.streams[k]) (void)hipStreamSynchronize(c.streams[k]);
     nnc_hip_graph_destroy();
     for (auto& p : g_pending) {
         (void)hipEventDestroy(p.start);
@@ -226,12 +253,17 @@ void nnc_hip_shutdown(void) {
     for (auto e : g_event_pool) (void)hipEventDestroy(e);
     g_event_pool.clear();
     if (c.arena) (void)hipFree(c.arena);
-    if (c.workspace) (void)hipFree(c.workspace);
-    if (c.counters) (void)hipFree(c.counters);
-    if (c.repack) (void)hipFree(c.repack);
+    for (int k = 0; k < kStreams; ++k) {
+        if (c.workspace[k]) (void)hipFree(c.workspace[k]);
+        if (c.counters[k]) (void)hipFree(c.counters[k]);
+        if (c.repack[k]) (void)hipFree(c.repack[k]);
+    }
     for (void* p : g_retired) (void)hipFree(p);
     g_retired.clear();
-    (void)hipStreamDestroy(c.stream);
+    if (c.fork_ev) (void)hipEventDestroy(c.fork_ev);
+    if (c.join_ev) (void)hipEventDestroy(c.join_ev);
+    for (int k = 0; k < kStreams; ++k)
+        if (c.streams[k]) (void)hipStreamDestroy(c.streams[k]);
     g_ctx = Context{};
 }
 
@@ -239,7 +271,7 @@ int nnc_hip_arena_reserve(size_t bytes) {
     if (!ready("nnc_hip_arena_reserve")) return NNC_HIP_ESTATE;
     Context& c = g_ctx;
     if (c.arena && bytes <= c.arena_bytes) return NNC_HIP_OK;
-    (void)hipStreamSynchronize(c.stream);
+    (void)sync_all("nnc_hip_arena_reserve");
     if (c.arena) (void)hipFree(c.arena);
     c.arena = nullptr;
     c.arena_bytes = 0;
@@ -281,16 +313,17 @@ void* nnc_hip_malloc(size_t bytes) {
 
 void nnc_hip_free(void* ptr) {
     if (!ptr || !g_ctx.stream) return;
-    (void)hipStreamSynchronize(g_ctx.stream);
+    (void)sync_all("nnc_hip_free");
     (void)hipFree(ptr);
 }
 
 int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
     if (!ready("nnc_hip_memcpy_h2d")) return NNC_HIP_ESTATE;
     if (!bytes) return NNC_HIP_OK;
-    if (!hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx.stream),
+    if (!sync_all("nnc_hip_memcpy_h2d") ||
+        !hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx.streams[0]),
                 "nnc_hip_memcpy_h2d", "hipMemcpyAsync") ||
-        !hip_ok(hipStreamSynchronize(g_ctx.stream), "nnc_hip_memcpy_h2d", "hipStreamSynchronize"))
+        !hip_ok(hipStreamSynchronize(g_ctx.streams[0]), "nnc_hip_memcpy_h2d", "hipStreamSynchronize"))
         return NNC_HIP_EDEVICE;
     return NNC_HIP_OK;
 }
@@ -298,9 +331,10 @@ int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
 int nnc_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
     if (!ready("nnc_hip_memcpy_d2h")) return NNC_HIP_ESTATE;
     if (!bytes) return NNC_HIP_OK;
-    if (!hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.stream),
+    if (!sync_all("nnc_hip_memcpy_d2h") ||
+        !hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.streams[0]),
                 "nnc_hip_memcpy_d2h", "hipMemcpyAsync") ||
-        !hip_ok(hipStreamSynchronize(g_ctx.stream), "nnc_hip_memcpy_d2h", "hipStreamSynchronize"))
+        !hip_ok(hipStreamSynchronize(g_ctx.streams[0]), "nnc_hip_memcpy_d2h", "hipStreamSynchronize"))
         return NNC_HIP_EDEVICE;
     return NNC_HIP_OK;
 }
@@ -323,12 +357,42 @@ int nnc_hip_download(const Tensor* t, void* host_dst) {
 
 int nnc_hip_sync(void) {
     if (!ready("nnc_hip_sync")) return NNC_HIP_ESTATE;
-    return hip_ok(hipStreamSynchronize(g_ctx.stream), "nnc_hip_sync", "hipStreamSynchronize")
-               ? NNC_HIP_OK
-               : NNC_HIP_EDEVICE;
+    for (int k = 0; k < kStreams; ++k)
+        if (!hip_ok(hipStreamSynchronize(g_ctx.streams[k]), "nnc_hip_sync", "hipStreamSynchronize"))
+            return NNC_HIP_EDEVICE;
+    return NNC_HIP_OK;
 }
 
-void* nnc_hip_stream(void) { return g_ctx.stream; }
+void* nnc_hip_stream(void) { return g_ctx.streams[0]; }
+
+int nnc_hip_stream_fork(void) {
+    if (!ready("nnc_hip_stream_fork")) return NNC_HIP_ESTATE;
+    Context& c = g_ctx;
+    if (!hip_ok(hipEventRecord(c.fork_ev, c.streams[0]), "nnc_hip_stream_fork", "hipEventRecord") ||
+        !hip_ok(hipStreamWaitEvent(c.streams[1], c.fork_ev, 0), "nnc_hip_stream_fork", "hipStreamWaitEvent"))
+        return NNC_HIP_EDEVICE;
+    return NNC_HIP_OK;
+}
+
+int nnc_hip_stream_select(int slot) {
+    if (!ready("nnc_hip_stream_select")) return NNC_HIP_ESTATE;
+    if (slot < 0 || slot >= kStreams) {
+        fail(NNC_HIP_EINVAL, "nnc_hip_stream_select", "stream %d out of range (0..%d)", slot, kStreams - 1);
+        return NNC_HIP_EINVAL;
+    }
+    g_ctx.cur = slot;
+    g_ctx.stream = g_ctx.streams[slot];
+    return NNC_HIP_OK;
+}
+
+int nnc_hip_stream_join(void) {
+    if (!ready("nnc_hip_stream_join")) return NNC_HIP_ESTATE;
+    Context& c = g_ctx;
+    if (!hip_ok(hipEventRecord(c.join_ev, c.streams[1]), "nnc_hip_stream_join", "hipEventRecord") ||
+        !hip_ok(hipStreamWaitEvent(c.streams[0], c.join_ev, 0), "nnc_hip_stream_join", "hipStreamWaitEvent"))
+        return NNC_HIP_EDEVICE;
+    return NNC_HIP_OK;
+}
 
 int nnc_hip_last_error(void) { return g_last_error.load(); }
 const char* nnc_hip_last_error_message(void) { return g_last_msg; }
@@ -422,7 +486,11 @@ int nnc_hip_graph_begin(void) {
     if (!ready("nnc_hip_graph_begin")) return NNC_HIP_ESTATE;
     nnc_hip_graph_destroy();
     resolve_pending();
-    if (!hip_ok(hipStreamBeginCapture(g_ctx.stream, hipStreamCaptureModeRelaxed),
+    if (g_ctx.cur != 0) {
+        fail(NNC_HIP_ESTATE, "nnc_hip_graph_begin", "capture starts on stream 0 (stream %d selected)", g_ctx.cur);
+        return NNC_HIP_ESTATE;
+    }
+    if (!hip_ok(hipStreamBeginCapture(g_ctx.streams[0], hipStreamCaptureModeRelaxed),
                 "nnc_hip_graph_begin", "hipStreamBeginCapture"))
         return NNC_HIP_EDEVICE;
     g_ctx.capturing = true;
@@ -437,7 +505,9 @@ int nnc_hip_graph_end(void) {
     }
     g_ctx.capturing = false;
     hipGraph_t g = nullptr;
-    if (!hip_ok(hipStreamEndCapture(g_ctx.stream, &g), "nnc_hip_graph_end", "hipStreamEndCapture"))
+    g_ctx.cur = 0;
+    g_ctx.stream = g_ctx.streams[0];
+    if (!hip_ok(hipStreamEndCapture(g_ctx.streams[0], &g), "nnc_hip_graph_end", "hipStreamEndCapture"))
         return NNC_HIP_EDEVICE;
     g_ctx.graph = g;
     if (!hip_ok(hipGraphInstantiate(&g_ctx.graph_exec, g, nullptr, nullptr, 0), "nnc_hip_graph_end",
@@ -453,7 +523,7 @@ int nnc_hip_graph_launch(void) {
         return NNC_HIP_ESTATE;
     }
     TimedScope scope("graph");
-    return hip_ok(hipGraphLaunch(g_ctx.graph_exec, g_ctx.stream), "nnc_hip_graph_launch",
+    return hip_ok(hipGraphLaunch(g_ctx.graph_exec, g_ctx.streams[0]), "nnc_hip_graph_launch",
                   "hipGraphLaunch")
                ? NNC_HIP_OK
                : NNC_HIP_EDEVICE;

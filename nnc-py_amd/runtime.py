@@ -52,6 +52,9 @@ _HIP_SIGNATURES = {
     "nnc_hip_profile_work": ([ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
                              ctypes.c_int),
     "nnc_hip_debug_dump": ([abi.TP, ctypes.c_char_p, ctypes.c_int, ctypes.c_void_p], ctypes.c_int),
+    "nnc_hip_stream_fork": ([], ctypes.c_int),
+    "nnc_hip_stream_select": ([ctypes.c_int], ctypes.c_int),
+    "nnc_hip_stream_join": ([], ctypes.c_int),
     "nnc_hip_graph_begin": ([], ctypes.c_int),
     "nnc_hip_graph_end": ([], ctypes.c_int),
     "nnc_hip_graph_launch": ([], ctypes.c_int),

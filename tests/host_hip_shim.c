@@ -51,6 +51,9 @@ int nnc_hip_profile_entry(int i, char* n, int c, int64_t* l, double* m) {
     return NNC_HIP_EINVAL;
 }
 int nnc_hip_profile_work(int i, double* f, double* b) { (void)i; (void)f; (void)b; return NNC_HIP_EINVAL; }
+int nnc_hip_stream_fork(void) { return 0; }
+int nnc_hip_stream_select(int slot) { (void)slot; return 0; }
+int nnc_hip_stream_join(void) { return 0; }
 int nnc_hip_graph_begin(void) { return NNC_HIP_EUNSUPP; }
 int nnc_hip_graph_end(void) { return NNC_HIP_EUNSUPP; }
 int nnc_hip_graph_launch(void) { return NNC_HIP_EUNSUPP; }

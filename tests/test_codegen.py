@@ -124,9 +124,32 @@ def test_generated_c_runs_on_the_oracle(tmp_path, pkg, oracle_lib, opt):
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)  # printed with %f
 
 
+def test_generated_c_with_stream_branches_runs_on_the_oracle(tmp_path, pkg, oracle_lib, monkeypatch):
+    """ResNet-18 with its downsample branches on the second stream: model.c
+    calls the fork/select/join entry points inline between the node
+    functions and computes what the executor computes."""
+    from nnc_py_amd.compiler import Executor, build_program, executor, zoo
+    monkeypatch.setattr(executor, "BRANCH_STREAMS", True)
+    prog = _compile(tmp_path, zoo.resnet18(batch=1, seed=1), opt=3)
+    assert len(prog.branches) == 3
+    src = (tmp_path / "model.c").read_text()
+    assert src.count("nnc_hip_stream_fork();") == 3 and src.count("nnc_hip_stream_join();") == 3
+    assert src.count("nnc_hip_stream_select(1);") == 3 and src.count("nnc_hip_stream_select(0);") == 3
+    exe = _build_with_shim(tmp_path)
+    run = subprocess.run([str(exe), str(tmp_path / "constants.bin"), "1"], capture_output=True, text=True,
+                         timeout=120)
+    assert run.returncode == 0, run.stderr
+    ex = Executor(build_program(zoo.resnet18(batch=1, seed=1), opt_level=3), device=False, lib=oracle_lib)
+    ex.set_input("input", (np.arange(3 * 224 * 224, dtype=np.float32) * np.float32(0.01)).reshape(1, 3, 224, 224))
+    ex.run()
+    np.testing.assert_allclose(_parse_outputs(run.stdout), ex.get("output").ravel()[:10], rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.gpu
-def test_generated_c_on_gpu_make_and_run(tmp_path, hip, oracle_lib):
-    from nnc_py_amd.compiler import Executor, build_program, zoo
+@pytest.mark.parametrize("branches", [False, True])
+def test_generated_c_on_gpu_make_and_run(tmp_path, hip, oracle_lib, monkeypatch, branches):
+    from nnc_py_amd.compiler import Executor, build_program, executor, zoo
+    monkeypatch.setattr(executor, "BRANCH_STREAMS", branches)
     _compile(tmp_path, zoo.resnet18(batch=1, seed=1), opt=3)
     subprocess.run(["make", "-C", str(tmp_path), "-j4"], check=True, capture_output=True, text=True)
     print("built generated ResNet-18 model", flush=True)

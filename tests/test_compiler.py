@@ -66,7 +66,7 @@ def test_o3_fusion_and_prepack_on_resnet18(pkg):
     weight as gemm_nt."""
     from nnc_py_amd.compiler import build_program, zoo
     prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
-    ops = [c.op for c in prog.calls]
+    ops = [c.op for c in prog.calls if c.node]  # without the stream fork/select/join calls
     assert len(ops) == 23  # Flatten is an alias of the pooled tensor: no call
     assert "nnc_flatten" not in ops and prog.plan.aliases
     assert ops.count("nnc_hip_conv_packed") == 17  # the stem and every 3x3 conv
@@ -120,13 +120,13 @@ def test_target_rewrites_can_be_switched_off(pkg):
     ex_mod.PACK_CONV_WEIGHTS = False
     try:
         prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
-        ops = [c.op for c in prog.calls]
+        ops = [c.op for c in prog.calls if c.node]  # without stream fork/select/join
         assert len(ops) == 23 and ops.count("nnc_hip_conv_add_relu") == 8
         assert ops.count("nnc_conv_relu3x3_s1") == 5  # conv1 of the five stride-1 blocks
         assert ops[0] == "nnc_conv_relu7x7_s2"
         ex_mod.RESIDUAL_FUSION = False
         prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
-        ops = [c.op for c in prog.calls]
+        ops = [c.op for c in prog.calls if c.node]
         assert len(ops) == 31 and ops.count("nnc_add_relu") == 8
     finally:
         ex_mod.PACK_CONV_WEIGHTS = True
@@ -186,3 +186,41 @@ def test_executor_on_oracle_matches_numpy_for_reduce_chain(pkg, oracle_lib):
     ex.run()
     out = ex.get(b.g.outputs[0])
     np.testing.assert_allclose(out.ravel(), v.astype(np.float64).mean((2, 3)).sum(1), rtol=1e-5, atol=1e-5)
+
+
+def test_o3_downsample_branches_on_the_second_stream(pkg):
+    """Small batches: each downsample block's two convolutions reading the
+    block input run on two streams (fork before the first, side call on
+    stream 1, join before the residual conv); none of the tensors they touch
+    is freed or reused before the join. Batch 32: every convolution fills
+    the GPU alone, no branches."""
+    from nnc_py_amd.compiler import build_program, zoo
+    from nnc_py_amd.compiler.passes import check_plan, liveness
+    assert not build_program(zoo.resnet18(batch=1, seed=0), opt_level=3).branches  # opt-in
+    prog = build_program(zoo.resnet18(batch=1, seed=0), opt_level=3, branch_streams=True)
+    assert len(prog.branches) == 3
+    seq = [c.op for c in prog.calls]
+    for i, op in enumerate(seq):
+        if op == "nnc_hip_stream_fork":
+            assert seq[i + 1:i + 4] == ["nnc_hip_stream_select", "nnc_hip_conv_packed", "nnc_hip_stream_select"]
+            assert [a[1] for a in prog.calls[i + 1].args] == [1] and [a[1] for a in prog.calls[i + 3].args] == [0]
+            assert seq[i + 4] == "nnc_conv1x1" and seq[i + 5] == "nnc_hip_stream_join"
+            assert prog.calls[i + 6].op == "nnc_hip_conv_packed" and prog.calls[i + 6].args[3][0] == "t"
+    assert seq.count("nnc_hip_stream_fork") == seq.count("nnc_hip_stream_join") == 3
+    # every tensor of a concurrent pair stays live (unshared) until the join
+    pos = {n.name: i for i, n in enumerate(prog.order)}
+    live = liveness(prog.graph, prog.order, [[b.side] + b.main for b in prog.branches])
+    for b in prog.branches:
+        nodes = [prog.order[pos[n]] for n in [b.side] + b.main]
+        end = max(pos[n.name] for n in nodes)
+        touched = {t for n in nodes for t in list(n.inputs) + list(n.outputs) if t in live}
+        assert all(live[t].end >= end for t in touched)
+        offs = {t: prog.plan.offsets[t] for t in touched if t not in prog.graph.constants}
+        sizes = {t: prog.graph.tensors[t].nbytes for t in offs}
+        names = sorted(offs)
+        for x in range(len(names)):
+            for y in range(x + 1, len(names)):
+                a, c = names[x], names[y]
+                assert offs[a] + sizes[a] <= offs[c] or offs[c] + sizes[c] <= offs[a], (a, c)
+    check_plan(prog.graph, prog.order, prog.plan, [[b.side] + b.main for b in prog.branches])
+    assert not build_program(zoo.resnet18(batch=32, seed=0), opt_level=3, branch_streams=True).branches
