@@ -56,9 +56,28 @@ size_t nnc_hip_arena_size(void);
  * the arena or offset is not 16-byte aligned. */
 int nnc_hip_bind(Tensor* t, size_t offset);
 
+/* ---- the spill pool (a fast-memory budget below the plan's peak) ------- */
+/* Replaces the reference's `_nnc_slow_pool` and the memcpy calls of its
+ * spill/reload code (codegen/x86_emitters/model_source.py:259-290,
+ * 1535-1659): the HBM arena is the fast pool, pinned host memory the slow
+ * one. nnc_hip_spill_reserve allocates it with one hipHostMalloc (again with
+ * a larger size: replaced, previous bindings dangle; refused during graph
+ * capture); nnc_hip_bind_spill sets t->data = pool + offset like
+ * nnc_hip_bind. */
+int nnc_hip_spill_reserve(size_t bytes);
+void* nnc_hip_spill_base(void);
+int nnc_hip_bind_spill(Tensor* t, size_t offset);
+/* Copy src's t->nbytes bytes to dst (same nbytes) asynchronously on the
+ * selected library stream: a spill (arena -> pool) or a reload (pool ->
+ * arena); under graph capture a memcpy node. Errors as for nnc_* calls. */
+void nnc_hip_transfer(Tensor* src, Tensor* dst);
+
 /* ---- explicit allocations (tests and callers without an arena) --------- */
 void* nnc_hip_malloc(size_t bytes);
 void nnc_hip_free(void* ptr);
+/* pinned host memory (hipHostMalloc): a spill pool of one's own */
+void* nnc_hip_host_malloc(size_t bytes);
+void nnc_hip_host_free(void* ptr);
 
 /* ---- host <-> device (synchronous with respect to the library stream) -- */
 int nnc_hip_upload(Tensor* t, const void* host_src);    /* t->nbytes bytes */

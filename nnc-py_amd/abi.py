@@ -118,6 +118,7 @@ NOT_IN_REFERENCE = {"nnc_matmul_relu"}
 TARGET_SIGNATURES = {
     "nnc_hip_conv_add_relu": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int],
     "nnc_hip_conv_packed": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
+    "nnc_hip_transfer": [TP, TP],
 }
 
 

@@ -22,9 +22,9 @@ import numpy as np
 from .. import abi
 from .ir import Graph, Node
 from .lower import Call, lower
-from .passes import (Branch, MemoryPlan, branch_calls, check_plan, eliminate_dead_code, eliminate_identity,
-                     find_branches, fuse_matmul_bias, fuse_patterns, fuse_residual, pack_conv_weights, plan_memory,
-                     prepack_lowering)
+from .passes import (SPILL_OPS, Branch, MemoryPlan, branch_calls, check_plan, eliminate_dead_code,
+                     eliminate_identity, find_branches, fit_memory, fuse_matmul_bias, fuse_patterns, fuse_residual,
+                     pack_conv_weights, plan_memory, prepack_lowering)
 
 
 @dataclass
@@ -80,8 +80,18 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
                 else [])
     groups = [[b.side] + b.main for b in branches]
     strategy = memory_strategy or ("basic" if opt_level == 0 else "cost_aware")
-    plan = plan_memory(graph, order, strategy, max_memory, alias_views=opt_level >= 3 and target_passes,
-                       concurrent=groups)
+
+    def plan_fn(o, budget=None):
+        return plan_memory(graph, o, strategy, None, alias_views=opt_level >= 3 and target_passes,
+                           concurrent=groups, budget=budget)
+
+    plan = plan_fn(order, max_memory)
+    if max_memory is not None and plan.activation_bytes > max_memory:
+        if strategy != "cost_aware":
+            raise ValueError(f"max_memory ({max_memory}) < peak activation footprint ({plan.activation_bytes}) "
+                             f"of the {strategy} plan; spilling needs the cost_aware strategy")
+        branches, groups = [], []  # spills go between the nodes of one stream
+        order, plan = fit_memory(graph, order, max_memory, plan_fn)
     check_plan(graph, order, plan, groups)
     calls = branch_calls(lower(graph, order, plan.aliases), branches, lambda op, args: Call(op, args, ""))
     return Program(graph, order, plan, calls, opt_level, branches)
@@ -107,10 +117,22 @@ class Executor:
             addr = self._host.ctypes.data
             self.base = addr + (-addr % 256)
         self._keep = []
+        self.slow = None  # spill pool: pinned host memory on a device, host memory otherwise
+        if plan.slow_bytes:
+            if device:
+                self.slow = self.lib.nnc_hip_host_malloc(plan.slow_bytes)
+                if not self.slow:
+                    raise runtime.HipError(f"cannot allocate a {plan.slow_bytes}-byte spill pool")
+            else:
+                self._slow_host = np.zeros(plan.slow_bytes + 256, np.uint8)
+                addr = self._slow_host.ctypes.data
+                self.slow = addr + (-addr % 256)
         self.tensors: dict[str, abi.Tensor] = {}
-        for name, off in plan.offsets.items():
+        places = [(n, self.base + off) for n, off in plan.offsets.items()]
+        places += [(n, self.slow + off) for n, off in plan.slow_offsets.items()]
+        for name, addr in places:
             t = g.tensors[name]
-            ten, sh = abi.make_tensor(self.base + off, abi.NUMPY_TO_NNC[t.dtype], t.shape, t.nbytes)
+            ten, sh = abi.make_tensor(addr, abi.NUMPY_TO_NNC[t.dtype], t.shape, t.nbytes)
             self._keep.append(sh)
             self.tensors[name] = ten
         for name, t in g.constants.items():
@@ -206,6 +228,8 @@ class Executor:
             for node in self.prog.order:
                 for fn, args in by_node.get(node.name, []):
                     fn(*args)
+                if node.op_type in SPILL_OPS:  # the compiler's copies, not graph nodes
+                    continue
                 for out in node.outputs:
                     if out in consts or out not in self.prog.plan.offsets:
                         continue
@@ -227,6 +251,9 @@ class Executor:
         if self.device and self.base:
             self.lib.nnc_hip_free(self.base)
             self.base = None
+        if self.device and self.slow:
+            self.lib.nnc_hip_host_free(self.slow)
+            self.slow = None
 
     def __del__(self):
         try:

@@ -37,6 +37,7 @@ class TensorInfo:
     shape: tuple
     dtype: str = "float32"
     data: np.ndarray | None = None  # constants only
+    pool: str = "fast"  # "slow": a spilled copy in the spill pool (pinned host memory)
 
     @property
     def numel(self) -> int:

@@ -140,6 +140,8 @@ def lower_node(g: Graph, node: Node) -> Call:
     ins, outs = node.inputs, node.outputs
     if op in ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu"):
         return _conv_call(g, node)
+    if op in ("Spill", "Reload"):  # arena <-> spill pool (include/nnc_hip.h)
+        return Call("nnc_hip_transfer", [_t(ins[0]), _t(outs[0])], node.name)
     if op in ("FusedMatMulBias", "FusedMatMulBiasRelu"):
         return _matmul_bias_call(g, node)
     if op == "Gemm":

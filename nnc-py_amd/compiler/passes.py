@@ -5,8 +5,9 @@ Same pass sequence and semantics as the reference's default pipelines
 
   O0   liveness -> memory plan
   O1   identity elimination -> dead-code elimination -> liveness -> plan
-  O2   as O1 (the reference's spill re-plan targets its x86 fast/slow pools;
-       on the GPU the whole plan lives in HBM, see MemoryPlan)
+  O2   as O1; at any level a max_memory below the plan's peak is met by
+       spilling tensors to pinned host memory and reloading them before
+       their next use (fit_memory)
   O3   O1 + pattern fusion (conv_relu, conv_sigmoid, add_relu, add_sigmoid,
        matmul_relu; pattern/fusion_patterns.py:105-153) + prepack lowering
        (conv kernel kind, constant Gemm B transposed to [N, K];
@@ -25,7 +26,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .ir import Graph, Node
+from .ir import Graph, Node, TensorInfo
 
 ALIGN = 256  # arena offsets; 16-byte vector loads need 16, 256 keeps rows cache-line aligned
 
@@ -287,7 +288,7 @@ def liveness(g: Graph, order: list[Node], concurrent: list[list[str]] | None = N
         live[name] = Liveness(0, 0, is_input=True)
     for idx, node in enumerate(order):
         for o in node.outputs:
-            if o and not g.tensors[o].is_constant:
+            if o and not g.tensors[o].is_constant and g.tensors[o].pool == "fast":
                 live.setdefault(o, Liveness(idx, idx))
         for i in node.inputs:
             if i in live:
@@ -320,6 +321,10 @@ class MemoryPlan:
     total_bytes: int = 0
     inplace: dict[str, str] = field(default_factory=dict)  # output -> reused input
     aliases: dict[str, str] = field(default_factory=dict)  # view output -> its input (no copy)
+    # spilled copies: offsets in the spill pool (pinned host memory)
+    slow_offsets: dict[str, int] = field(default_factory=dict)
+    slow_bytes: int = 0
+    first_over: int | None = None  # first node whose allocation passed the budget
 
 
 def _align(x: int) -> int:
@@ -332,7 +337,7 @@ VIEW_OPS = {"Flatten", "Reshape", "Squeeze", "Unsqueeze", "Identity"}
 
 def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
                 max_memory: int | None = None, alias_views: bool = False,
-                concurrent: list[list[str]] | None = None) -> MemoryPlan:
+                concurrent: list[list[str]] | None = None, budget: int | None = None) -> MemoryPlan:
     """Greedy offset assignment over the execution order.
 
     alias_views (mi355x O3): a view op whose input dies there gets the
@@ -341,16 +346,24 @@ def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
     basic:       every activation gets its own region (no reuse).
     cost_aware:  freed regions are reused best-fit; element-wise nodes write
                  over a same-sized input that dies there.
-    Raises ValueError when the activations exceed max_memory (the reference
-    raises the same way when the budget is below the peak node demand,
-    cost_aware_allocator.py:88-102)."""
+    Raises ValueError when the activations exceed max_memory (fit_memory
+    spills instead). With `budget`, plan.first_over is the first node at
+    which the arena grew past it. Spilled copies (pool "slow") get offsets
+    in the spill pool, one region each."""
     live = liveness(g, order, concurrent)
     sizes = {n: _align(g.tensors[n].nbytes) for n in live}
     plan = MemoryPlan()
     free: list[tuple[int, int]] = []  # (offset, size)
     top = 0
+    at = 0  # node being planned
 
     def take(size: int) -> int:
+        off = _take(size)
+        if budget is not None and plan.first_over is None and off + size > budget:
+            plan.first_over = at
+        return off
+
+    def _take(size: int) -> int:
         nonlocal top
         if strategy == "cost_aware":
             best = None
@@ -386,6 +399,7 @@ def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
     for name in g.inputs:
         plan.offsets[name] = take(sizes[name])
     for idx, node in enumerate(order):
+        at = idx
         reused = set()
         for o in node.outputs:
             if not o or o not in live or o in plan.offsets:
@@ -434,6 +448,13 @@ def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
         plan.offsets[name] = off
         off += _align(t.nbytes)
     plan.total_bytes = _align(off)
+    slow = 0
+    for node in order:
+        for o in node.outputs:
+            if o and g.tensors[o].pool == "slow" and o not in plan.slow_offsets:
+                plan.slow_offsets[o] = slow
+                slow += _align(g.tensors[o].nbytes)
+    plan.slow_bytes = slow
     return plan
 
 
@@ -443,6 +464,8 @@ def check_plan(g: Graph, order: list[Node], plan: MemoryPlan, concurrent: list[l
     tensor inside the arena."""
     live = liveness(g, order, concurrent)
     names = list(live)
+    for n, off in plan.slow_offsets.items():
+        assert off % ALIGN == 0 and off + g.tensors[n].nbytes <= plan.slow_bytes, n
     for n in plan.offsets:
         assert plan.offsets[n] % ALIGN == 0, n
         assert plan.offsets[n] + g.tensors[n].nbytes <= plan.total_bytes, n
@@ -456,6 +479,89 @@ def check_plan(g: Graph, order: list[Node], plan: MemoryPlan, concurrent: list[l
                 pair = plan.inplace.get(a) == b or plan.inplace.get(b) == a
                 if not pair:
                     raise AssertionError(f"{a} and {b} overlap in time and memory")
+
+
+# ---------------------------------------------------------------------------
+# a fast-memory budget: spill to pinned host memory, reload before next use
+# ---------------------------------------------------------------------------
+SPILL_OPS = ("Spill", "Reload")
+
+
+def _fresh(names, base: str) -> str:
+    k, name = 0, base
+    while name in names:
+        k += 1
+        name = f"{base}{k}"
+    return name
+
+
+def _spill_victim(g: Graph, order: list[Node], idx: int, need: int) -> str | None:
+    """The tensor to spill when the arena passes its budget at node `idx`:
+    live across the node (made before it, read after it) and not read by
+    it; graph inputs and outputs stay resident. Prefer one that alone frees
+    what is missing, then the one read again last (Belady's rule), then the
+    larger."""
+    live = liveness(g, order)
+    reads = set(order[idx].inputs)
+    best, best_key = None, None
+    for t, lv in live.items():
+        if lv.is_input or lv.is_output or t in reads or not (lv.start < idx < lv.end):
+            continue
+        nxt = next(k for k in range(idx + 1, len(order)) if t in order[k].inputs)
+        size = g.tensors[t].nbytes
+        key = (_align(size) >= need, nxt, size)
+        if best_key is None or key > best_key:
+            best, best_key = t, key
+    return best
+
+
+def _insert_spill(g: Graph, order: list[Node], t: str, idx: int) -> list[Node]:
+    """Spill `t` after its last read before node `idx` (or after its
+    producer), reload it into a new tensor before its next read after
+    `idx`; later nodes read the reloaded tensor."""
+    reads = [k for k, n in enumerate(order) if t in n.inputs]
+    made = next(k for k, n in enumerate(order) if t in n.outputs)
+    after = max([k for k in reads if k < idx] + [made])
+    nxt = min(k for k in reads if k > idx)
+    info = g.tensors[t]
+    held = _fresh(g.tensors, f"{t}.spilled")
+    g.add_tensor(TensorInfo(held, info.shape, info.dtype, pool="slow"))
+    back = _fresh(g.tensors, f"{t}.reloaded")
+    g.add_tensor(TensorInfo(back, info.shape, info.dtype))
+    names = {n.name for n in order}
+    spill = Node(_fresh(names, f"spill_{t}"), "Spill", [t], [held])
+    names.add(spill.name)
+    reload = Node(_fresh(names, f"reload_{t}"), "Reload", [held], [back])
+    for n in order[nxt:]:
+        n.inputs = [back if i == t else i for i in n.inputs]
+    new = order[:after + 1] + [spill] + order[after + 1:nxt] + [reload] + order[nxt:]
+    g.nodes = list(new)
+    return new
+
+
+def fit_memory(g: Graph, order: list[Node], max_memory: int, plan_fn) -> tuple[list[Node], MemoryPlan]:
+    """Meet a fast-memory budget (the HBM arena's activation region) by
+    spilling. `plan_fn(order, budget)` plans an order; while the plan passes
+    `max_memory`, the tensor chosen by _spill_victim at the first node
+    where the arena grew past the budget is spilled to the spill pool
+    (pinned host memory) and reloaded before its next read, and the order is
+    planned again. Same contract as the reference's cost_aware allocator
+    with a budget (cost_aware_allocator.py:63-102, 267-377; spill and
+    reload copies, model_source.py:259-290): the fast pool stays within
+    max_memory, and a budget that cannot hold what one node needs at once
+    raises ValueError. The eviction rule is this module's own."""
+    for _ in range(8 * len(order) + 64):
+        plan = plan_fn(order, max_memory)
+        if plan.activation_bytes <= max_memory:
+            return order, plan
+        idx = plan.first_over if plan.first_over is not None else len(order) - 1
+        victim = _spill_victim(g, order, idx, plan.activation_bytes - max_memory)
+        if victim is None:
+            node = order[idx].name if order else "(graph inputs)"
+            raise ValueError(f"max_memory ({max_memory}) < the fast memory node {node} needs with every "
+                             f"tensor it cannot spill resident (plan peak {plan.activation_bytes})")
+        order = _insert_spill(g, order, victim, idx)
+    raise ValueError(f"max_memory ({max_memory}): spilling did not converge")
 
 
 # ---------------------------------------------------------------------------

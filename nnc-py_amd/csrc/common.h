@@ -28,6 +28,9 @@ struct Context {
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     char* arena = nullptr;
     size_t arena_bytes = 0;
+    // pinned host memory: the slow pool that spilled tensors wait in
+    char* spill = nullptr;
+    size_t spill_bytes = 0;
     // per stream: split-K partials and other per-call scratch; grown outside capture only
     float* workspace[kStreams] = {};
     size_t workspace_bytes[kStreams] = {};

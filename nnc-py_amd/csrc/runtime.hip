@@ -253,6 +253,7 @@ void nnc_hip_shutdown(void) {
     for (auto e : g_event_pool) (void)hipEventDestroy(e);
     g_event_pool.clear();
     if (c.arena) (void)hipFree(c.arena);
+    if (c.spill) (void)hipHostFree(c.spill);
     for (int k = 0; k < kStreams; ++k) {
         if (c.workspace[k]) (void)hipFree(c.workspace[k]);
         if (c.counters[k]) (void)hipFree(c.counters[k]);
@@ -304,6 +305,65 @@ int nnc_hip_bind(Tensor* t, size_t offset) {
     return NNC_HIP_OK;
 }
 
+int nnc_hip_spill_reserve(size_t bytes) {
+    const char* who = "nnc_hip_spill_reserve";
+    if (!ready(who)) return NNC_HIP_ESTATE;
+    Context& c = g_ctx;
+    if (c.spill && bytes <= c.spill_bytes) return NNC_HIP_OK;
+    if (c.capturing) {
+        fail(NNC_HIP_ESTATE, who, "cannot allocate the spill pool during graph capture");
+        return NNC_HIP_ESTATE;
+    }
+    (void)sync_all(who);
+    if (c.spill) (void)hipHostFree(c.spill);
+    c.spill = nullptr;
+    c.spill_bytes = 0;
+    void* p = nullptr;
+    if (!hip_ok(hipHostMalloc(&p, bytes ? bytes : 256, hipHostMallocDefault), who, "hipHostMalloc"))
+        return NNC_HIP_ENOMEM;
+    c.spill = static_cast<char*>(p);
+    c.spill_bytes = bytes;
+    return NNC_HIP_OK;
+}
+
+void* nnc_hip_spill_base(void) { return g_ctx.spill; }
+
+int nnc_hip_bind_spill(Tensor* t, size_t offset) {
+    const char* who = "nnc_hip_bind_spill";
+    if (!t) {
+        fail(NNC_HIP_EINVAL, who, "NULL tensor");
+        return NNC_HIP_EINVAL;
+    }
+    if (!g_ctx.spill) {
+        fail(NNC_HIP_ESTATE, who, "no spill pool reserved");
+        return NNC_HIP_ESTATE;
+    }
+    if ((offset & 15u) != 0 || offset + (size_t)t->nbytes > g_ctx.spill_bytes) {
+        fail(NNC_HIP_EINVAL, who, "offset %zu + %lld bytes outside the spill pool of %zu (or misaligned)", offset,
+             (long long)t->nbytes, g_ctx.spill_bytes);
+        return NNC_HIP_EINVAL;
+    }
+    t->data = g_ctx.spill + offset;
+    return NNC_HIP_OK;
+}
+
+// Spill (HBM -> pinned host) or reload (pinned host -> HBM): one async copy
+// on the selected stream, so it orders with the kernels around it and is
+// recorded as a memcpy node under graph capture.
+void nnc_hip_transfer(Tensor* src, Tensor* dst) {
+    const char* who = "nnc_hip_transfer";
+    if (!ready(who)) return;
+    if (!src || !dst || !src->data || !dst->data) return fail(NNC_HIP_EINVAL, who, "NULL tensor or data pointer");
+    if (src->nbytes != dst->nbytes)
+        return fail(NNC_HIP_EINVAL, who, "source has %lld bytes, destination %lld", (long long)src->nbytes,
+                    (long long)dst->nbytes);
+    if (src->nbytes <= 0 || src->data == dst->data) return;
+    set_work(0.0, (double)src->nbytes);
+    TimedScope scope(who);
+    hip_ok(hipMemcpyAsync(dst->data, src->data, (size_t)src->nbytes, hipMemcpyDefault, g_ctx.stream), who,
+           "hipMemcpyAsync");
+}
+
 void* nnc_hip_malloc(size_t bytes) {
     if (!ready("nnc_hip_malloc")) return nullptr;
     void* p = nullptr;
@@ -315,6 +375,21 @@ void nnc_hip_free(void* ptr) {
     if (!ptr || !g_ctx.stream) return;
     (void)sync_all("nnc_hip_free");
     (void)hipFree(ptr);
+}
+
+void* nnc_hip_host_malloc(size_t bytes) {
+    if (!ready("nnc_hip_host_malloc")) return nullptr;
+    void* p = nullptr;
+    if (!hip_ok(hipHostMalloc(&p, bytes ? bytes : 16, hipHostMallocDefault), "nnc_hip_host_malloc",
+                "hipHostMalloc"))
+        return nullptr;
+    return p;
+}
+
+void nnc_hip_host_free(void* ptr) {
+    if (!ptr || !g_ctx.stream) return;
+    (void)sync_all("nnc_hip_host_free");
+    (void)hipHostFree(ptr);
 }
 
 int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {

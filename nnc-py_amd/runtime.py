@@ -32,8 +32,13 @@ _HIP_SIGNATURES = {
     "nnc_hip_arena_base": ([], ctypes.c_void_p),
     "nnc_hip_arena_size": ([], ctypes.c_size_t),
     "nnc_hip_bind": ([abi.TP, ctypes.c_size_t], ctypes.c_int),
+    "nnc_hip_spill_reserve": ([ctypes.c_size_t], ctypes.c_int),
+    "nnc_hip_spill_base": ([], ctypes.c_void_p),
+    "nnc_hip_bind_spill": ([abi.TP, ctypes.c_size_t], ctypes.c_int),
     "nnc_hip_malloc": ([ctypes.c_size_t], ctypes.c_void_p),
     "nnc_hip_free": ([ctypes.c_void_p], None),
+    "nnc_hip_host_malloc": ([ctypes.c_size_t], ctypes.c_void_p),
+    "nnc_hip_host_free": ([ctypes.c_void_p], None),
     "nnc_hip_upload": ([abi.TP, ctypes.c_void_p], ctypes.c_int),
     "nnc_hip_download": ([abi.TP, ctypes.c_void_p], ctypes.c_int),
     "nnc_hip_memcpy_h2d": ([ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int),
@@ -61,6 +66,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_graph_destroy": ([], None),
     "nnc_hip_conv_add_relu": (abi.TARGET_SIGNATURES["nnc_hip_conv_add_relu"], None),
     "nnc_hip_conv_packed": (abi.TARGET_SIGNATURES["nnc_hip_conv_packed"], None),
+    "nnc_hip_transfer": (abi.TARGET_SIGNATURES["nnc_hip_transfer"], None),
 }
 
 

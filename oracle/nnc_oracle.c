@@ -951,6 +951,18 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
 }
 
 /* ------------------------------------------------------------------------
+ * Spill / reload of the mi355x target (include/nnc_hip.h): a byte copy of
+ * src into dst, as the reference's spill and reload code copies between its
+ * fast and slow pools (codegen/x86_emitters/model_source.py:276-287). Pinned
+ * by the spill tests: a program under a memory budget computes the same
+ * bytes as without one.
+ * ---------------------------------------------------------------------- */
+void nnc_hip_transfer(Tensor* src, Tensor* dst) {
+    if (!src || !dst || !src->data || !dst->data || src->nbytes != dst->nbytes) return;
+    memmove(dst->data, src->data, (size_t)src->nbytes);
+}
+
+/* ------------------------------------------------------------------------
  * Packed-weight convolution of the mi355x target (include/nnc_hip.h), no
  * reference counterpart: the weights, [Co][kh][kw][Ci] or [Co][Kp] (rows of
  * K = kh*kw*Ci tap-major values padded to Kp), are unpacked to the

@@ -32,7 +32,24 @@ int nnc_hip_bind(Tensor* t, size_t offset) {
     t->data = arena + offset;
     return 0;
 }
+static char* spill = NULL;
+static size_t spill_size = 0;
+int nnc_hip_spill_reserve(size_t bytes) {
+    if (spill && bytes <= spill_size) return 0;
+    free(spill);
+    spill = aligned_alloc(256, (bytes + 255) / 256 * 256 + 256);
+    spill_size = spill ? bytes : 0;
+    return spill ? 0 : NNC_HIP_ENOMEM;
+}
+void* nnc_hip_spill_base(void) { return spill; }
+int nnc_hip_bind_spill(Tensor* t, size_t offset) {
+    if (!spill || offset + (size_t)t->nbytes > spill_size) return NNC_HIP_EINVAL;
+    t->data = spill + offset;
+    return 0;
+}
 void* nnc_hip_malloc(size_t bytes) { return malloc(bytes); }
+void* nnc_hip_host_malloc(size_t bytes) { return malloc(bytes); }
+void nnc_hip_host_free(void* p) { free(p); }
 void nnc_hip_free(void* p) { free(p); }
 int nnc_hip_upload(Tensor* t, const void* src) { memcpy(t->data, src, (size_t)t->nbytes); return 0; }
 int nnc_hip_download(const Tensor* t, void* dst) { memcpy(dst, t->data, (size_t)t->nbytes); return 0; }
