@@ -75,7 +75,26 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} ({LIB.stat().st_size / 1e6:.1f} MB, {len(objs)} objects)")
+    build_costmodel(verbose)
     return LIB
+
+
+COSTMODEL = LIBDIR / "libnnc_costmodel.so"
+
+
+def build_costmodel(verbose: bool = True) -> Path:
+    """lib/libnnc_costmodel.so: the cost-model runtime (host C++, no HIP)."""
+    LIBDIR.mkdir(exist_ok=True)
+    tmp = COSTMODEL.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
+           f"-I{ROOT / 'include'}", f"-I{CSRC}", str(CSRC / "costmodel.cpp"), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"cost model build failed:\n{res.stderr}")
+    os.replace(tmp, COSTMODEL)
+    if verbose:
+        print(f"built {COSTMODEL}")
+    return COSTMODEL
 
 
 if __name__ == "__main__":

@@ -44,6 +44,7 @@
 #pragma once
 
 #include "common.h"
+#include "plan.h"
 
 namespace nnc {
 
@@ -386,30 +387,6 @@ __device__ __forceinline__ int xcd_remap(int lin, int total) {
     return (lin % 8) * per + lin / 8;
 }
 
-// ---------------------------------------------------------------------------
-// stream-K bookkeeping. The stream-K region holds S = sk_tiles * iters slice
-// iterations; workgroup g owns [lo(g), hi(g)) with lo(g) = g*S/G.
-// ---------------------------------------------------------------------------
-struct StreamK {
-    int tiles, iters, G, sk_tiles;
-    __host__ __device__ int64_t total() const { return (int64_t)sk_tiles * iters; }
-    __host__ __device__ int64_t lo(int g) const { return total() * g / G; }
-    __host__ __device__ int64_t hi(int g) const { return total() * (g + 1) / G; }
-    // first workgroup whose range reaches into stream-K tile t
-    __host__ __device__ int first_owner(int t) const {
-        const int64_t start = (int64_t)t * iters;
-        int g = (int)(start * G / total());
-        while (g > 0 && hi(g - 1) > start) --g;
-        while (hi(g) <= start) ++g;
-        return g;
-    }
-    // true if some stream-K tile is shared (a range boundary inside a tile)
-    __host__ bool needs_fixup() const {
-        if (sk_tiles == 0 || iters == 1) return false;
-        return !(total() % G == 0 && (total() / G) % iters == 0);
-    }
-};
-
 // One unit of a workgroup's work: slices [kb, ke) of `tile`. `slot` is the
 // partial slot (0: first segment of the range, 1: last) or -1 for a whole
 // tile written straight to the output.
@@ -463,58 +440,12 @@ __host__ __device__ inline bool tile_partials(const StreamK& sk, int t, int& g0,
     return true;
 }
 
-// Host: choose the grid and the stream-K region for `tiles` tiles of
-// `iters` slices on `slots` resident workgroups. `fixup_slices` is what
-// finishing the shared tiles costs, in slice times of this tile shape (the
-// fixup kernel's launch and partial traffic).
-//  - few slices per tile (< 4): splitting costs more than the tail; plain
-//    round-robin over min(tiles, slots) workgroups
-//  - otherwise round-robin (every tile whole) unless stream-K's estimated
-//    time, ceil(tiles * iters / G) + fixup_slices, is shorter than
-//    round-robin's ceil(tiles / slots) * iters
-//  - stream-K with tiles >= slots: all but the last full round plus the
-//    partial round are split, so every workgroup ends at the same time
-//  - stream-K with tiles < slots: everything is split, each workgroup
-//    taking at least 4 slices (fewer workgroups for short problems)
-inline StreamK plan_streamk(int tiles, int iters, int slots, int fixup_slices) {
-    StreamK sk{};
-    sk.tiles = tiles;
-    sk.iters = iters;
-    const int kMinSplitIters = 4, kMinRangeIters = 4;
-    const int64_t total = (int64_t)tiles * iters;
-    const int64_t dp_time = (int64_t)((tiles + slots - 1) / slots) * iters;
-    if (iters < kMinSplitIters) {
-        sk.G = tiles < slots ? tiles : slots;
-        sk.sk_tiles = 0;
-        return sk;
-    }
-    if (tiles >= slots) {
-        const int rem = tiles % slots;
-        sk.G = slots;
-        const int64_t sk_time = (total + slots - 1) / slots + fixup_slices;
-        sk.sk_tiles = (rem == 0 || sk_time >= dp_time) ? 0 : tiles - (tiles / slots - 1) * slots;
-        return sk;
-    }
-    int64_t G = total / kMinRangeIters;
-    if (G > slots) G = slots;
-    if (G < tiles) G = tiles;
-    const int64_t sk_time = (total + G - 1) / G + fixup_slices;
-    if (sk_time >= dp_time) {
-        sk.G = tiles;
-        sk.sk_tiles = 0;
-        return sk;
-    }
-    sk.G = (int)G;
-    sk.sk_tiles = tiles;
-    return sk;
-}
-
 // Fixup cost in slice times, measured on ResNet-18 and transformer layers:
 // about one slice for 128x128 tiles, scaled by tile area for smaller tiles
 // (shorter slices). Round-robin wins only when stream-K saves less.
 template <class T>
 constexpr int fixup_slices() {
-    return (128 * 128) / (T::BM * T::BN);
+    return fixup_slices_for(T::BM, T::BN);
 }
 
 // Persistent-grid size: workgroups of `kernel` resident on the device at once.
