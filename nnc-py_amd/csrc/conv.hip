@@ -585,8 +585,10 @@ struct DmaPacked {
 template <class T, int KH, int KW, int CI>
 struct DmaSmallC {
     typedef DmaStage<T> D;
-    // (the in-kernel finish's registers would cost this kernel occupancy)
-    static constexpr bool kFinishInKernel = false;
+    // shared tiles finished in the kernel: the stem at batch 32 grows from
+    // 100 to 111 us but its 15 us fixup launch goes (batch 32 even, batch 8
+    // +1%)
+    static constexpr bool kFinishInKernel = true;
     static constexpr int A_LOADS = T::BM / (8 * T::NW);
     static constexpr int KMAX = 256;  // table entries (Kp <= KMAX, checked on the host)
     static_assert(KH * KW < 64, "tap 63 marks k >= K");
@@ -889,8 +891,8 @@ static void launch_conv_t(ConvArgs& a, const char* entry) {
 template <class T, class L>
 static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) {
     // the in-kernel finish only where it measured faster than the fixup
-    // kernel (64x128 tiles: ResNet's 64-channel layers); elsewhere its code
-    // costs the main loop registers
+    // kernel (64x128 tiles: ResNet's 64-channel layers and the stem);
+    // elsewhere its code costs the main loop registers
     constexpr bool FIN = kInKernelFixup && L::kFinishInKernel && T::NW == 4 &&
                          ((T::BM == 64 && T::BN == 128) || (NNC_CONV_FIN128 && T::BM == 128 && T::BN == 128));
     auto kernel = conv_dma_k<T, L, FIN>;

@@ -66,7 +66,7 @@ struct MfmaKind {
 const MfmaKind kConv128 = {"conv_dma_128", 128, 128, 2, 0.75, 0.47};
 const MfmaKind kConv64x128 = {"conv_dma_64x128", 64, 128, 3, 0.65, 4.0};
 const MfmaKind kConv64 = {"conv_dma_64", 64, 64, 4, 0.60, 1.0};
-const MfmaKind kStem64x128 = {"stem_64x128", 64, 128, 3, 0.56, 1.26};
+const MfmaKind kStem64x128 = {"stem_64x128", 64, 128, 3, 0.50, 1.26};  // with the in-kernel finish
 const MfmaKind kStem64 = {"stem_64", 64, 64, 4, 0.30, 1.43};
 const MfmaKind kGather128 = {"conv_gather_128", 128, 128, 2, 0.60, 0.6};
 const MfmaKind kGather64x128 = {"conv_gather_64x128", 64, 128, 3, 0.52, 4.0};
@@ -234,7 +234,7 @@ void conv(const char* op, Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor*
     if (!m.sk.needs_fixup()) return;
     // the 64x128 direct-to-LDS kernels finish a shared tile in the kernel
     // when at most kMaxInKernelParts workgroups share it
-    const bool fin = dma && !stem && k == &kConv64x128;
+    const bool fin = (dma && !stem && k == &kConv64x128) || k == &kStem64x128;
     const int64_t per = m.sk.total() / m.sk.G;
     // (its cost is inside the kernel's fitted efficiency)
     if (fin && (m.sk.iters + per - 1) / per + 1 <= kMaxInKernelParts) return;
