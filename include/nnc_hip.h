@@ -177,6 +177,18 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
 void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,
                          int sw, int ph, int pw, int act);
 
+/* nnc_hip_conv_proj: a residual block's last convolution with its 1x1
+ * projection shortcut folded into the same contraction:
+ *   out = act(conv(in, W3) + conv1x1(x, Wp, stride psh x psw) + b)
+ * with w packed [Co][kh*kw*Ci + Cx]: each row is W3 tap-major
+ * ([kh][kw][Ci]) followed by the Cx projection weights, and b the sum of the
+ * two biases. Equal to nnc_conv + nnc_conv1x1 + nnc_add_relu (act 1) up to
+ * fp32 accumulation order. Needs a 3x3 kernel, Ci and Cx multiples of 32,
+ * every (oh * psh, ow * psw) inside x, 16-byte aligned weights
+ * (NNC_HIP_EUNSUPP / NNC_HIP_EINVAL otherwise). */
+void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
+                       int ph, int pw, int psh, int psw, int act);
+
 #ifdef __cplusplus
 }
 #endif

@@ -119,6 +119,7 @@ TARGET_SIGNATURES = {
     "nnc_hip_conv_add_relu": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int],
     "nnc_hip_conv_packed": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
     "nnc_hip_transfer": [TP, TP],
+    "nnc_hip_conv_proj": [TP, TP, TP, TP, TP] + [c_int] * 9,
 }
 
 

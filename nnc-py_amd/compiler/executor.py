@@ -23,8 +23,8 @@ from .. import abi
 from .ir import Graph, Node
 from .lower import Call, lower
 from .passes import (SPILL_OPS, Branch, MemoryPlan, branch_calls, check_plan, eliminate_dead_code,
-                     eliminate_identity, find_branches, fit_memory, fuse_matmul_bias, fuse_patterns, fuse_residual,
-                     pack_conv_weights, plan_memory, prepack_lowering)
+                     eliminate_identity, find_branches, fit_memory, fuse_matmul_bias, fuse_patterns, fuse_projection,
+                     fuse_residual, pack_conv_weights, plan_memory, prepack_lowering)
 
 
 @dataclass
@@ -41,6 +41,9 @@ class Program:
 RESIDUAL_FUSION = True
 # tap-major 3x3 conv weights and nnc_hip_conv_packed at O3 (mi355x target).
 PACK_CONV_WEIGHTS = True
+# a residual block's 1x1 projection folded into its last 3x3 conv
+# (nnc_hip_conv_proj) at O3 (mi355x target).
+PROJECTION_FUSION = True
 # independent side branches (ResNet's downsample convolutions) on the second
 # library stream at O3 (mi355x target), while the main branch's convolutions
 # total at most BRANCH_MAX_FLOPS: two kernels overlap only while neither fills
@@ -65,6 +68,7 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
     if opt_level >= 1:
         eliminate_identity(graph)
         eliminate_dead_code(graph)
+    use_branches = opt_level >= 3 and target_passes and (BRANCH_STREAMS if branch_streams is None else branch_streams)
     if opt_level >= 3:
         fuse_patterns(graph)
         if target_passes:
@@ -73,11 +77,12 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
             fuse_matmul_bias(graph)
             if PACK_CONV_WEIGHTS:
                 pack_conv_weights(graph)
+                # the downsample conv either joins the residual conv or runs beside it on stream 1
+                if PROJECTION_FUSION and RESIDUAL_FUSION and not use_branches:
+                    fuse_projection(graph)
         prepack_lowering(graph)
     order = graph.topological_sort()
-    branches = (find_branches(graph, order, BRANCH_MAX_FLOPS)
-                if opt_level >= 3 and target_passes and (BRANCH_STREAMS if branch_streams is None else branch_streams)
-                else [])
+    branches = find_branches(graph, order, BRANCH_MAX_FLOPS) if use_branches else []
     groups = [[b.side] + b.main for b in branches]
     strategy = memory_strategy or ("basic" if opt_level == 0 else "cost_aware")
 

@@ -140,6 +140,13 @@ def lower_node(g: Graph, node: Node) -> Call:
     ins, outs = node.inputs, node.outputs
     if op in ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu"):
         return _conv_call(g, node)
+    if op == "FusedConvProjRelu":  # 3x3 conv + folded 1x1 projection (include/nnc_hip.h)
+        kh, kw = node.attrs.get("kernel_shape", [3, 3])
+        sh, sw = (list(node.attrs.get("strides", [1, 1])) + [1])[:2]
+        ph, pw = (list(node.attrs.get("pads", [0, 0, 0, 0])) + [0, 0])[:2]
+        psh, psw = (list(node.attrs.get("proj_strides", [1, 1])) + [1])[:2]
+        return Call("nnc_hip_conv_proj", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(ins[3]), _t(outs[0])]
+                    + [("i", int(v)) for v in (kh, kw, sh, sw, ph, pw, psh, psw, 1)], node.name)
     if op in ("Spill", "Reload"):  # arena <-> spill pool (include/nnc_hip.h)
         return Call("nnc_hip_transfer", [_t(ins[0]), _t(outs[0])], node.name)
     if op in ("FusedMatMulBias", "FusedMatMulBiasRelu"):

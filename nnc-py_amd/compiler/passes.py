@@ -189,6 +189,67 @@ def pack_conv_weights(g: Graph) -> int:
     return packed
 
 
+def fuse_projection(g: Graph) -> int:
+    """mi355x target, O3, after pack_conv_weights: a residual block whose
+    shortcut is a 1x1 convolution P (constant weights, no padding, output
+    read only by the block's last convolution F, a packed 3x3
+    FusedConvAddRelu) becomes one FusedConvProjRelu node lowered to
+    nnc_hip_conv_proj: P's weights are appended to each packed row of F's
+    ([Co][9*Ci + Cx]), the two biases summed, and P's input read by F's
+    contraction, so the projection needs no launch and no tensor. Inputs:
+    x, w, bias or "", projection input; attrs: F's, plus proj_strides."""
+    fused = 0
+    for f in list(g.nodes):
+        if f.op_type != "FusedConvAddRelu" or len(f.inputs) != 4:
+            continue
+        if f.metadata.get("lowering", {}).get("weight_pack") != "tap_major":
+            continue
+        h, wname, bname, res = f.inputs
+        wf = g.tensors[wname]
+        if wf.data is None or wf.data.ndim != 4 or wf.data.shape[1:3] != (3, 3):
+            continue
+        p = g.producer(res)
+        if p is None or p.op_type != "Conv" or res in g.outputs or len(g.consumers(res)) != 1:
+            continue
+        if len(p.inputs) < 2 or not g.tensors[p.inputs[1]].is_constant or len(g.consumers(p.inputs[1])) != 1:
+            continue
+        wp = g.tensors[p.inputs[1]].data
+        x = g.tensors[p.inputs[0]]
+        if wp is None or wp.ndim != 4 or wp.shape[2:] != (1, 1) or len(x.shape) != 4:
+            continue
+        if list(p.attrs.get("pads", [0, 0, 0, 0])) != [0, 0, 0, 0] or int(p.attrs.get("group", 1)) != 1:
+            continue
+        if list(p.attrs.get("dilations", [1, 1])) != [1, 1] or g.tensors[res].shape != g.tensors[f.outputs[0]].shape:
+            continue
+        co, ci, cx = wf.data.shape[0], wf.data.shape[3], wp.shape[1]
+        if wp.shape[0] != co or ci % 32 or cx % 32:
+            continue
+        biases = [n for n in (bname, p.inputs[2] if len(p.inputs) > 2 else "") if n]
+        if any(not g.tensors[n].is_constant or len(g.consumers(n)) != 1 for n in biases):
+            continue
+        rows = np.concatenate([wf.data.reshape(co, 9 * ci), wp.reshape(co, cx)], axis=1)
+        w_new = _fresh(g.tensors, f"{wname}.proj")
+        g.add_tensor(TensorInfo(w_new, tuple(rows.shape), wf.dtype, np.ascontiguousarray(rows)))
+        b_new = ""
+        if biases:
+            total = np.zeros(co, np.float32)
+            for n in biases:
+                total = total + g.tensors[n].data.reshape(co).astype(np.float32)
+            b_new = _fresh(g.tensors, f"{bname or biases[0]}.proj")
+            g.add_tensor(TensorInfo(b_new, (co,), "float32", total.astype(np.float32)))
+        f.metadata["weights_from"] = [wname, p.inputs[1]]
+        for n in [wname, p.inputs[1]] + biases:
+            g.tensors.pop(n, None)
+        f.inputs = [h, w_new, b_new, p.inputs[0]]
+        f.op_type = "FusedConvProjRelu"
+        f.attrs["proj_strides"] = list(p.attrs.get("strides", [1, 1]))
+        f.metadata["fused_from"] = f.metadata.get("fused_from", [f.name]) + [p.name]
+        g.nodes.remove(p)
+        g.tensors.pop(res, None)
+        fused += 1
+    return fused
+
+
 def fuse_matmul_bias(g: Graph) -> int:
     """mi355x target, O3: MatMul(activation, constant W [K, N]) whose only
     consumer adds a constant 1-D bias [N] becomes one GEMM with the bias in

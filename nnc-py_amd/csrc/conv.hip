@@ -47,6 +47,11 @@ struct ConvArgs {
     int tiles_m, tiles_n;
     int vec_out;  // out (and res) 16-byte aligned: the fixup may store float4
     int out32;    // output (and residual) below 2 GiB: whole tiles use 32-bit buffer offsets
+    // 1x1 projection folded into the contraction (nnc_hip_conv_proj): input
+    // [N][pci][pH][pW] read at (oh * psh, ow * psw); its weights are the last
+    // pci of each packed weight row
+    const float* pin;
+    int pci, pH, pW, psh, psw;
 };
 
 // B operand: gathers input taps for X consecutive output pixels; each thread
@@ -574,6 +579,98 @@ struct DmaPacked {
         constexpr int H = D::B_LOADS / 2;
 #pragma unroll
         for (int i = part * H; i < (part + 1) * H; ++i) dma_load4(rin, d0 + i * T::BN, bv, s0 + (uint32_t)(i * HW) * 4u);
+    }
+};
+
+// A KH x KW convolution of `in` and a 1x1 projection of a second input (a
+// residual block's strided downsample) as one contraction, so the
+// projection needs no launch and no tensor of its own: k < KH*KW*Ci walks
+// `in` as DmaPacked does, the last pci k walk `pin` at the output pixel's
+// position times the projection stride (always inside that image). Weights
+// [Co][KH*KW*Ci + pci]: slice s starts at k = 32 s in both parts. Needs Ci
+// and pci multiples of 32.
+template <class T, int KH, int KW>
+struct DmaProj {
+    typedef DmaStage<T> D;
+    static constexpr bool kFinishInKernel = true;
+    static constexpr int EXTRA_LDS_FLOATS = 0;
+    __device__ void prepare(float*, const ConvArgs&) {}
+    static constexpr int A_LOADS = T::BM / (8 * T::NW);
+    static constexpr int TAPS = KH * KW;  // cursor tap TAPS: the projection
+    static_assert(T::BM % (8 * T::NW) == 0, "A rows split evenly over the waves");
+    __amdgpu_buffer_rsrc_t rin, rx, rw;
+    int wave, b_grp, b_kr0, CB, CBX, HW, HWX, W, Ci;
+    uint32_t avo[A_LOADS];
+    PixelTaps<KH, KW> px;
+    uint32_t xvo;  // this lane's pixel in the projection input at channel 0 (bytes; out of range past Npix)
+    int t, cb;     // slice cursor: tap (TAPS: projection), 32-channel block
+    uint32_t bv;
+
+    __device__ void init(const ConvArgs& a, int wave_, int lane) {
+        rin = make_rsrc(a.in);
+        rx = make_rsrc(a.pin);
+        rw = make_rsrc(a.w);
+        wave = wave_;
+        b_grp = wave % D::PX_GROUPS;
+        b_kr0 = (wave / D::PX_GROUPS) * D::B_LOADS;
+        CB = a.Ci >> 5;
+        CBX = a.pci >> 5;
+        HW = a.H * a.W;
+        HWX = a.pH * a.pW;
+        W = a.W;
+        Ci = a.Ci;
+    }
+    __device__ void tile(const ConvArgs& a, int i0, int j0, int lane) {
+        const int a_kc = (lane & 7) ^ ((lane >> 3) & 7);
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) {
+            const int co = i0 + (wave + T::NW * i) * 8 + (lane >> 3);
+            avo[i] = keep_or_oob((uint32_t)(co * a.ldw) * 4u + (uint32_t)a_kc * 16u, co < a.Co);
+        }
+        const int p = j0 + b_grp * 64 + lane;
+        px.init(a, p);
+        const bool valid = p < a.Npix;
+        const int q = valid ? p : 0;
+        const int hw = a.Ho * a.Wo;
+        const int n = q / hw, rem = q - n * hw;
+        const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
+        xvo = keep_or_oob((uint32_t)(n * a.pci * HWX + oh * a.psh * a.pW + ow * a.psw) * 4u, valid);
+    }
+    __device__ void begin(int kb) {
+        const bool proj = kb >= TAPS * CB;
+        t = proj ? TAPS : kb / CB;
+        cb = proj ? kb - TAPS * CB : kb - t * CB;
+    }
+    __device__ void step(bool more) {
+        const bool wrap = t < TAPS && cb + 1 == CB;
+        const int cb1 = wrap ? 0 : cb + 1;
+        const int t1 = wrap ? t + 1 : t;
+        t = more ? t1 : t;
+        cb = more ? cb1 : cb;
+    }
+    // part 0: A and the first half of B; part 1: the rest of B
+    __device__ void issue(float* S, bool on, int part) {
+        const bool proj = t == TAPS;
+        if (part == 0) {
+            const uint32_t sa = (uint32_t)(t * Ci + cb * 32) * 4u;
+#pragma unroll
+            for (int i = 0; i < A_LOADS; ++i)
+                dma_load16(rw, S + (wave + T::NW * i) * 8 * 32, on ? avo[i] : kOutOfRange, sa);
+            const int r = t / KW, c = t - r * KW;
+            const uint32_t tap = keep_or_oob((uint32_t)(px.bpo + r * W + c) * 4u, on && !proj && px.inside(t));
+            bv = proj ? (on ? xvo : kOutOfRange) : tap;
+        }
+        const int hw = proj ? HWX : HW;
+        const uint32_t s0 = (uint32_t)((cb * 32 + b_kr0) * hw) * 4u;
+        float* d0 = S + D::A_FLOATS + b_kr0 * T::BN + b_grp * 64;
+        constexpr int H = D::B_LOADS / 2;
+        if (proj) {
+#pragma unroll
+            for (int i = part * H; i < (part + 1) * H; ++i) dma_load4(rx, d0 + i * T::BN, bv, s0 + (uint32_t)(i * hw) * 4u);
+        } else {
+#pragma unroll
+            for (int i = part * H; i < (part + 1) * H; ++i) dma_load4(rin, d0 + i * T::BN, bv, s0 + (uint32_t)(i * hw) * 4u);
+        }
     }
 };
 
@@ -1107,6 +1204,76 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
         launch_conv<ConvTSmall>(a, avec, dma, name);
 }
 
+template <class T>
+static void launch_conv_proj(ConvArgs& a, const char* entry) {
+    a.tiles_m = (int)ceil_div(a.Co, T::BM);
+    a.tiles_n = (int)ceil_div(a.Npix, T::BN);
+    char name[64];
+    snprintf(name, sizeof name, "conv_igemm_%dx%d_k3x3p_dma", T::BM, T::BN);
+    launch_conv_dma_t<T, DmaProj<T, 3, 3>>(a, entry, name);
+}
+
+// nnc_hip_conv_proj: act(conv3x3(in, w[:, :9*Ci]) + conv1x1(x, w[:, 9*Ci:],
+// stride psh x psw) + bias); w packed [Co][9*Ci + Cx].
+static void conv_proj_run(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
+                          int ph, int pw, int psh, int psw, int act, const char* name) {
+    if (!conv_check(in, x, out, name)) return;
+    if (!w || !w->data || !w->shape || w->ndim != 2) return fail(NNC_HIP_EINVAL, name, "weights must be [Co][K]");
+    if (!(kh == 3 && kw == 3)) return fail(NNC_HIP_EUNSUPP, name, "only 3x3 convolutions take a projection");
+    if (sh <= 0 || sw <= 0 || ph < 0 || pw < 0 || psh <= 0 || psw <= 0)
+        return fail(NNC_HIP_EINVAL, name, "bad stride/pad");
+    ConvArgs a{};
+    a.in = (const float*)in->data;
+    a.w = (const float*)w->data;
+    a.bias = (b && b->data) ? (const float*)b->data : nullptr;
+    a.out = (float*)out->data;
+    a.pin = (const float*)x->data;
+    a.N = (int)in->shape[0];
+    a.Ci = (int)in->shape[1];
+    a.H = (int)in->shape[2];
+    a.W = (int)in->shape[3];
+    a.Co = (int)out->shape[1];
+    a.Ho = (int)out->shape[2];
+    a.Wo = (int)out->shape[3];
+    a.pci = (int)x->shape[1];
+    a.pH = (int)x->shape[2];
+    a.pW = (int)x->shape[3];
+    a.kh = kh;
+    a.kw = kw;
+    a.sh = sh;
+    a.sw = sw;
+    a.ph = ph;
+    a.pw = pw;
+    a.psh = psh;
+    a.psw = psw;
+    a.act = act;
+    const int64_t K = (int64_t)a.Ci * kh * kw + a.pci;
+    if (w->shape[0] != a.Co || w->shape[1] != K) return fail(NNC_HIP_EINVAL, name, "weights are not [Co][9*Ci + Cx]");
+    if (x->shape[0] != a.N) return fail(NNC_HIP_EINVAL, name, "projection input batch differs");
+    if (out->shape[0] != a.N) return fail(NNC_HIP_EINVAL, name, "output batch differs");
+    // every projection tap (oh * psh, ow * psw) inside the projection input
+    if ((int64_t)(a.Ho - 1) * psh >= a.pH || (int64_t)(a.Wo - 1) * psw >= a.pW)
+        return fail(NNC_HIP_EINVAL, name, "output larger than the strided projection input");
+    if (a.bias && numel(b) < a.Co) return fail(NNC_HIP_EINVAL, name, "bias smaller than Co");
+    if (a.Ci % 32 != 0 || a.pci % 32 != 0 || !aligned16(a.w))
+        return fail(NNC_HIP_EUNSUPP, name, "needs Ci and Cx multiples of 32 and 16-byte aligned weights");
+    const int64_t npix = (int64_t)a.N * a.Ho * a.Wo;
+    const int64_t in_bytes = (int64_t)a.N * a.Ci * a.H * a.W * 4, x_bytes = numel(x) * 4;
+    if (K >= (1 << 30) || npix >= (1 << 30) || in_bytes >= ((int64_t)1 << 31) || x_bytes >= ((int64_t)1 << 31) ||
+        (int64_t)a.Co * K * 4 >= ((int64_t)1 << 31))
+        return fail(NNC_HIP_EUNSUPP, name, "inputs or weights of 2 GiB or more");
+    a.K = (int)K;
+    a.ldw = (int)K;
+    a.Npix = (int)npix;
+    a.vec_out = aligned16(a.out);
+    a.out32 = (int64_t)a.N * a.Co * a.Ho * a.Wo * 4 < ((int64_t)1 << 31);
+    if (a.N == 0 || a.Co == 0 || a.Ho <= 0 || a.Wo <= 0) return;
+    // the tile choice of conv_run
+    if (a.K >= 512 && a.Co >= 128 && a.Npix >= 1024) return launch_conv_proj<ConvT128>(a, name);
+    if (a.K >= 512 && a.Co <= 64 && a.Npix >= 4096) return launch_conv_proj<ConvT64>(a, name);
+    launch_conv_proj<ConvTSmall>(a, name);
+}
+
 }  // namespace nnc
 
 using namespace nnc;
@@ -1171,6 +1338,13 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
 // up to 32). out = act(conv(in, w) + bias (+ res)), act 0 none, 1 relu, 2
 // sigmoid; `b` and `res` may be NULL, `res` may be the same buffer as `out`.
 // Weights 16-byte aligned; other shapes give NNC_HIP_EUNSUPP.
+void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
+                       int ph, int pw, int psh, int psw, int act) {
+    const char* name = "nnc_hip_conv_proj";
+    if (act < kActNone || act > kActSigmoid) return fail(NNC_HIP_EINVAL, name, "act must be 0, 1 or 2");
+    conv_proj_run(in, w, b, x, out, kh, kw, sh, sw, ph, pw, psh, psw, act, name);
+}
+
 void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh, int sw,
                          int ph, int pw, int act) {
     const char* name = "nnc_hip_conv_packed";

@@ -467,6 +467,29 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
     (void)sh, (void)sw, (void)ph, (void)pw;
     conv("nnc_hip_conv_add_relu", in, w, b, res, out, kh, kw, false);
 }
+// conv.hip conv_proj_run: one direct-to-LDS kernel over K = 9*Ci + Cx
+void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
+                       int ph, int pw, int psh, int psw, int act) {
+    (void)kh, (void)kw, (void)sh, (void)sw, (void)ph, (void)pw, (void)psh, (void)psw, (void)act;
+    const char* op = "nnc_hip_conv_proj";
+    if (!in || !w || !x || !out || !in->shape || !w->shape || !out->shape || w->ndim != 2 || out->ndim != 4) return;
+    const int64_t N = out->shape[0], Co = out->shape[1], npix = N * out->shape[2] * out->shape[3];
+    const int64_t K = w->shape[1];
+    if (N == 0 || Co == 0 || npix == 0) return;
+    const double flops = 2.0 * Co * (double)npix * K;
+    const double bytes = nbytes(in) + nbytes(x) + nbytes(w) + nbytes(b) + nbytes(out);
+    const MfmaKind* k = (K >= 512 && Co >= 128 && npix >= 1024) ? &kConv128
+                        : (K >= 512 && Co <= 64 && npix >= 4096) ? &kConv64x128 : &kConv64;
+    char name[64];
+    snprintf(name, sizeof name, "conv_igemm_%dx%d_k3x3p_dma", k->bm, k->bn);
+    const int tiles = (int)(ceil_div(Co, k->bm) * ceil_div(npix, k->bn));
+    MfmaResult m = mfma_kernel(*k, tiles, K, bytes, nbytes(w));
+    record(op, name, m.us, flops, bytes);
+    if (!m.sk.needs_fixup()) return;
+    const int64_t per = m.sk.total() / m.sk.G;
+    if (k == &kConv64x128 && (m.sk.iters + per - 1) / per + 1 <= kMaxInKernelParts) return;
+    record(op, "conv_streamk_fixup", fixup_us(*k, m.sk), 0.0, 0.0);
+}
 void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh, int sw,
                          int ph, int pw, int act) {
     (void)sh, (void)sw, (void)ph, (void)pw, (void)act;

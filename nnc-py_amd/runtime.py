@@ -67,6 +67,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_conv_add_relu": (abi.TARGET_SIGNATURES["nnc_hip_conv_add_relu"], None),
     "nnc_hip_conv_packed": (abi.TARGET_SIGNATURES["nnc_hip_conv_packed"], None),
     "nnc_hip_transfer": (abi.TARGET_SIGNATURES["nnc_hip_transfer"], None),
+    "nnc_hip_conv_proj": (abi.TARGET_SIGNATURES["nnc_hip_conv_proj"], None),
 }
 
 

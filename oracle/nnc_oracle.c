@@ -1014,3 +1014,51 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
     free(wt);
     free(tmp);
 }
+
+/* ------------------------------------------------------------------------
+ * Convolution with a folded 1x1 projection of the mi355x target
+ * (include/nnc_hip.h), no reference counterpart: the rows of w, [Co][kh*kw*Ci
+ * + Cx], are split into the tap-major kernel and the projection weights;
+ * nnc_conv of x with the projection (1x1, stride psh x psw, no bias,
+ * ops.c:720-1050) gives the residual that nnc_hip_conv_packed (above) adds
+ * before the activation, as the reference's Conv -> Conv -> Add -> Relu
+ * sequence would. Pinned by composition of pinned entry points.
+ * ---------------------------------------------------------------------- */
+void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
+                       int ph, int pw, int psh, int psw, int act) {
+    if (!in || !w || !x || !out || w->ndim != 2 || in->ndim != 4 || x->ndim != 4 || out->ndim != 4) return;
+    const int64_t co = w->shape[0], ci = in->shape[1], cx = x->shape[1], taps = (int64_t)kh * kw;
+    const int64_t row = w->shape[1], k3 = taps * ci;
+    if (row != k3 + cx) return;
+    const int64_t n = numel(out);
+    float* w3 = (float*)malloc((size_t)(co * k3 > 0 ? co * k3 : 1) * sizeof(float));
+    float* wp = (float*)malloc((size_t)(co * cx > 0 ? co * cx : 1) * sizeof(float));
+    float* proj = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    if (!w3 || !wp || !proj) {
+        free(w3);
+        free(wp);
+        free(proj);
+        return;
+    }
+    const float* src = (const float*)w->data;
+    for (int64_t o = 0; o < co; ++o) {
+        memcpy(w3 + o * k3, src + o * row, (size_t)k3 * sizeof(float));
+        memcpy(wp + o * cx, src + o * row + k3, (size_t)cx * sizeof(float));
+    }
+    int64_t w3shape[4] = {co, kh, kw, ci}, wpshape[4] = {co, cx, 1, 1};
+    Tensor tw3 = *w, twp = *w, tproj = *out;
+    tw3.data = w3;
+    tw3.ndim = 4;
+    tw3.shape = w3shape;
+    tw3.nbytes = (size_t)(co * k3) * sizeof(float);
+    twp.data = wp;
+    twp.ndim = 4;
+    twp.shape = wpshape;
+    twp.nbytes = (size_t)(co * cx) * sizeof(float);
+    tproj.data = proj;
+    nnc_conv(x, &twp, NULL, &tproj, 1, 1, psh, psw, 0, 0);
+    nnc_hip_conv_packed(in, &tw3, b, &tproj, out, kh, kw, sh, sw, ph, pw, act);
+    free(w3);
+    free(wp);
+    free(proj);
+}

@@ -67,14 +67,21 @@ def test_o3_fusion_and_prepack_on_resnet18(pkg):
     from nnc_py_amd.compiler import build_program, zoo
     prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
     ops = [c.op for c in prog.calls if c.node]  # without the stream fork/select/join calls
-    assert len(ops) == 23  # Flatten is an alias of the pooled tensor: no call
+    assert len(ops) == 20  # Flatten is an alias of the pooled tensor: no call
     assert "nnc_flatten" not in ops and prog.plan.aliases
-    assert ops.count("nnc_hip_conv_packed") == 17  # the stem and every 3x3 conv
+    assert ops.count("nnc_hip_conv_packed") == 14  # the stem and every 3x3 conv without a projection
     assert "nnc_add_relu" not in ops and "nnc_relu" not in ops
-    assert ops[0] == "nnc_hip_conv_packed" and ops.count("nnc_conv1x1") == 3
+    # the three downsample blocks: their 1x1 projection folded into the last conv
+    assert ops[0] == "nnc_hip_conv_packed" and ops.count("nnc_conv1x1") == 0 and ops.count("nnc_hip_conv_proj") == 3
     assert ops[-1] == "nnc_gemm_nt"
     with_res = [c for c in prog.calls if c.op == "nnc_hip_conv_packed" and c.args[3][0] == "t"]
-    assert len(with_res) == 8
+    assert len(with_res) == 5
+    for c in prog.calls:
+        if c.op == "nnc_hip_conv_proj":
+            h, w, x, out = (prog.graph.tensors[c.args[k][1]] for k in (0, 1, 3, 4))
+            co, ci, cx = out.shape[1], h.shape[1], x.shape[1]
+            assert w.shape == (co, 9 * ci + cx) and cx == ci // 2 and x.shape[2] == 2 * out.shape[2]
+            assert [a[1] for a in c.args[5:]] == [3, 3, 1, 1, 1, 1, 2, 2, 1]
     for c in prog.calls:
         if c.op != "nnc_hip_conv_packed":
             continue
@@ -107,6 +114,14 @@ def test_packed_conv_weights_are_the_transposed_constants(pkg):
                 assert not packed[:, k:].any() and packed.shape[1] % 32 == 0
             else:
                 np.testing.assert_array_equal(packed, w.transpose(0, 2, 3, 1))
+            n += 1
+        elif c.op == "nnc_hip_conv_proj":
+            rows = prog.graph.tensors[c.args[1][1]].data
+            node = next(m for m in prog.order if m.name == c.node)
+            w3, w1 = (orig[m] for m in node.metadata["weights_from"])
+            co = w3.shape[0]
+            np.testing.assert_array_equal(rows, np.concatenate([w3.transpose(0, 2, 3, 1).reshape(co, -1),
+                                                                w1.reshape(co, -1)], axis=1))
             n += 1
     assert n == 17
 

@@ -187,6 +187,75 @@ def test_conv_packed_stem(n, h, hip, dmem, abi, oracle_lib):
     _check(got, exp, case["name"])
 
 
+def _proj_case(rng, n, ci, h, co, cx, xh, ps, act=1, bias=True):
+    """nnc_hip_conv_proj case: 3x3 / stride 1 / pad 1 over x [n, ci, h, h]
+    plus a 1x1 stride-ps projection of p [n, cx, xh, xh]; weights drawn in
+    the reference layout, packed [Co][9*Ci + Cx]."""
+    x = rng.standard_normal((n, ci, h, h)).astype(np.float32)
+    pin = rng.standard_normal((n, cx, xh, xh)).astype(np.float32)
+    w3 = (rng.standard_normal((co, ci, 3, 3)) / np.sqrt(ci * 9)).astype(np.float32)
+    w1 = (rng.standard_normal((co, cx, 1, 1)) / np.sqrt(cx)).astype(np.float32)
+    rows = np.concatenate([w3.transpose(0, 2, 3, 1).reshape(co, -1), w1.reshape(co, cx)], axis=1)
+    tensors = {"x": x, "w": np.ascontiguousarray(rows), "p": pin, "out": np.zeros((n, co, h, h), np.float32)}
+    if bias:
+        tensors["b"] = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    args = [("t", "x"), ("t", "w"), ("t", "b") if bias else ("null",), ("t", "p"), ("t", "out")]
+    args += [("i", v) for v in (3, 3, 1, 1, 1, 1, ps, ps, act)]
+    return {"name": f"proj_{n}x{ci}x{h}_{co}_p{cx}x{xh}s{ps}_a{act}{'b' if bias else ''}",
+            "op": "nnc_hip_conv_proj", "tensors": tensors, "args": args, "outputs": ["out"], "bar": "fp"}
+
+
+# every tile configuration (64x64, 64x128 with the in-kernel finish, 128x128),
+# ResNet-18's three downsample blocks at batch 1 and 32, a stride-1
+# projection, odd images and Co / pixel tails
+PROJ_SHAPES = [
+    (2, 64, 28, 64, 32, 56, 2),
+    (4, 64, 56, 64, 64, 112, 2),
+    (8, 128, 28, 128, 64, 56, 2),
+    (1, 128, 28, 128, 64, 56, 2),
+    (1, 512, 7, 512, 256, 14, 2),
+    (32, 256, 14, 256, 128, 28, 2),
+    (3, 32, 13, 96, 32, 13, 1),
+    (2, 64, 9, 40, 96, 17, 2),
+]
+
+
+@pytest.mark.parametrize("shape", PROJ_SHAPES, ids=[str(s) for s in PROJ_SHAPES])
+def test_conv_proj_shapes(shape, hip, dmem, abi, oracle_lib):
+    case = _proj_case(np.random.default_rng(29), *shape)
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    _check(got, exp, case["name"])
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("bias", [True, False])
+def test_conv_proj_epilogues(act, bias, hip, dmem, abi, oracle_lib):
+    for shape in ((2, 64, 12, 64, 32, 24, 2), (8, 128, 28, 128, 64, 56, 2)):
+        case = _proj_case(np.random.default_rng(31), *shape, act=act, bias=bias)
+        print(f"case {case['name']}", flush=True)
+        exp = caserun.run_case(oracle_lib, case, abi)["out"]
+        got = caserun.run_case(hip, case, abi, dmem)["out"]
+        _check(got, exp, case["name"])
+
+
+@pytest.mark.parametrize("why,cx,xh,cols", [("Cx not a multiple of 32", 48, 24, None),
+                                            ("projection input too small", 32, 22, None),
+                                            ("weight rows of the wrong length", 32, 24, 9 * 64 + 16)])
+def test_conv_proj_rejects(why, cx, xh, cols, hip, dmem, abi):
+    """Refused on the host (error code, nothing launched, output untouched)."""
+    from nnc_py_amd import runtime
+    case = _proj_case(np.random.default_rng(3), 2, 64, 12, 64, cx, xh, 2)
+    if cols is not None:
+        case["tensors"]["w"] = np.zeros((64, cols), np.float32)
+    runtime.clear_error()
+    out = caserun.run_case(hip, case, abi, dmem)["out"]
+    assert runtime.last_error()[0] != 0, why
+    assert not out.any()
+    runtime.clear_error()
+
+
 @pytest.mark.parametrize("act", [0, 1, 2])
 @pytest.mark.parametrize("bias,res", [(True, False), (False, True), (False, False)])
 def test_conv_packed_epilogues(act, bias, res, hip, dmem, abi, oracle_lib):

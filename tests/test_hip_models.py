@@ -154,8 +154,14 @@ def test_branch_streams_match_one_stream(hip, batch):
     (the same kernels, each on its own per-stream scratch)."""
     from nnc_py_amd import runtime
     from nnc_py_amd.compiler import Executor, build_program, zoo
+    from nnc_py_amd.compiler import executor
     x = np.random.default_rng(6).standard_normal((batch, 3, 224, 224)).astype(np.float32)
-    one = Executor(build_program(zoo.resnet18(batch=batch, seed=1), opt_level=3, branch_streams=False), device=True)
+    executor.PROJECTION_FUSION = False  # the kernels of the two-stream program, on one stream
+    try:
+        one = Executor(build_program(zoo.resnet18(batch=batch, seed=1), opt_level=3, branch_streams=False),
+                       device=True)
+    finally:
+        executor.PROJECTION_FUSION = True
     one.set_input("input", x)
     one.run()
     want = one.get("output")
