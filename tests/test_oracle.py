@@ -323,6 +323,37 @@ def test_oracle_conv_packed_rows_stem(oracle_lib, abi):
     assert caserun.same_bits(got, ref)
 
 
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("ps,xh", [(2, 12), (1, 6), (2, 13)])
+def test_oracle_conv_proj_composition(act, ps, xh, oracle_lib, abi):
+    """nnc_hip_conv_proj: rows [W3 tap-major | Wp] give the float64 3x3
+    convolution of x plus the float64 strided 1x1 convolution of p plus
+    the bias, then the activation; a row split one column off, a missed
+    stride or a dropped projection fails."""
+    rng = np.random.default_rng(43 + act)
+    n, ci, h, co, cx = 2, 32, 6, 5, 32
+    x = rng.standard_normal((n, ci, h, h)).astype(F32)
+    p = rng.standard_normal((n, cx, xh, xh)).astype(F32)
+    w3 = rng.standard_normal((co, ci, 3, 3)).astype(F32)
+    w1 = rng.standard_normal((co, cx, 1, 1)).astype(F32)
+    b = rng.standard_normal(co).astype(F32)
+    rows = np.concatenate([w3.transpose(0, 2, 3, 1).reshape(co, -1), w1.reshape(co, cx)], axis=1)
+    t = {"x": x, "w": np.ascontiguousarray(rows), "b": b, "p": p, "out": np.zeros((n, co, h, h), F32)}
+    args = [("t", "x"), ("t", "w"), ("t", "b"), ("t", "p"), ("t", "out")]
+    args += [("i", v) for v in (3, 3, 1, 1, 1, 1, ps, ps, act)]
+    got = caserun.run_case(oracle_lib, {"name": "proj", "op": "nnc_hip_conv_proj", "tensors": t, "args": args,
+                                        "outputs": ["out"]}, abi)["out"]
+    pre = (_np_conv_f64(x, w3, b, 1, 1, 1, 1, h, h)
+           + _np_conv_f64(p, w1, np.zeros(co, F32), ps, ps, 0, 0, h, h))
+    if act == 1:
+        want = np.maximum(pre, 0.0)
+    elif act == 2:
+        want = 1.0 / (1.0 + np.exp(-pre))
+    else:
+        want = pre
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
 def test_oracle_conv_add_relu_composition(oracle_lib, abi):
     rng = np.random.default_rng(41)
     c = _conv_case(rng, "nnc_conv", 2, 5, 8, 8, 4, 3, 3, 1, 1, 1, 1)
