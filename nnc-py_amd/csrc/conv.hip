@@ -917,6 +917,83 @@ __global__ void __launch_bounds__(256) conv_fixup_k(ConvArgs a, StreamK sk) {
     fixup_store(a, co, p0, v);
 }
 
+// Shared tiles with many partials (short problems: few tiles, long K): the
+// partial list is split over four groups of 64 threads (group q sums
+// partials q, q + 4, ... in workgroup order), and group 0 adds the four
+// sums in group order through LDS - deterministic, and each thread waits
+// on a quarter of the loads. Grid (BM*BN/256, stream-K tiles): a workgroup
+// finishes 64 float4 of a tile.
+template <class T>
+__global__ void __launch_bounds__(256) conv_fixup_split_k(ConvArgs a, StreamK sk) {
+    __shared__ float4 part[3][64];
+    const int t = blockIdx.y;
+    int g0, g1, first_slot;
+    if (!tile_partials(sk, t, g0, g1, first_slot)) return;  // uniform over the workgroup
+    const int grp = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int e4 = blockIdx.x * 64 + lane;
+    const int mt = t % a.tiles_m, nt = t / a.tiles_m;
+    const int co = mt * T::BM + (e4 * 4) / T::BN;
+    const int p0 = nt * T::BN + (e4 * 4) % T::BN;
+    const bool valid = e4 < T::BM * T::BN / 4 && co < a.Co && p0 < a.Npix;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) {
+        int g = g0 + grp;
+        if (grp == 0) {
+            v = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g0, first_slot))[e4];
+            g += 4;
+        }
+        for (; g + 12 <= g1; g += 16) {
+            float4 p[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) p[q] = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g + 4 * q, 0))[e4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v.x += p[q].x;
+                v.y += p[q].y;
+                v.z += p[q].z;
+                v.w += p[q].w;
+            }
+        }
+        for (; g <= g1; g += 4) {
+            const float4 p = reinterpret_cast<const float4*>(partial_slot<T>(a.ws, g, 0))[e4];
+            v.x += p.x;
+            v.y += p.y;
+            v.z += p.z;
+            v.w += p.w;
+        }
+    }
+    if (grp > 0) part[grp - 1][lane] = v;
+    __syncthreads();
+    if (grp > 0 || !valid) return;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const float4 p = part[q][lane];
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
+    }
+    fixup_store(a, co, p0, v);
+}
+
+// The fixup launch of a stream-K conv. The split kernel only where the
+// plain one leaves the GPU nearly empty (at most kSplitFixupGroups
+// workgroups) and each shared tile has at least kSplitFixupParts partials:
+// ResNet-18's layers 3 and 4 at batch 1 (+1.3%); with larger grids its 4x
+// workgroups measured slower (batch 8 -3 to -12%).
+static constexpr int kSplitFixupParts = 16, kSplitFixupGroups = 64;
+template <class T>
+static void launch_conv_fixup(ConvArgs& a, const StreamK& sk) {
+    set_work(0.0, 0.0);
+    const int64_t per = sk.total() / sk.G;  // slices per workgroup range (>= 1)
+    const int64_t parts = (sk.iters + per - 1) / per + 1;
+    if (parts >= kSplitFixupParts && (int64_t)(T::BM * T::BN / 1024) * sk.sk_tiles <= kSplitFixupGroups)
+        launch("conv_streamk_fixup", conv_fixup_split_k<T>, dim3(T::BM * T::BN / 256, sk.sk_tiles), dim3(256), 0, a,
+               sk);
+    else
+        launch("conv_streamk_fixup", conv_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, a, sk);
+}
+
 // Reference-layout weights [Co][Ci][T] to tap-major [Co][T][Ci] (T = kh*kw),
 // so that reference-layout 3x3 calls reach the direct-to-LDS kernel. One
 // thread per output element: writes coalesce, reads stride T (cached).
@@ -979,10 +1056,7 @@ static void launch_conv_t(ConvArgs& a, const char* entry) {
         snprintf(name, sizeof name, "conv_igemm_%dx%d_kany_%s", T::BM, T::BN, AVEC ? "v4" : "s1");
     set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
     launch(name, kernel, dim3(sk.G), dim3(256), lds, a, sk);
-    if (sk.needs_fixup()) {
-        set_work(0.0, 0.0);
-        launch("conv_streamk_fixup", conv_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, a, sk);
-    }
+    if (sk.needs_fixup()) launch_conv_fixup<T>(a, sk);
 }
 
 template <class T, class L>
@@ -1021,10 +1095,7 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
     a.cnt = in_kernel ? tile_counters((size_t)sk.sk_tiles) : nullptr;
     set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
     launch(name, kernel, dim3(sk.G), dim3(T::THREADS), lds, a, sk);
-    if (sk.needs_fixup() && !a.cnt) {
-        set_work(0.0, 0.0);
-        launch("conv_streamk_fixup", conv_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, a, sk);
-    }
+    if (sk.needs_fixup() && !a.cnt) launch_conv_fixup<T>(a, sk);
 }
 
 template <class T, int KH, int KW>
