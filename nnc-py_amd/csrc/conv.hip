@@ -1261,12 +1261,6 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
     // ones (1x1, the 3-channel stem) and small images run best on 64x64
     // tiles, whose shorter per-tile latency and larger tile count fill the
     // GPU.
-#ifdef NNC_1X1_TILE
-    if (kh == 1 && kw == 1 && dma) {
-        if (NNC_1X1_TILE == 2) return launch_conv<ConvT128>(a, avec, dma, name);
-        if (NNC_1X1_TILE == 1) return launch_conv<ConvT64>(a, avec, dma, name);
-    }
-#endif
     if (a.K >= 512 && a.Co >= 128 && a.Npix >= 1024)
         launch_conv<ConvT128>(a, avec, dma, name);
     else if (a.K >= 512 && a.Co <= 64 && a.Npix >= 4096)
