@@ -231,6 +231,13 @@ __global__ void __launch_bounds__(256) maxpool3s2_k(PoolArgs a, int nbands, int 
     }
 }
 
+template <int R>
+static void maxpool3s2_launch(const char* name, const PoolArgs& a, int64_t nc, int nchunks) {
+    const int nbands = (int)ceil_div(a.Ho, R);
+    const int64_t waves = nc * nbands * nchunks;
+    launch(name, maxpool3s2_k<R>, dim3((unsigned)ceil_div(waves, 4)), dim3(256), 0, a, nbands, nchunks);
+}
+
 __global__ void fill_value_k(float* out, int64_t n, float v) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = v;
@@ -280,12 +287,15 @@ static void pool_entry(const char* name, Tensor* in, Tensor* out, int kh, int kw
     if ((int64_t)a.Ho * a.Wo >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "output plane too large");
     if (MAX && kh == 3 && kw == 3 && sh == 2 && sw == 2 && ph == 1 && pw == 1 && a.W % 2 == 0 && a.H > 0 &&
         a.Ho > 0 && a.Wo > 0 && nc > 0 && numel(in) * 4 < ((int64_t)1 << 31)) {
-        constexpr int R = 8;
-        const int nbands = (int)ceil_div(a.Ho, R), nchunks = (int)ceil_div(a.Wo, 64);
-        const int64_t waves = nc * nbands * nchunks;
-        if (waves < ((int64_t)1 << 31) - 4) {
-            launch(name, maxpool3s2_k<R>, dim3((unsigned)ceil_div(waves, 4)), dim3(256), 0, a, nbands, nchunks);
-            return;
+        // 8 output rows per wave, fewer where that leaves the GPU short of
+        // waves (ResNet-18 stem pool: batch 1 448 waves -> 2 rows, 11.9 ->
+        // 6.2 us; batch 8 3584 waves -> 4 rows, 13.4 -> 10.3 us)
+        const int nchunks = (int)ceil_div(a.Wo, 64);
+        const int64_t waves8 = nc * ceil_div(a.Ho, 8) * nchunks;
+        if (waves8 < ((int64_t)1 << 28)) {
+            if (waves8 < 1024) return maxpool3s2_launch<2>(name, a, nc, nchunks);
+            if (waves8 < 4096) return maxpool3s2_launch<4>(name, a, nc, nchunks);
+            return maxpool3s2_launch<8>(name, a, nc, nchunks);
         }
     }
     if (hw <= 16384 && hw > 0 && a.Ho > 0 && a.Wo > 0 && nc > 0) {

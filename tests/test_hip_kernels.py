@@ -361,7 +361,9 @@ def _maxpool_case(x, ho, wo, k=3, s=2, p=1):
 # (N, C, H, W, Ho, Wo): the ResNet stem pool, two column chunks (Wo > 64),
 # odd H, and outputs past the natural size (clamped and empty windows)
 MAXPOOL_SHAPES = [
-    (2, 64, 112, 112, 56, 56),
+    (2, 64, 112, 112, 56, 56),    # 896 waves of 8 rows: 2 rows per wave
+    (8, 64, 112, 112, 56, 56),    # 3584 waves of 8 rows: 4 rows per wave
+    (20, 64, 112, 112, 56, 56),   # 8 rows per wave
     (1, 3, 130, 130, 65, 65),
     (2, 5, 7, 8, 4, 4),
     (1, 2, 8, 8, 6, 6),
