@@ -148,6 +148,9 @@ def fuse_residual(g: Graph) -> int:
 
 
 CONV_OPS = ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu")
+# every node that runs a convolution, for FLOP accounting (the projection
+# conv's packed [Co][9*Ci + Cx] weight gives its K)
+FLOP_CONV_OPS = CONV_OPS + ("FusedConvProjRelu",)
 
 
 def pack_conv_weights(g: Graph) -> int:
@@ -481,6 +484,12 @@ def plan_memory(g: Graph, order: list[Node], strategy: str = "cost_aware",
                 for k, i in enumerate(node.inputs):
                     if allowed is not None and k not in allowed:
                         continue
+                    # a tensor the node also reads through a restricted input
+                    # (the fused conv's image, relu(conv(h) + h)) is still read
+                    # by other workgroups while finished tiles are stored
+                    if allowed is not None and any(j == i for kk, j in enumerate(node.inputs)
+                                                   if kk not in allowed):
+                        continue
                     li = live.get(i)
                     if (li and li.end == idx and not li.is_output and not li.is_input
                             and i in plan.offsets and i not in reused and sizes[i] == sizes[o]):
@@ -628,7 +637,6 @@ def fit_memory(g: Graph, order: list[Node], max_memory: int, plan_fn) -> tuple[l
 # ---------------------------------------------------------------------------
 # independent branches on the second library stream (mi355x O3)
 # ---------------------------------------------------------------------------
-CONV_OPS = ("Conv", "FusedConvRelu", "FusedConvSigmoid", "FusedConvAddRelu")
 
 
 def conv_flops(g: Graph, node: Node) -> float:
@@ -689,7 +697,7 @@ def find_branches(g: Graph, order: list[Node], max_flops: float) -> list[Branch]
         made = {t for n in main for t in n.outputs}
         if not any(t in made for t in j.inputs):
             continue
-        flops = sum(conv_flops(g, n) for n in main if n.op_type in CONV_OPS)
+        flops = sum(conv_flops(g, n) for n in main if n.op_type in FLOP_CONV_OPS)
         if max(flops, conv_flops(g, d)) > max_flops:
             continue
         out.append(Branch(d.name, [n.name for n in main], j.name))

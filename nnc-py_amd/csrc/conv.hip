@@ -1396,13 +1396,12 @@ void nnc_hip_conv_add_relu(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor
     conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, kActRelu, name, res);
 }
 
-// No reference counterpart: convolution with weights packed tap-major,
-// emitted by the mi355x target at O3 (the compiler packs the constant):
-// [Co][kh][kw][Ci] with Ci % 32 == 0 and a 1x1 or 3x3 kernel, or [Co][Kp]
-// for the 3-channel 7x7 stem (k = tap * Ci + ci, zero up to Kp = K rounded
-// up to 32). out = act(conv(in, w) + bias (+ res)), act 0 none, 1 relu, 2
-// sigmoid; `b` and `res` may be NULL, `res` may be the same buffer as `out`.
-// Weights 16-byte aligned; other shapes give NNC_HIP_EUNSUPP.
+// No reference counterpart: a residual block's 3x3 convolution with its 1x1
+// projection shortcut folded into the same contraction. Each weight row is
+// [Co][9*Ci + Cx]: the 3x3 taps tap-major over `in`, then the Cx projection
+// weights over `x` read at (oh*psh, ow*psw). out = act(conv3x3(in) +
+// conv1x1(x) + b), b the sum of both biases (may be NULL); no residual
+// argument. Ci and Cx multiples of 32.
 void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
                        int ph, int pw, int psh, int psw, int act) {
     const char* name = "nnc_hip_conv_proj";
@@ -1410,6 +1409,13 @@ void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out,
     conv_proj_run(in, w, b, x, out, kh, kw, sh, sw, ph, pw, psh, psw, act, name);
 }
 
+// No reference counterpart: convolution with weights packed tap-major,
+// emitted by the mi355x target at O3 (the compiler packs the constant):
+// [Co][kh][kw][Ci] with Ci % 32 == 0 and a 1x1 or 3x3 kernel, or [Co][Kp]
+// for the 3-channel 7x7 stem (k = tap * Ci + ci, zero up to Kp = K rounded
+// up to 32). out = act(conv(in, w) + bias (+ res)), act 0 none, 1 relu, 2
+// sigmoid; `b` and `res` may be NULL, `res` may be the same buffer as `out`
+// but not as `in`. Weights 16-byte aligned; other shapes give NNC_HIP_EUNSUPP.
 void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh, int sw,
                          int ph, int pw, int act) {
     const char* name = "nnc_hip_conv_packed";

@@ -393,6 +393,7 @@ void nnc_softmax(Tensor* in, Tensor* out, int axis) {
     if (!has_data(in) || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
     int64_t outer, len, inner;
     if (!split_axis(name, in, axis, outer, len, inner)) return;
+    if (numel(out) < numel(in)) return fail(NNC_HIP_EINVAL, name, "output smaller than input");
     if (outer * len * inner == 0) return;
     const float* x = (const float*)in->data;
     float* y = (float*)out->data;
@@ -420,6 +421,7 @@ void nnc_layernorm(Tensor* in, Tensor* scale, Tensor* bias, Tensor* out, int axi
     int64_t outer, len, inner;
     if (!split_axis(name, in, axis, outer, len, inner)) return;
     const int64_t span = len * inner;
+    if (numel(out) < numel(in)) return fail(NNC_HIP_EINVAL, name, "output smaller than input");
     if (outer * span == 0) return;
     const float* x = (const float*)in->data;
     const float* g = (scale && scale->data) ? (const float*)scale->data : nullptr;

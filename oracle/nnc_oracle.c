@@ -303,9 +303,13 @@ static void conv_generic(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, 
     const float* bias = b ? (const float*)b->data : NULL;
     float* z = (float*)out->data;
     const int64_t taps = (int64_t)Ci * kh * kw;
+    /* output planes are independent and each element's sum is the same
+     * sequential loop whichever thread runs it: threads change the time, not
+     * a bit of the result */
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
     for (int n = 0; n < N; ++n) {
-        const float* img = x + (int64_t)n * Ci * H * W;
         for (int co = 0; co < Co; ++co) {
+            const float* img = x + (int64_t)n * Ci * H * W;
             const float* filt = wt + (int64_t)co * taps;
             float* plane = z + ((int64_t)n * Co + co) * Ho * Wo;
             for (int oh = 0; oh < Ho; ++oh) {

@@ -239,3 +239,41 @@ def test_o3_downsample_branches_on_the_second_stream(pkg):
                 assert offs[a] + sizes[a] <= offs[c] or offs[c] + sizes[c] <= offs[a], (a, c)
     check_plan(prog.graph, prog.order, prog.plan, [[b.side] + b.main for b in prog.branches])
     assert not build_program(zoo.resnet18(batch=32, seed=0), opt_level=3, branch_streams=True).branches
+
+
+def _self_residual_graph(batch=1, c=64, hw=16, seed=0):
+    """relu(conv(h) + h) with h an intermediate: the fused conv reads h as
+    its image and as its residual."""
+    from nnc_py_amd.compiler import GraphBuilder
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder("self_residual")
+    x = b.input("x", (batch, c, hw, hw))
+
+    def conv(t, name):
+        w = b.const(f"{name}.w", (rng.standard_normal((c, c, 3, 3)) * np.sqrt(2.0 / (9 * c))).astype(np.float32))
+        bias = b.const(f"{name}.b", (rng.standard_normal(c) * 0.01).astype(np.float32))
+        return b.conv(t, w, bias, pads=(1, 1, 1, 1), name=f"/{name}")
+
+    h = b.relu(conv(x, "c0"))
+    s = b.add(conv(h, "c1"), h)
+    b.output(b.relu(s))
+    return b.build()
+
+
+def test_fused_conv_never_writes_over_its_own_image(pkg):
+    """relu(conv(h) + h): the residual is also the conv's image, which other
+    workgroups still read while finished tiles are stored, so the output must
+    not take over h's arena slot."""
+    from nnc_py_amd.compiler import build_program
+    from nnc_py_amd.compiler.passes import check_plan
+    prog = build_program(_self_residual_graph(), opt_level=3)
+    fused = [n for n in prog.order if n.op_type == "FusedConvAddRelu"]
+    assert len(fused) == 1 and fused[0].inputs[0] == fused[0].inputs[3]
+    h, out = fused[0].inputs[0], fused[0].outputs[0]
+    assert out not in prog.plan.inplace
+    assert prog.plan.offsets[out] != prog.plan.offsets[h]
+    check_plan(prog.graph, prog.order, prog.plan)
+    # a residual that is not the image may still be taken over
+    from nnc_py_amd.compiler import zoo
+    r18 = build_program(zoo.resnet18(batch=1, seed=0), opt_level=3)
+    assert any(n.op_type in ("FusedConvAddRelu",) and n.outputs[0] in r18.plan.inplace for n in r18.order)

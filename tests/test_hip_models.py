@@ -4,7 +4,9 @@
    no-reuse arena so every intermediate survives; each nnc_* call of the
    program is then replayed alone on the GPU from the oracle's inputs and
    compared with the oracle's output of that call, at the ResNet-18 layer
-   shapes (batch 1 and 2). Bar: 1e-4 abs / 1e-3 rel, bit-exact for pools and
+   shapes (batch 1, 2 and the benchmark's batch 32, whose kernel choices -
+   tile shapes, stream-K splits, in-kernel finishes and fixups - differ from
+   the smaller batches'). Bar: 1e-4 abs / 1e-3 rel, bit-exact for pools and
    copies.
 2. End to end: logits of the GPU program vs the oracle program. Errors
    compound over 20 unnormalised layers, so the bar is the reference's own
@@ -66,8 +68,8 @@ def _call_case(prog, call, values):
     return {"name": call.node, "op": call.op, "tensors": tensors, "args": args, "outputs": outs}
 
 
-@pytest.mark.parametrize("model,batch,opt", [("resnet18", 1, 3), ("resnet18", 2, 1), ("lenet5", 1, 1),
-                                             ("lenet5", 3, 3)])
+@pytest.mark.parametrize("model,batch,opt", [("resnet18", 1, 3), ("resnet18", 2, 1), ("resnet18", 32, 3),
+                                             ("lenet5", 1, 1), ("lenet5", 3, 3)])
 def test_per_op_parity_on_oracle_activations(model, batch, opt, hip, dmem, abi, oracle_lib):
     from nnc_py_amd.compiler import zoo
     fn = {"resnet18": lambda: zoo.resnet18(batch=batch, seed=1),
@@ -200,3 +202,29 @@ def test_graph_replay_matches_eager(hip):
         ex.run()  # eager work between replays
         runtime.sync()
     ex.close()
+
+
+def test_self_residual_block_matches_oracle(hip, oracle_lib):
+    """relu(conv(h) + h) with h an intermediate, at a size with many tiles
+    (batch 8, 64 channels, 56x56: 196 pixel tiles): the fused conv reads h
+    as image and residual and must not write over it (the arena plan gives
+    the output its own slot). GPU program vs the oracle program, O3."""
+    from nnc_py_amd.compiler import Executor, build_program
+    from test_compiler import _self_residual_graph
+    prog = build_program(_self_residual_graph(batch=8, c=64, hw=56), opt_level=3)
+    fused = [n for n in prog.order if n.op_type == "FusedConvAddRelu"]
+    assert len(fused) == 1 and prog.plan.offsets[fused[0].outputs[0]] != prog.plan.offsets[fused[0].inputs[0]]
+    x = np.random.default_rng(3).standard_normal((8, 64, 56, 56)).astype(np.float32)
+    dev = Executor(prog, device=True)
+    dev.set_input("x", x)
+    dev.run()
+    out = prog.graph.outputs[0]
+    got = dev.get(out)
+    dev.close()
+    host = Executor(build_program(_self_residual_graph(batch=8, c=64, hw=56), opt_level=3), device=False,
+                    lib=oracle_lib)
+    host.set_input("x", x)
+    host.run()
+    want = host.get(out)
+    bad = caserun.fp_violations(got, want, 1e-4, 1e-3)
+    assert bad.size == 0, f"{bad.size} of {want.size} outside the bar"
