@@ -16,9 +16,17 @@
  *     nnc_run();                                // enqueues nnc_* kernels
  *     nnc_hip_download(&tensor_output, host);   // waits, copies back
  *
- * All calls are made from one host thread at a time per device (the O0-O2
- * generated code is serial, c_emitter.py:832-847). Return codes: 0 = success,
- * otherwise an NNC_HIP_E* value, also kept for nnc_hip_last_error().
+ * Threads: the O0-O2 generated code is serial (c_emitter.py:832-847); the
+ * reference's O3 runtime calls ops from four pthreads
+ * (codegen/x86_emitters/model_source.py:609-674). Every nnc_* entry point is
+ * reentrant: each calling host thread gets its own pair of library streams
+ * with its own stream-K scratch on its first call (released for reuse when
+ * the thread exits), and its calls run in order on its own streams. Work is
+ * not ordered across threads: a thread that hands a tensor to another calls
+ * nnc_hip_sync() first. The arena, the spill pool, nnc_hip_init and
+ * nnc_hip_shutdown are process-wide: reserve and shut down while no other
+ * thread is calling. Return codes: 0 = success, otherwise an NNC_HIP_E*
+ * value, also kept (process-wide) for nnc_hip_last_error().
  */
 #ifndef NNC_HIP_H
 #define NNC_HIP_H
@@ -40,10 +48,11 @@ enum {
     NNC_HIP_ESTATE = 5    /* called before nnc_hip_init                  */
 };
 
-/* Select the device, create the library stream (default priority) and the
- * per-device workspace. Idempotent for the same device. */
+/* Select the device and create the calling thread's library streams
+ * (default priority) and workspace. Idempotent for the same device; another
+ * thread's first call (this or any nnc_* call) sets up that thread. */
 int nnc_hip_init(int device);
-/* Wait for all work, free the arena, workspace and stream. */
+/* Wait for the device, free the arena, every thread's streams and scratch. */
 void nnc_hip_shutdown(void);
 
 /* ---- the HBM arena ----------------------------------------------------- */
@@ -79,22 +88,24 @@ void nnc_hip_free(void* ptr);
 void* nnc_hip_host_malloc(size_t bytes);
 void nnc_hip_host_free(void* ptr);
 
-/* ---- host <-> device (synchronous with respect to the library stream) -- */
+/* ---- host <-> device (synchronous with respect to the calling thread's
+ * library streams) ---------------------------------------------------------- */
 int nnc_hip_upload(Tensor* t, const void* host_src);    /* t->nbytes bytes */
 int nnc_hip_download(const Tensor* t, void* host_dst);  /* t->nbytes bytes */
 int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int nnc_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
 
 /* ---- synchronisation and errors ---------------------------------------- */
-int nnc_hip_sync(void);             /* waits for the library streams */
-void* nnc_hip_stream(void);         /* stream 0's hipStream_t, for callers
+int nnc_hip_sync(void);             /* waits for the calling thread's streams */
+void* nnc_hip_stream(void);         /* the calling thread's stream 0, for callers
                                        that order their own work after ours */
 int nnc_hip_last_error(void);       /* last non-zero code since reset */
 const char* nnc_hip_last_error_message(void);
 void nnc_hip_clear_error(void);
 
 /* ---- a second stream for independent branches ---------------------------
- * Calls go to stream 0 unless stream 1 is selected. The compiler's O3
+ * Per calling thread: its calls go to its stream 0 unless it selects its
+ * stream 1. The compiler's O3
  * schedule (mi355x target) runs a branch that only depends on the fork
  * point - a residual block's 1x1 downsample convolution - on stream 1 while
  * the main branch continues on stream 0:
@@ -114,8 +125,9 @@ int nnc_hip_stream_join(void);
 
 /* ---- per-kernel timing --------------------------------------------------
  * While enabled, every kernel launch is bracketed by hipEvents recorded on
- * the library stream; durations accumulate per kernel name. Reading the
- * table synchronises. Used by bench.py for the roofline figures. */
+ * the stream it runs on; durations accumulate per kernel name in one
+ * process-wide table. Reading the table waits for the recorded events. Used
+ * by bench.py for the roofline figures. */
 void nnc_hip_profile_enable(int on);
 void nnc_hip_profile_reset(void);
 int nnc_hip_profile_count(void);
@@ -129,9 +141,10 @@ int nnc_hip_profile_entry(int i, char* name, int cap, int64_t* launches,
 int nnc_hip_profile_work(int i, double* flops, double* bytes);
 
 /* ---- launch capture ------------------------------------------------------
- * Record every kernel the following nnc_* calls enqueue into a hipGraph and
- * replay it with one launch. Between begin and end nothing executes. The
- * graph keeps the device pointers of the captured calls. */
+ * Record every kernel the calling thread's following nnc_* calls enqueue
+ * into a hipGraph (one per thread) and replay it with one launch on that
+ * thread's stream 0. Between begin and end nothing of it executes. The graph
+ * keeps the device pointers of the captured calls. */
 int nnc_hip_graph_begin(void);
 int nnc_hip_graph_end(void);
 int nnc_hip_graph_launch(void);

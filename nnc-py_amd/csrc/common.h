@@ -6,31 +6,50 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "nnc_hip.h"
 #include "nnc_ops.h"
 
 namespace nnc {
 
 // ---------------------------------------------------------------------------
-// device context (one per process; the generated code drives one device)
+// device and calling-thread state
 // ---------------------------------------------------------------------------
-// Library streams: 0 carries every call unless the caller selects 1, the
-// side stream of a forked branch (nnc_hip_stream_fork/select/join). Each
-// stream has its own scratch, so calls running concurrently on the two never
-// share partial tiles, counters or repacked weights.
+// The process drives one device (nnc_hip_init); its arena and spill pool are
+// process-wide. Everything a call mutates is per calling host thread: each
+// thread gets its own pair of library streams with their own scratch on its
+// first call, so threads calling nnc_* concurrently (the reference's O3
+// runtime runs its steps on four pthreads) never share partial tiles,
+// counters, repacked weights, a stream selection or a capture.
+// Stream 0 carries a thread's calls unless it selects 1, the side stream of
+// a forked branch (nnc_hip_stream_fork/select/join).
 static constexpr int kStreams = 2;
 
-struct Context {
+struct Device {
     int device = -1;
-    hipStream_t stream = nullptr;  // the selected stream (streams[cur])
-    hipStream_t streams[kStreams] = {};
-    int cur = 0;
-    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    int cu_count = 256;
     char* arena = nullptr;
     size_t arena_bytes = 0;
     // pinned host memory: the slow pool that spilled tensors wait in
     char* spill = nullptr;
     size_t spill_bytes = 0;
+};
+
+// Caller-provided scratch that replaces the grow-only buffers for the
+// duration of one call (the allocation-free entry point): stream-K partials
+// and tile counters; nothing is allocated while it is set.
+struct FixedScratch {
+    float* ws = nullptr;
+    size_t ws_bytes = 0;
+    int* cnt = nullptr;
+    size_t cnt_n = 0;
+};
+
+struct ThreadState {
+    hipStream_t streams[kStreams] = {};
+    int cur = 0;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     // per stream: split-K partials and other per-call scratch; grown outside capture only
     float* workspace[kStreams] = {};
     size_t workspace_bytes[kStreams] = {};
@@ -44,13 +63,24 @@ struct Context {
     bool capturing = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
-    bool profiling = false;
-    int cu_count = 256;
+    const FixedScratch* fixed = nullptr;
+    // algorithmic work of this thread's next launch (set_work)
+    double next_flops = 0.0, next_bytes = 0.0;
+    bool in_use = false;  // held by a live thread (released at thread exit, reused)
+    hipStream_t stream() const { return streams[cur]; }
 };
 
-Context& ctx();
+Device& dev();
+inline int cu_count() { return dev().cu_count; }
 
-// Returns false (and records NNC_HIP_ESTATE) if nnc_hip_init has not run.
+// The calling thread's state; valid once ready() has returned true on this
+// thread.
+ThreadState& ts();
+inline hipStream_t cur_stream() { return ts().stream(); }
+
+// Returns false (and records NNC_HIP_ESTATE) if nnc_hip_init has not run;
+// otherwise makes sure the calling thread has its streams and scratch
+// (created on its first call, NNC_HIP_EDEVICE / ENOMEM if that fails).
 bool ready(const char* who);
 
 // Record an error code + message (printed once to stderr, kept for
@@ -61,17 +91,25 @@ void fail(int code, const char* who, const char* fmt, ...);
 bool hip_ok(hipError_t e, const char* who, const char* what);
 
 // Ensure the selected stream's workspace holds at least `bytes`; returns
-// nullptr if it cannot (inside graph capture the workspace cannot grow).
+// nullptr if it cannot (inside graph capture the workspace cannot grow; with
+// fixed scratch: more than it holds).
 float* workspace(size_t bytes);
 size_t workspace_capacity();
 
 // At least `n` zeroed tile counters, or nullptr if they cannot be provided
-// (inside graph capture the buffer cannot grow). Kernels leave them zero.
+// (inside graph capture the buffer cannot grow; fixed scratch too small).
+// Kernels leave them zero; fixed scratch is cleared by a fill kernel on the
+// current stream first.
 int* tile_counters(size_t n);
 
 // At least `bytes` of scratch for a repacked weight tensor, or nullptr if it
-// cannot be provided (inside graph capture the buffer cannot grow).
+// cannot be provided (inside graph capture the buffer cannot grow; never
+// with fixed scratch).
 float* repack_buffer(size_t bytes);
+
+// Record the failure of a call whose stream-K partials did not fit: ENOMEM
+// for the grow-only workspace, EUNSUPP with the sizes for fixed scratch.
+void partials_fail(const char* who, size_t bytes);
 
 // ---------------------------------------------------------------------------
 // kernel launch with optional hipEvent timing (keyed by kernel name)
@@ -94,7 +132,7 @@ inline void launch(const char* name, Kernel kernel, dim3 grid, dim3 block, size_
                    Args... args) {
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) return;
     TimedScope scope(name);
-    hipLaunchKernelGGL(kernel, grid, block, lds, ctx().stream, args...);
+    hipLaunchKernelGGL(kernel, grid, block, lds, cur_stream(), args...);
     hip_ok(hipGetLastError(), name, "launch");
 }
 
@@ -128,7 +166,7 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // items per thread.
 inline unsigned grid_for(int64_t n, int per, int block = 256) {
     int64_t g = ceil_div(ceil_div(n, per), block);
-    const int64_t cap = (int64_t)ctx().cu_count * 16;
+    const int64_t cap = (int64_t)cu_count() * 16;
     if (g > cap) g = cap;
     return (unsigned)(g < 1 ? 1 : g);
 }

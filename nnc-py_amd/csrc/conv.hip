@@ -1031,23 +1031,23 @@ template <class T, int KH, int KW, bool AVEC>
 static void launch_conv_t(ConvArgs& a, const char* entry) {
     auto kernel = conv_streamk_k<T, KH, KW, AVEC>;
     const size_t lds = (size_t)T::LDS_FLOATS * sizeof(float);
-    static bool configured = false;
-    static int slots = 0;
-    if (!configured) {
-        if (!hip_ok(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)lds),
-                    entry, "hipFuncSetAttribute"))
-            return;
-        slots = resident_groups(kernel, lds);
-        configured = true;
-    }
+    // once per kernel, thread-safe (C++ static initialisation): the LDS limit
+    // and the persistent grid size; -1 if the attribute could not be set
+    static const int slots = [&] {
+        if (hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+            return -1;
+        return resident_groups(kernel, lds);
+    }();
+    if (slots < 0) return fail(NNC_HIP_EDEVICE, entry, "hipFuncSetAttribute failed");
     // K == 0 (no input channels) still runs one empty slice so the epilogue
     // writes act(bias)
     const int iters = a.K > 0 ? (int)ceil_div(a.K, T::BK) : 1;
     const StreamK sk = plan_streamk(a.tiles_m * a.tiles_n, iters, slots, fixup_slices<T>());
     if (sk.G < 1) return;
-    float* ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
-    if (!ws) return fail(NNC_HIP_ENOMEM, entry, "no workspace for stream-K partials");
+    const size_t ws_bytes = (size_t)sk.G * 2 * T::BM * T::BN * sizeof(float);
+    float* ws = workspace(ws_bytes);
+    if (!ws) return partials_fail(entry, ws_bytes);
     a.ws = ws;
     char name[64];
     if (KH > 0)
@@ -1068,23 +1068,23 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
                          ((T::BM == 64 && T::BN == 128) || (NNC_CONV_FIN128 && T::BM == 128 && T::BN == 128));
     auto kernel = conv_dma_k<T, L, FIN>;
     const size_t lds = (size_t)(DmaStage<T>::LDS_FLOATS + L::EXTRA_LDS_FLOATS) * sizeof(float);
-    static bool configured = false;
-    static int slots = 0;
-    if (!configured) {
-        if (!hip_ok(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)lds),
-                    entry, "hipFuncSetAttribute"))
-            return;
-        slots = resident_groups(kernel, lds, T::THREADS);
-        configured = true;
-    }
+    // once per kernel, thread-safe (C++ static initialisation): the LDS limit
+    // and the persistent grid size; -1 if the attribute could not be set
+    static const int slots = [&] {
+        if (hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+            return -1;
+        return resident_groups(kernel, lds, T::THREADS);
+    }();
+    if (slots < 0) return fail(NNC_HIP_EDEVICE, entry, "hipFuncSetAttribute failed");
     // K == 0 (no input channels) still runs one empty slice so the epilogue
     // writes act(bias)
     const int iters = a.K > 0 ? (int)ceil_div(a.K, T::BK) : 1;
     const StreamK sk = plan_streamk(a.tiles_m * a.tiles_n, iters, slots, fixup_slices<T>());
     if (sk.G < 1) return;
-    float* ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
-    if (!ws) return fail(NNC_HIP_ENOMEM, entry, "no workspace for stream-K partials");
+    const size_t ws_bytes = (size_t)sk.G * 2 * T::BM * T::BN * sizeof(float);
+    float* ws = workspace(ws_bytes);
+    if (!ws) return partials_fail(entry, ws_bytes);
     a.ws = ws;
     // shared tiles with at most kMaxInKernelParts contributors are finished
     // inside the kernel by the last to arrive; tiles split further (short

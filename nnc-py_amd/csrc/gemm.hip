@@ -307,16 +307,15 @@ template <class T, int AK, int BKIND>
 static void launch_mfma(GemmArgs& g, int batches, const char* name) {
     auto kernel = gemm_streamk_k<T, AK, BKIND>;
     const size_t lds = (size_t)T::LDS_FLOATS * sizeof(float);
-    static bool configured = false;
-    static int slots = 0;
-    if (!configured) {
-        if (!hip_ok(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)lds),
-                    name, "hipFuncSetAttribute"))
-            return;
-        slots = resident_groups(kernel, lds);
-        configured = true;
-    }
+    // once per kernel, thread-safe (C++ static initialisation): the LDS limit
+    // and the persistent grid size; -1 if the attribute could not be set
+    static const int slots = [&] {
+        if (hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+            return -1;
+        return resident_groups(kernel, lds);
+    }();
+    if (slots < 0) return fail(NNC_HIP_EDEVICE, name, "hipFuncSetAttribute failed");
     g.tiles_m = (int)ceil_div(g.M, T::BM);
     g.tiles_n = (int)ceil_div(g.N, T::BN);
     if ((int64_t)g.tiles_m * g.tiles_n * batches >= (1 << 30))
@@ -324,8 +323,9 @@ static void launch_mfma(GemmArgs& g, int batches, const char* name) {
     const StreamK sk = plan_streamk(g.tiles_m * g.tiles_n * batches, (int)ceil_div(g.K, T::BK), slots,
                                     fixup_slices<T>());
     if (sk.G < 1) return;
-    g.ws = workspace((size_t)sk.G * 2 * T::BM * T::BN * sizeof(float));
-    if (!g.ws) return fail(NNC_HIP_ENOMEM, name, "no workspace for stream-K partials");
+    const size_t ws_bytes = (size_t)sk.G * 2 * T::BM * T::BN * sizeof(float);
+    g.ws = workspace(ws_bytes);
+    if (!g.ws) return partials_fail(name, ws_bytes);
     static const char* kinds[4] = {"k4", "k1", "x4", "x1"};
     char kname[64];
     snprintf(kname, sizeof kname, "gemm_mfma_%dx%d_%s%s", T::BM, T::BN, kinds[AK], kinds[BKIND]);
@@ -402,7 +402,7 @@ static void gemm_run(const GemmProblem& p, const char* name) {
         const bool vec = aligned16(p.B) && p.ldb % 4 == 0 && p.N % 4 == 0;
         const int cols_per_block = vec ? 1024 : 256;
         const int col_blocks = (int)ceil_div(p.N, cols_per_block);
-        int splits = (int)ceil_div(4 * ctx().cu_count, col_blocks);
+        int splits = (int)ceil_div(4 * cu_count(), col_blocks);
         const int max_by_k = (int)ceil_div(p.K, 16);
         if (splits > max_by_k) splits = max_by_k;
         if (splits < 1) splits = 1;
@@ -445,7 +445,7 @@ static void gemm_run(const GemmProblem& p, const char* name) {
     // a multiple of 4)
     const int akind = p.a_kc ? ((a_al && p.K % 4 == 0) ? kKC4 : kKC) : ((a_al && p.M % 4 == 0) ? kXC4 : kXC);
     const int bkind = p.b_kc ? ((b_al && p.K % 4 == 0) ? kKC4 : kKC) : ((b_al && p.N % 4 == 0) ? kXC4 : kXC);
-    const bool big = (int64_t)p.M * p.N * p.batches >= (int64_t)128 * 128 * 2 * ctx().cu_count / 4 &&
+    const bool big = (int64_t)p.M * p.N * p.batches >= (int64_t)128 * 128 * 2 * cu_count() / 4 &&
                      p.M >= 128 && p.N >= 128;
     if (big && (akind == kKC4 || akind == kXC4) && (bkind == kKC4 || bkind == kXC4)) {
         if (akind == kKC4 && bkind == kKC4) return launch_mfma<GemmT128, kKC4, kKC4>(g, p.batches, name);

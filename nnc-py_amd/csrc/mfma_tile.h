@@ -455,7 +455,7 @@ static int resident_groups(K kernel, size_t lds_bytes, int threads = 256) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds_bytes) != hipSuccess ||
         per_cu < 1)
         per_cu = 1;
-    return per_cu * ctx().cu_count;
+    return per_cu * cu_count();
 }
 
 // Partial-tile slots in the workspace: two per workgroup (the segment where

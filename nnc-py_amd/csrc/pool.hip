@@ -300,7 +300,7 @@ static void pool_entry(const char* name, Tensor* in, Tensor* out, int kh, int kw
     }
     if (hw <= 16384 && hw > 0 && a.Ho > 0 && a.Wo > 0 && nc > 0) {
         // whole plane in LDS (at most 64 KB): the input is read once
-        const int64_t cap = (int64_t)ctx().cu_count * 8;
+        const int64_t cap = (int64_t)cu_count() * 8;
         const unsigned grid = (unsigned)(nc < cap ? nc : cap);
         launch(name, pool2d_lds_k<MAX>, dim3(grid), dim3(256), (size_t)hw * sizeof(float), a);
         return;

@@ -3,8 +3,10 @@
 //
 // The reference runtime owns no state: generated tensors.c places tensors in
 // a static host pool (codegen/x86_emitters/tensors.py:589-600). Here the pool
-// becomes one hipMalloc'd arena and this file owns the device, the stream and
-// a grow-only workspace for split-K partials.
+// becomes one hipMalloc'd arena and this file owns the device and, per
+// calling host thread, a pair of streams with grow-only scratch for split-K
+// partials (the reference's O3 runtime calls the ops from four pthreads,
+// codegen/x86_emitters/model_source.py:609-674).
 #include <stdarg.h>
 #include <string.h>
 
@@ -16,16 +18,29 @@
 
 namespace nnc {
 
-static Context g_ctx;
+static Device g_dev;
 static std::atomic<int> g_last_error{0};
+static std::mutex g_err_mutex;
 static char g_last_msg[512] = "";
 
-Context& ctx() { return g_ctx; }
+// Calling-thread states: created on a thread's first call, released for
+// reuse when the thread exits, freed by nnc_hip_shutdown. A state found
+// through t_state is current only while t_gen equals g_gen (shutdown and a
+// new init start a new generation).
+static std::mutex g_state_mutex;
+static std::vector<ThreadState*> g_states;
+static std::atomic<int> g_gen{0};
+static thread_local ThreadState* t_state = nullptr;
+static thread_local int t_gen = -1;
 
-static bool sync_all(const char* who) {
+Device& dev() { return g_dev; }
+static int last_code() { return g_last_error.load(); }
+ThreadState& ts() { return *t_state; }
+
+static bool sync_thread(const char* who) {
+    ThreadState& t = ts();
     for (int k = 0; k < kStreams; ++k)
-        if (g_ctx.streams[k] && !hip_ok(hipStreamSynchronize(g_ctx.streams[k]), who, "hipStreamSynchronize"))
-            return false;
+        if (t.streams[k] && !hip_ok(hipStreamSynchronize(t.streams[k]), who, "hipStreamSynchronize")) return false;
     return true;
 }
 
@@ -35,6 +50,7 @@ void fail(int code, const char* who, const char* fmt, ...) {
     va_start(ap, fmt);
     vsnprintf(body, sizeof body, fmt, ap);
     va_end(ap);
+    std::lock_guard<std::mutex> lock(g_err_mutex);
     snprintf(g_last_msg, sizeof g_last_msg, "%s: %s", who, body);
     g_last_error.store(code);
     fprintf(stderr, "%s\n", g_last_msg);
@@ -47,85 +63,209 @@ bool hip_ok(hipError_t e, const char* who, const char* what) {
     return false;
 }
 
-bool ready(const char* who) {
-    if (g_ctx.stream) return true;
-    fail(NNC_HIP_ESTATE, who, "nnc_hip_init() has not been called");
-    return false;
-}
-
 // Default workspace: stream-K partials of a full persistent grid (2 slots of
 // 128x128 floats for 512 workgroups = 64 MiB) with room; grows outside capture.
 static const size_t kDefaultWorkspace = 128u << 20;
+static const size_t kDefaultCounters = 1u << 16;
 
 // Scratch buffers replaced by larger ones stay allocated until shutdown: a
 // hipGraph captured earlier still holds their addresses.
+static std::mutex g_retired_mutex;
 static std::vector<void*> g_retired;
 static void retire(void* p) {
-    if (p) g_retired.push_back(p);
+    if (!p) return;
+    std::lock_guard<std::mutex> lock(g_retired_mutex);
+    g_retired.push_back(p);
+}
+
+static void free_state(ThreadState* t) {
+    for (int k = 0; k < kStreams; ++k)
+        if (t->streams[k]) (void)hipStreamSynchronize(t->streams[k]);
+    if (t->graph_exec) (void)hipGraphExecDestroy(t->graph_exec);
+    if (t->graph) (void)hipGraphDestroy(t->graph);
+    for (int k = 0; k < kStreams; ++k) {
+        if (t->workspace[k]) (void)hipFree(t->workspace[k]);
+        if (t->counters[k]) (void)hipFree(t->counters[k]);
+        if (t->repack[k]) (void)hipFree(t->repack[k]);
+    }
+    if (t->fork_ev) (void)hipEventDestroy(t->fork_ev);
+    if (t->join_ev) (void)hipEventDestroy(t->join_ev);
+    for (int k = 0; k < kStreams; ++k)
+        if (t->streams[k]) (void)hipStreamDestroy(t->streams[k]);
+    delete t;
+}
+
+// Hands the calling thread's state back for reuse when the thread exits
+// (work it queued stays ordered on the state's streams).
+struct ThreadRelease {
+    ~ThreadRelease() {
+        if (!t_state || t_gen != g_gen.load()) return;
+        std::lock_guard<std::mutex> lock(g_state_mutex);
+        if (t_gen == g_gen.load()) t_state->in_use = false;
+        t_state = nullptr;
+    }
+};
+static ThreadRelease& thread_release() {
+    static thread_local ThreadRelease r;
+    return r;
+}
+
+// Streams (default priority: streams of different priorities are not used
+// anywhere in this library), fork/join events and the default scratch of a
+// new thread state.
+static ThreadState* new_state(const char* who) {
+    ThreadState* t = new ThreadState();
+    bool ok = true;
+    for (int k = 0; ok && k < kStreams; ++k)
+        ok = hip_ok(hipStreamCreateWithFlags(&t->streams[k], hipStreamNonBlocking), who, "hipStreamCreate");
+    ok = ok && hip_ok(hipEventCreateWithFlags(&t->fork_ev, hipEventDisableTiming), who, "hipEventCreate") &&
+         hip_ok(hipEventCreateWithFlags(&t->join_ev, hipEventDisableTiming), who, "hipEventCreate");
+    if (!ok) {
+        free_state(t);
+        return nullptr;
+    }
+    ThreadState* saved = t_state;
+    const int saved_gen = t_gen;
+    t_state = t;  // workspace()/tile_counters() act on the current thread's state
+    t_gen = g_gen.load();
+    for (int k = 0; ok && k < kStreams; ++k) {
+        t->cur = k;
+        ok = workspace(kDefaultWorkspace) && tile_counters(kDefaultCounters);
+    }
+    t->cur = 0;
+    t_state = saved;
+    t_gen = saved_gen;
+    if (!ok) {
+        free_state(t);
+        return nullptr;
+    }
+    return t;
+}
+
+// Gives the calling thread a state: a released one if any, else a new one.
+static bool attach_thread(const char* who) {
+    // HIP's current device is per host thread
+    if (!hip_ok(hipSetDevice(g_dev.device), who, "hipSetDevice")) return false;
+    ThreadState* t = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_state_mutex);
+        for (ThreadState* s : g_states)
+            if (!s->in_use) {
+                t = s;
+                break;
+            }
+        if (t) t->in_use = true;
+    }
+    if (!t) {
+        t = new_state(who);
+        if (!t) return false;
+        t->in_use = true;
+        std::lock_guard<std::mutex> lock(g_state_mutex);
+        g_states.push_back(t);
+    }
+    t->cur = 0;
+    t->fixed = nullptr;
+    t_state = t;
+    t_gen = g_gen.load();
+    (void)thread_release();
+    return true;
+}
+
+bool ready(const char* who) {
+    if (t_state && t_gen == g_gen.load()) return true;
+    if (g_dev.device < 0) {
+        fail(NNC_HIP_ESTATE, who, "nnc_hip_init() has not been called");
+        return false;
+    }
+    return attach_thread(who);
+}
+
+void partials_fail(const char* who, size_t bytes) {
+    const FixedScratch* f = ts().fixed;
+    if (f)
+        return fail(NNC_HIP_EUNSUPP, who, "needs %zu bytes of stream-K scratch, more than the %zu-byte static buffer",
+                    bytes, f->ws_bytes);
+    fail(NNC_HIP_ENOMEM, who, "no workspace for %zu bytes of stream-K partials", bytes);
 }
 
 float* workspace(size_t bytes) {
-    Context& c = g_ctx;
-    const int k = c.cur;
-    if (bytes <= c.workspace_bytes[k]) return c.workspace[k];
-    if (c.capturing) return nullptr;
-    if (!hip_ok(hipStreamSynchronize(c.stream), "workspace", "hipStreamSynchronize")) return nullptr;
-    retire(c.workspace[k]);
-    c.workspace[k] = nullptr;
-    c.workspace_bytes[k] = 0;
+    ThreadState& t = ts();
+    if (t.fixed) return bytes <= t.fixed->ws_bytes ? t.fixed->ws : nullptr;
+    const int k = t.cur;
+    if (bytes <= t.workspace_bytes[k]) return t.workspace[k];
+    if (t.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(t.stream()), "workspace", "hipStreamSynchronize")) return nullptr;
+    retire(t.workspace[k]);
+    t.workspace[k] = nullptr;
+    t.workspace_bytes[k] = 0;
     size_t want = bytes < kDefaultWorkspace ? kDefaultWorkspace : bytes;
     void* p = nullptr;
     if (!hip_ok(hipMalloc(&p, want), "workspace", "hipMalloc")) return nullptr;
-    c.workspace[k] = static_cast<float*>(p);
-    c.workspace_bytes[k] = want;
-    return c.workspace[k];
+    t.workspace[k] = static_cast<float*>(p);
+    t.workspace_bytes[k] = want;
+    return t.workspace[k];
 }
 
-size_t workspace_capacity() { return g_ctx.workspace_bytes[g_ctx.cur]; }
+size_t workspace_capacity() {
+    ThreadState& t = ts();
+    return t.fixed ? t.fixed->ws_bytes : t.workspace_bytes[t.cur];
+}
 
 float* repack_buffer(size_t bytes) {
-    Context& c = g_ctx;
-    const int k = c.cur;
-    if (bytes <= c.repack_bytes[k]) return c.repack[k];
-    if (c.capturing) return nullptr;
-    if (!hip_ok(hipStreamSynchronize(c.stream), "repack_buffer", "hipStreamSynchronize")) return nullptr;
-    retire(c.repack[k]);
-    c.repack[k] = nullptr;
-    c.repack_bytes[k] = 0;
+    ThreadState& t = ts();
+    if (t.fixed) return nullptr;
+    const int k = t.cur;
+    if (bytes <= t.repack_bytes[k]) return t.repack[k];
+    if (t.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(t.stream()), "repack_buffer", "hipStreamSynchronize")) return nullptr;
+    retire(t.repack[k]);
+    t.repack[k] = nullptr;
+    t.repack_bytes[k] = 0;
     const size_t want = bytes < (16u << 20) ? (16u << 20) : bytes;
     void* p = nullptr;
     if (!hip_ok(hipMalloc(&p, want), "repack_buffer", "hipMalloc")) return nullptr;
-    c.repack[k] = static_cast<float*>(p);
-    c.repack_bytes[k] = want;
-    return c.repack[k];
+    t.repack[k] = static_cast<float*>(p);
+    t.repack_bytes[k] = want;
+    return t.repack[k];
 }
 
-static const size_t kDefaultCounters = 1u << 16;
+__global__ void __launch_bounds__(256) zero_ints_k(int* p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
 
 int* tile_counters(size_t n) {
-    Context& c = g_ctx;
-    const int k = c.cur;
-    if (n <= c.counters_n[k]) return c.counters[k];
-    if (c.capturing) return nullptr;
-    if (!hip_ok(hipStreamSynchronize(c.stream), "tile_counters", "hipStreamSynchronize")) return nullptr;
-    retire(c.counters[k]);
-    c.counters[k] = nullptr;
-    c.counters_n[k] = 0;
+    ThreadState& t = ts();
+    if (t.fixed) {
+        // fixed scratch keeps whatever the last call on this device left:
+        // clear the counters this launch uses (a fill kernel, also under capture)
+        if (n > t.fixed->cnt_n) return nullptr;
+        launch("zero_tile_counters", zero_ints_k, dim3((unsigned)ceil_div((int64_t)n, 256)), dim3(256), 0,
+               t.fixed->cnt, (int64_t)n);
+        return t.fixed->cnt;
+    }
+    const int k = t.cur;
+    if (n <= t.counters_n[k]) return t.counters[k];
+    if (t.capturing) return nullptr;
+    if (!hip_ok(hipStreamSynchronize(t.stream()), "tile_counters", "hipStreamSynchronize")) return nullptr;
+    retire(t.counters[k]);
+    t.counters[k] = nullptr;
+    t.counters_n[k] = 0;
     const size_t want = n < kDefaultCounters ? kDefaultCounters : n;
     void* p = nullptr;
     if (!hip_ok(hipMalloc(&p, want * sizeof(int)), "tile_counters", "hipMalloc")) return nullptr;
-    if (!hip_ok(hipMemsetAsync(p, 0, want * sizeof(int), c.stream), "tile_counters", "hipMemsetAsync") ||
-        !hip_ok(hipStreamSynchronize(c.stream), "tile_counters", "hipStreamSynchronize")) {
+    if (!hip_ok(hipMemsetAsync(p, 0, want * sizeof(int), t.stream()), "tile_counters", "hipMemsetAsync") ||
+        !hip_ok(hipStreamSynchronize(t.stream()), "tile_counters", "hipStreamSynchronize")) {
         (void)hipFree(p);
         return nullptr;
     }
-    c.counters[k] = static_cast<int*>(p);
-    c.counters_n[k] = want;
-    return c.counters[k];
+    t.counters[k] = static_cast<int*>(p);
+    t.counters_n[k] = want;
+    return t.counters[k];
 }
 
 // ---------------------------------------------------------------------------
-// per-kernel timing
+// per-kernel timing (one table for the process, behind a mutex)
 // ---------------------------------------------------------------------------
 struct Pending {
     std::string name;
@@ -137,50 +277,62 @@ struct Stat {
     int64_t launches = 0;
     double ms = 0.0, flops = 0.0, bytes = 0.0;
 };
-static double g_next_flops = 0.0, g_next_bytes = 0.0;
-
-void set_work(double flops, double bytes) {
-    g_next_flops = flops;
-    g_next_bytes = bytes;
-}
+static std::atomic<bool> g_profiling{false};
+static std::mutex g_prof_mutex;
 static std::vector<Pending> g_pending;
 static std::vector<hipEvent_t> g_event_pool;
 static std::vector<Stat> g_stats;
 
+void set_work(double flops, double bytes) {
+    ThreadState& t = ts();
+    t.next_flops = flops;
+    t.next_bytes = bytes;
+}
+
 static hipEvent_t take_event() {
-    if (!g_event_pool.empty()) {
-        hipEvent_t e = g_event_pool.back();
-        g_event_pool.pop_back();
-        return e;
+    {
+        std::lock_guard<std::mutex> lock(g_prof_mutex);
+        if (!g_event_pool.empty()) {
+            hipEvent_t e = g_event_pool.back();
+            g_event_pool.pop_back();
+            return e;
+        }
     }
     hipEvent_t e = nullptr;
     (void)hipEventCreate(&e);
     return e;
 }
 
-TimedScope::TimedScope(const char* n) : name(n), flops(g_next_flops), bytes(g_next_bytes) {
-    g_next_flops = g_next_bytes = 0.0;
-    if (!g_ctx.profiling || g_ctx.capturing) return;
+TimedScope::TimedScope(const char* n) : name(n) {
+    ThreadState& t = ts();
+    flops = t.next_flops;
+    bytes = t.next_bytes;
+    t.next_flops = t.next_bytes = 0.0;
+    if (!g_profiling.load() || t.capturing) return;
     start = take_event();
     stop = take_event();
-    (void)hipEventRecord(start, g_ctx.stream);
+    (void)hipEventRecord(start, t.stream());
 }
 
 TimedScope::~TimedScope() {
     if (!start) return;
-    (void)hipEventRecord(stop, g_ctx.stream);
+    (void)hipEventRecord(stop, cur_stream());
+    std::lock_guard<std::mutex> lock(g_prof_mutex);
     g_pending.push_back({name, flops, bytes, start, stop});
 }
 
 static void resolve_pending() {
-    if (g_pending.empty()) return;
-    (void)sync_all("profile");
+    std::lock_guard<std::mutex> lock(g_prof_mutex);
     for (auto& p : g_pending) {
         float ms = 0.f;
+        (void)hipEventSynchronize(p.stop);
         (void)hipEventElapsedTime(&ms, p.start, p.stop);
         Stat* s = nullptr;
         for (auto& st : g_stats)
-            if (st.name == p.name) { s = &st; break; }
+            if (st.name == p.name) {
+                s = &st;
+                break;
+            }
         if (!s) {
             g_stats.push_back(Stat{p.name, 0, 0.0, 0.0, 0.0});
             s = &g_stats.back();
@@ -202,9 +354,9 @@ using namespace nnc;
 extern "C" {
 
 int nnc_hip_init(int device) {
-    Context& c = g_ctx;
-    if (c.stream && c.device == device) return NNC_HIP_OK;
-    if (c.stream) nnc_hip_shutdown();
+    if (g_dev.device == device && t_state && t_gen == g_gen.load()) return NNC_HIP_OK;
+    if (g_dev.device == device) return ready("nnc_hip_init") ? NNC_HIP_OK : last_code();
+    if (g_dev.device >= 0) nnc_hip_shutdown();
     int count = 0;
     if (!hip_ok(hipGetDeviceCount(&count), "nnc_hip_init", "hipGetDeviceCount"))
         return NNC_HIP_EDEVICE;
@@ -215,118 +367,104 @@ int nnc_hip_init(int device) {
     if (!hip_ok(hipSetDevice(device), "nnc_hip_init", "hipSetDevice")) return NNC_HIP_EDEVICE;
     hipDeviceProp_t prop;
     if (hip_ok(hipGetDeviceProperties(&prop, device), "nnc_hip_init", "hipGetDeviceProperties"))
-        c.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-    // default priority for every stream (streams of different priorities
-    // are not used anywhere in this library)
-    for (int k = 0; k < kStreams; ++k)
-        if (!hip_ok(hipStreamCreateWithFlags(&c.streams[k], hipStreamNonBlocking), "nnc_hip_init",
-                    "hipStreamCreate"))
-            return NNC_HIP_EDEVICE;
-    if (!hip_ok(hipEventCreateWithFlags(&c.fork_ev, hipEventDisableTiming), "nnc_hip_init", "hipEventCreate") ||
-        !hip_ok(hipEventCreateWithFlags(&c.join_ev, hipEventDisableTiming), "nnc_hip_init", "hipEventCreate"))
-        return NNC_HIP_EDEVICE;
-    c.cur = 0;
-    c.stream = c.streams[0];
-    c.device = device;
-    for (int k = 0; k < kStreams; ++k) {
-        c.cur = k;
-        c.stream = c.streams[k];
-        if (!workspace(kDefaultWorkspace)) return NNC_HIP_ENOMEM;
-        if (!tile_counters(kDefaultCounters)) return NNC_HIP_ENOMEM;
+        g_dev.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    g_dev.device = device;
+    if (!ready("nnc_hip_init")) {
+        const int code = last_code();
+        g_dev.device = -1;
+        return code;
     }
-    c.cur = 0;
-    c.stream = c.streams[0];
     return NNC_HIP_OK;
 }
 
 void nnc_hip_shutdown(void) {
-    Context& c = g_ctx;
-    if (!c.stream) return;
-    for (int k = 0; k < kStreams; ++k)
-        if (c.streams[k]) (void)hipStreamSynchronize(c.streams[k]);
-    nnc_hip_graph_destroy();
-    for (auto& p : g_pending) {
-        (void)hipEventDestroy(p.start);
-        (void)hipEventDestroy(p.stop);
+    if (g_dev.device < 0) return;
+    (void)hipDeviceSynchronize();
+    {
+        std::lock_guard<std::mutex> lock(g_state_mutex);
+        for (ThreadState* t : g_states) free_state(t);
+        g_states.clear();
+        g_gen.fetch_add(1);
+        t_state = nullptr;
+        t_gen = -1;
     }
-    g_pending.clear();
-    for (auto e : g_event_pool) (void)hipEventDestroy(e);
-    g_event_pool.clear();
-    if (c.arena) (void)hipFree(c.arena);
-    if (c.spill) (void)hipHostFree(c.spill);
-    for (int k = 0; k < kStreams; ++k) {
-        if (c.workspace[k]) (void)hipFree(c.workspace[k]);
-        if (c.counters[k]) (void)hipFree(c.counters[k]);
-        if (c.repack[k]) (void)hipFree(c.repack[k]);
+    {
+        std::lock_guard<std::mutex> lock(g_prof_mutex);
+        for (auto& p : g_pending) {
+            (void)hipEventDestroy(p.start);
+            (void)hipEventDestroy(p.stop);
+        }
+        g_pending.clear();
+        for (auto e : g_event_pool) (void)hipEventDestroy(e);
+        g_event_pool.clear();
     }
-    for (void* p : g_retired) (void)hipFree(p);
-    g_retired.clear();
-    if (c.fork_ev) (void)hipEventDestroy(c.fork_ev);
-    if (c.join_ev) (void)hipEventDestroy(c.join_ev);
-    for (int k = 0; k < kStreams; ++k)
-        if (c.streams[k]) (void)hipStreamDestroy(c.streams[k]);
-    g_ctx = Context{};
+    if (g_dev.arena) (void)hipFree(g_dev.arena);
+    if (g_dev.spill) (void)hipHostFree(g_dev.spill);
+    {
+        std::lock_guard<std::mutex> lock(g_retired_mutex);
+        for (void* p : g_retired) (void)hipFree(p);
+        g_retired.clear();
+    }
+    g_dev = Device{};
 }
 
 int nnc_hip_arena_reserve(size_t bytes) {
     if (!ready("nnc_hip_arena_reserve")) return NNC_HIP_ESTATE;
-    Context& c = g_ctx;
-    if (c.arena && bytes <= c.arena_bytes) return NNC_HIP_OK;
-    (void)sync_all("nnc_hip_arena_reserve");
-    if (c.arena) (void)hipFree(c.arena);
-    c.arena = nullptr;
-    c.arena_bytes = 0;
+    if (g_dev.arena && bytes <= g_dev.arena_bytes) return NNC_HIP_OK;
+    (void)hipDeviceSynchronize();
+    if (g_dev.arena) (void)hipFree(g_dev.arena);
+    g_dev.arena = nullptr;
+    g_dev.arena_bytes = 0;
     void* p = nullptr;
     if (!hip_ok(hipMalloc(&p, bytes ? bytes : 256), "nnc_hip_arena_reserve", "hipMalloc"))
         return NNC_HIP_ENOMEM;
-    c.arena = static_cast<char*>(p);
-    c.arena_bytes = bytes;
+    g_dev.arena = static_cast<char*>(p);
+    g_dev.arena_bytes = bytes;
     return NNC_HIP_OK;
 }
 
-void* nnc_hip_arena_base(void) { return g_ctx.arena; }
-size_t nnc_hip_arena_size(void) { return g_ctx.arena_bytes; }
+void* nnc_hip_arena_base(void) { return g_dev.arena; }
+size_t nnc_hip_arena_size(void) { return g_dev.arena_bytes; }
 
 int nnc_hip_bind(Tensor* t, size_t offset) {
     if (!t) {
         fail(NNC_HIP_EINVAL, "nnc_hip_bind", "NULL tensor");
         return NNC_HIP_EINVAL;
     }
-    if (!g_ctx.arena) {
+    if (!g_dev.arena) {
         fail(NNC_HIP_ESTATE, "nnc_hip_bind", "no arena reserved");
         return NNC_HIP_ESTATE;
     }
-    if ((offset & 15u) != 0 || offset + (size_t)t->nbytes > g_ctx.arena_bytes) {
+    if ((offset & 15u) != 0 || offset + (size_t)t->nbytes > g_dev.arena_bytes) {
         fail(NNC_HIP_EINVAL, "nnc_hip_bind", "offset %zu + %lld bytes outside arena of %zu (or misaligned)",
-             offset, (long long)t->nbytes, g_ctx.arena_bytes);
+             offset, (long long)t->nbytes, g_dev.arena_bytes);
         return NNC_HIP_EINVAL;
     }
-    t->data = g_ctx.arena + offset;
+    t->data = g_dev.arena + offset;
     return NNC_HIP_OK;
 }
 
 int nnc_hip_spill_reserve(size_t bytes) {
     const char* who = "nnc_hip_spill_reserve";
     if (!ready(who)) return NNC_HIP_ESTATE;
-    Context& c = g_ctx;
-    if (c.spill && bytes <= c.spill_bytes) return NNC_HIP_OK;
-    if (c.capturing) {
+    if (g_dev.spill && bytes <= g_dev.spill_bytes) return NNC_HIP_OK;
+    if (ts().capturing) {
         fail(NNC_HIP_ESTATE, who, "cannot allocate the spill pool during graph capture");
         return NNC_HIP_ESTATE;
     }
-    (void)sync_all(who);
-    if (c.spill) (void)hipHostFree(c.spill);
-    c.spill = nullptr;
-    c.spill_bytes = 0;
+    (void)hipDeviceSynchronize();
+    if (g_dev.spill) (void)hipHostFree(g_dev.spill);
+    g_dev.spill = nullptr;
+    g_dev.spill_bytes = 0;
     void* p = nullptr;
     if (!hip_ok(hipHostMalloc(&p, bytes ? bytes : 256, hipHostMallocDefault), who, "hipHostMalloc"))
         return NNC_HIP_ENOMEM;
-    c.spill = static_cast<char*>(p);
-    c.spill_bytes = bytes;
+    g_dev.spill = static_cast<char*>(p);
+    g_dev.spill_bytes = bytes;
     return NNC_HIP_OK;
 }
 
-void* nnc_hip_spill_base(void) { return g_ctx.spill; }
+void* nnc_hip_spill_base(void) { return g_dev.spill; }
 
 int nnc_hip_bind_spill(Tensor* t, size_t offset) {
     const char* who = "nnc_hip_bind_spill";
@@ -334,16 +472,16 @@ int nnc_hip_bind_spill(Tensor* t, size_t offset) {
         fail(NNC_HIP_EINVAL, who, "NULL tensor");
         return NNC_HIP_EINVAL;
     }
-    if (!g_ctx.spill) {
+    if (!g_dev.spill) {
         fail(NNC_HIP_ESTATE, who, "no spill pool reserved");
         return NNC_HIP_ESTATE;
     }
-    if ((offset & 15u) != 0 || offset + (size_t)t->nbytes > g_ctx.spill_bytes) {
+    if ((offset & 15u) != 0 || offset + (size_t)t->nbytes > g_dev.spill_bytes) {
         fail(NNC_HIP_EINVAL, who, "offset %zu + %lld bytes outside the spill pool of %zu (or misaligned)", offset,
-             (long long)t->nbytes, g_ctx.spill_bytes);
+             (long long)t->nbytes, g_dev.spill_bytes);
         return NNC_HIP_EINVAL;
     }
-    t->data = g_ctx.spill + offset;
+    t->data = g_dev.spill + offset;
     return NNC_HIP_OK;
 }
 
@@ -360,7 +498,7 @@ void nnc_hip_transfer(Tensor* src, Tensor* dst) {
     if (src->nbytes <= 0 || src->data == dst->data) return;
     set_work(0.0, (double)src->nbytes);
     TimedScope scope(who);
-    hip_ok(hipMemcpyAsync(dst->data, src->data, (size_t)src->nbytes, hipMemcpyDefault, g_ctx.stream), who,
+    hip_ok(hipMemcpyAsync(dst->data, src->data, (size_t)src->nbytes, hipMemcpyDefault, cur_stream()), who,
            "hipMemcpyAsync");
 }
 
@@ -371,9 +509,11 @@ void* nnc_hip_malloc(size_t bytes) {
     return p;
 }
 
+// Freeing waits for the whole device: any thread's queued work may still
+// read the buffer.
 void nnc_hip_free(void* ptr) {
-    if (!ptr || !g_ctx.stream) return;
-    (void)sync_all("nnc_hip_free");
+    if (!ptr || g_dev.device < 0) return;
+    (void)hipDeviceSynchronize();
     (void)hipFree(ptr);
 }
 
@@ -387,31 +527,29 @@ void* nnc_hip_host_malloc(size_t bytes) {
 }
 
 void nnc_hip_host_free(void* ptr) {
-    if (!ptr || !g_ctx.stream) return;
-    (void)sync_all("nnc_hip_host_free");
+    if (!ptr || g_dev.device < 0) return;
+    (void)hipDeviceSynchronize();
     (void)hipHostFree(ptr);
 }
 
-int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
-    if (!ready("nnc_hip_memcpy_h2d")) return NNC_HIP_ESTATE;
+// Host copies wait for the calling thread's queued work, copy on its stream
+// 0 and wait for the copy.
+static int host_copy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, const char* who) {
+    if (!ready(who)) return NNC_HIP_ESTATE;
     if (!bytes) return NNC_HIP_OK;
-    if (!sync_all("nnc_hip_memcpy_h2d") ||
-        !hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx.streams[0]),
-                "nnc_hip_memcpy_h2d", "hipMemcpyAsync") ||
-        !hip_ok(hipStreamSynchronize(g_ctx.streams[0]), "nnc_hip_memcpy_h2d", "hipStreamSynchronize"))
+    ThreadState& t = ts();
+    if (!sync_thread(who) || !hip_ok(hipMemcpyAsync(dst, src, bytes, kind, t.streams[0]), who, "hipMemcpyAsync") ||
+        !hip_ok(hipStreamSynchronize(t.streams[0]), who, "hipStreamSynchronize"))
         return NNC_HIP_EDEVICE;
     return NNC_HIP_OK;
 }
 
+int nnc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    return host_copy(dst, src, bytes, hipMemcpyHostToDevice, "nnc_hip_memcpy_h2d");
+}
+
 int nnc_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
-    if (!ready("nnc_hip_memcpy_d2h")) return NNC_HIP_ESTATE;
-    if (!bytes) return NNC_HIP_OK;
-    if (!sync_all("nnc_hip_memcpy_d2h") ||
-        !hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.streams[0]),
-                "nnc_hip_memcpy_d2h", "hipMemcpyAsync") ||
-        !hip_ok(hipStreamSynchronize(g_ctx.streams[0]), "nnc_hip_memcpy_d2h", "hipStreamSynchronize"))
-        return NNC_HIP_EDEVICE;
-    return NNC_HIP_OK;
+    return host_copy(dst, src, bytes, hipMemcpyDeviceToHost, "nnc_hip_memcpy_d2h");
 }
 
 int nnc_hip_upload(Tensor* t, const void* host_src) {
@@ -432,19 +570,16 @@ int nnc_hip_download(const Tensor* t, void* host_dst) {
 
 int nnc_hip_sync(void) {
     if (!ready("nnc_hip_sync")) return NNC_HIP_ESTATE;
-    for (int k = 0; k < kStreams; ++k)
-        if (!hip_ok(hipStreamSynchronize(g_ctx.streams[k]), "nnc_hip_sync", "hipStreamSynchronize"))
-            return NNC_HIP_EDEVICE;
-    return NNC_HIP_OK;
+    return sync_thread("nnc_hip_sync") ? NNC_HIP_OK : NNC_HIP_EDEVICE;
 }
 
-void* nnc_hip_stream(void) { return g_ctx.streams[0]; }
+void* nnc_hip_stream(void) { return ready("nnc_hip_stream") ? ts().streams[0] : nullptr; }
 
 int nnc_hip_stream_fork(void) {
     if (!ready("nnc_hip_stream_fork")) return NNC_HIP_ESTATE;
-    Context& c = g_ctx;
-    if (!hip_ok(hipEventRecord(c.fork_ev, c.streams[0]), "nnc_hip_stream_fork", "hipEventRecord") ||
-        !hip_ok(hipStreamWaitEvent(c.streams[1], c.fork_ev, 0), "nnc_hip_stream_fork", "hipStreamWaitEvent"))
+    ThreadState& t = ts();
+    if (!hip_ok(hipEventRecord(t.fork_ev, t.streams[0]), "nnc_hip_stream_fork", "hipEventRecord") ||
+        !hip_ok(hipStreamWaitEvent(t.streams[1], t.fork_ev, 0), "nnc_hip_stream_fork", "hipStreamWaitEvent"))
         return NNC_HIP_EDEVICE;
     return NNC_HIP_OK;
 }
@@ -455,44 +590,56 @@ int nnc_hip_stream_select(int slot) {
         fail(NNC_HIP_EINVAL, "nnc_hip_stream_select", "stream %d out of range (0..%d)", slot, kStreams - 1);
         return NNC_HIP_EINVAL;
     }
-    g_ctx.cur = slot;
-    g_ctx.stream = g_ctx.streams[slot];
+    ts().cur = slot;
     return NNC_HIP_OK;
 }
 
 int nnc_hip_stream_join(void) {
     if (!ready("nnc_hip_stream_join")) return NNC_HIP_ESTATE;
-    Context& c = g_ctx;
-    if (!hip_ok(hipEventRecord(c.join_ev, c.streams[1]), "nnc_hip_stream_join", "hipEventRecord") ||
-        !hip_ok(hipStreamWaitEvent(c.streams[0], c.join_ev, 0), "nnc_hip_stream_join", "hipStreamWaitEvent"))
+    ThreadState& t = ts();
+    if (!hip_ok(hipEventRecord(t.join_ev, t.streams[1]), "nnc_hip_stream_join", "hipEventRecord") ||
+        !hip_ok(hipStreamWaitEvent(t.streams[0], t.join_ev, 0), "nnc_hip_stream_join", "hipStreamWaitEvent"))
         return NNC_HIP_EDEVICE;
     return NNC_HIP_OK;
 }
 
 int nnc_hip_last_error(void) { return g_last_error.load(); }
-const char* nnc_hip_last_error_message(void) { return g_last_msg; }
+
+// A copy per calling thread, so another thread's failure cannot rewrite the
+// text while the caller reads it.
+const char* nnc_hip_last_error_message(void) {
+    static thread_local char copy[512];
+    std::lock_guard<std::mutex> lock(g_err_mutex);
+    memcpy(copy, g_last_msg, sizeof copy);
+    return copy;
+}
+
 void nnc_hip_clear_error(void) {
+    std::lock_guard<std::mutex> lock(g_err_mutex);
     g_last_error.store(0);
     g_last_msg[0] = '\0';
 }
 
 void nnc_hip_profile_enable(int on) {
     if (!on) resolve_pending();
-    g_ctx.profiling = on != 0;
+    g_profiling.store(on != 0);
 }
 
 void nnc_hip_profile_reset(void) {
     resolve_pending();
+    std::lock_guard<std::mutex> lock(g_prof_mutex);
     g_stats.clear();
 }
 
 int nnc_hip_profile_count(void) {
     resolve_pending();
+    std::lock_guard<std::mutex> lock(g_prof_mutex);
     return (int)g_stats.size();
 }
 
 int nnc_hip_profile_entry(int i, char* name, int cap, int64_t* launches, double* total_ms) {
     resolve_pending();
+    std::lock_guard<std::mutex> lock(g_prof_mutex);
     if (i < 0 || i >= (int)g_stats.size()) return NNC_HIP_EINVAL;
     if (name && cap > 0) {
         strncpy(name, g_stats[i].name.c_str(), (size_t)cap - 1);
@@ -505,6 +652,7 @@ int nnc_hip_profile_entry(int i, char* name, int cap, int64_t* launches, double*
 
 int nnc_hip_profile_work(int i, double* flops, double* bytes) {
     resolve_pending();
+    std::lock_guard<std::mutex> lock(g_prof_mutex);
     if (i < 0 || i >= (int)g_stats.size()) return NNC_HIP_EINVAL;
     if (flops) *flops = g_stats[i].flops;
     if (bytes) *bytes = g_stats[i].bytes;
@@ -514,7 +662,7 @@ int nnc_hip_profile_work(int i, double* flops, double* bytes) {
 int nnc_hip_debug_dump(const Tensor* t, const char* name, int node_idx, void* file) {
     const char* fn = "nnc_hip_debug_dump";
     if (!ready(fn)) return NNC_HIP_ESTATE;
-    if (g_ctx.capturing) {
+    if (ts().capturing) {
         fail(NNC_HIP_ESTATE, fn, "cannot dump while a graph is being captured");
         return NNC_HIP_ESTATE;
     }
@@ -557,35 +705,38 @@ int nnc_hip_debug_dump(const Tensor* t, const char* name, int node_idx, void* fi
     return ferror(f) ? NNC_HIP_EINVAL : NNC_HIP_OK;
 }
 
+// Capture records the calling thread's stream 0 (and its side stream once
+// forked); other threads keep running eagerly on their own streams.
 int nnc_hip_graph_begin(void) {
     if (!ready("nnc_hip_graph_begin")) return NNC_HIP_ESTATE;
     nnc_hip_graph_destroy();
     resolve_pending();
-    if (g_ctx.cur != 0) {
-        fail(NNC_HIP_ESTATE, "nnc_hip_graph_begin", "capture starts on stream 0 (stream %d selected)", g_ctx.cur);
+    ThreadState& t = ts();
+    if (t.cur != 0) {
+        fail(NNC_HIP_ESTATE, "nnc_hip_graph_begin", "capture starts on stream 0 (stream %d selected)", t.cur);
         return NNC_HIP_ESTATE;
     }
-    if (!hip_ok(hipStreamBeginCapture(g_ctx.streams[0], hipStreamCaptureModeRelaxed),
-                "nnc_hip_graph_begin", "hipStreamBeginCapture"))
+    if (!hip_ok(hipStreamBeginCapture(t.streams[0], hipStreamCaptureModeRelaxed), "nnc_hip_graph_begin",
+                "hipStreamBeginCapture"))
         return NNC_HIP_EDEVICE;
-    g_ctx.capturing = true;
+    t.capturing = true;
     return NNC_HIP_OK;
 }
 
 int nnc_hip_graph_end(void) {
     if (!ready("nnc_hip_graph_end")) return NNC_HIP_ESTATE;
-    if (!g_ctx.capturing) {
+    ThreadState& t = ts();
+    if (!t.capturing) {
         fail(NNC_HIP_ESTATE, "nnc_hip_graph_end", "no capture in progress");
         return NNC_HIP_ESTATE;
     }
-    g_ctx.capturing = false;
+    t.capturing = false;
     hipGraph_t g = nullptr;
-    g_ctx.cur = 0;
-    g_ctx.stream = g_ctx.streams[0];
-    if (!hip_ok(hipStreamEndCapture(g_ctx.streams[0], &g), "nnc_hip_graph_end", "hipStreamEndCapture"))
+    t.cur = 0;
+    if (!hip_ok(hipStreamEndCapture(t.streams[0], &g), "nnc_hip_graph_end", "hipStreamEndCapture"))
         return NNC_HIP_EDEVICE;
-    g_ctx.graph = g;
-    if (!hip_ok(hipGraphInstantiate(&g_ctx.graph_exec, g, nullptr, nullptr, 0), "nnc_hip_graph_end",
+    t.graph = g;
+    if (!hip_ok(hipGraphInstantiate(&t.graph_exec, g, nullptr, nullptr, 0), "nnc_hip_graph_end",
                 "hipGraphInstantiate"))
         return NNC_HIP_EDEVICE;
     return NNC_HIP_OK;
@@ -593,22 +744,24 @@ int nnc_hip_graph_end(void) {
 
 int nnc_hip_graph_launch(void) {
     if (!ready("nnc_hip_graph_launch")) return NNC_HIP_ESTATE;
-    if (!g_ctx.graph_exec) {
+    ThreadState& t = ts();
+    if (!t.graph_exec) {
         fail(NNC_HIP_ESTATE, "nnc_hip_graph_launch", "no captured graph");
         return NNC_HIP_ESTATE;
     }
     TimedScope scope("graph");
-    return hip_ok(hipGraphLaunch(g_ctx.graph_exec, g_ctx.streams[0]), "nnc_hip_graph_launch",
-                  "hipGraphLaunch")
+    return hip_ok(hipGraphLaunch(t.graph_exec, t.streams[0]), "nnc_hip_graph_launch", "hipGraphLaunch")
                ? NNC_HIP_OK
                : NNC_HIP_EDEVICE;
 }
 
 void nnc_hip_graph_destroy(void) {
-    if (g_ctx.graph_exec) (void)hipGraphExecDestroy(g_ctx.graph_exec);
-    if (g_ctx.graph) (void)hipGraphDestroy(g_ctx.graph);
-    g_ctx.graph_exec = nullptr;
-    g_ctx.graph = nullptr;
+    if (!t_state || t_gen != g_gen.load()) return;
+    ThreadState& t = ts();
+    if (t.graph_exec) (void)hipGraphExecDestroy(t.graph_exec);
+    if (t.graph) (void)hipGraphDestroy(t.graph);
+    t.graph_exec = nullptr;
+    t.graph = nullptr;
 }
 
 }  // extern "C"

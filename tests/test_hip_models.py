@@ -228,3 +228,56 @@ def test_self_residual_block_matches_oracle(hip, oracle_lib):
     want = host.get(out)
     bad = caserun.fp_violations(got, want, 1e-4, 1e-3)
     assert bad.size == 0, f"{bad.size} of {want.size} outside the bar"
+
+
+def test_concurrent_host_threads_match_serial(hip):
+    """Four host threads, each running its own ResNet-18 batch-1 program
+    (O3, its own arena and input) three times while the others run: every
+    output equals that program's serial result bit for bit. Each thread gets
+    its own library streams and stream-K scratch on its first call, so the
+    concurrent calls share nothing but the kernels (the reference's O3
+    runtime calls the ops from four pthreads). Threads are started anew per
+    repetition, so released per-thread states are reused too."""
+    import threading
+    from nnc_py_amd import runtime
+    from nnc_py_amd.compiler import Executor, build_program, zoo
+    n = 4
+    rng = np.random.default_rng(11)
+    exes, want = [], []
+    for i in range(n):
+        ex = Executor(build_program(zoo.resnet18(batch=1, seed=1), opt_level=3), device=True)
+        ex.set_input("input", rng.standard_normal((1, 3, 224, 224)).astype(np.float32))
+        ex.run()
+        want.append(ex.get("output"))
+        exes.append(ex)
+    assert not caserun.same_bits(want[0], want[1])  # different inputs, different logits
+    failures: list[str] = []
+    stop = threading.Event()
+
+    def worker(i: int, rep: int) -> None:
+        try:
+            if stop.is_set():
+                return
+            for _ in range(4):
+                exes[i].run()
+            runtime.sync()  # this thread's streams
+            got = exes[i]._read("output")
+            if runtime.last_error()[0] != 0:
+                raise RuntimeError(runtime.last_error()[1])
+            if not caserun.same_bits(got, want[i]):
+                raise AssertionError(f"thread {i}, repetition {rep}: output differs from the serial run")
+        except Exception as e:  # noqa: BLE001 - reported by the main thread
+            failures.append(f"{type(e).__name__}: {e}")
+            stop.set()
+
+    for rep in range(3):
+        print(f"concurrent threads: repetition {rep}", flush=True)
+        threads = [threading.Thread(target=worker, args=(i, rep)) for i in range(n)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=120)
+        assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+        assert not failures, failures[0]
+    for ex in exes:
+        ex.close()
