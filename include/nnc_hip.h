@@ -202,6 +202,20 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
 void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
                        int ph, int pw, int psh, int psw, int act);
 
+/* nnc_hip_conv_packed_noalloc: nnc_hip_conv_packed for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference ABI.
+ * Same arguments, kernels and results (to the bit) as nnc_hip_conv_packed,
+ * but it allocates nothing: its stream-K partial tiles and tile counters
+ * live in a static device array of 64 MiB + 16384 counters that each GPU
+ * holds until the process ends; a shape needing more fails with
+ * NNC_HIP_EUNSUPP before any launch. Calls that overlap on one GPU (other
+ * threads, other streams) share that array and race. The calling thread must
+ * have its library state already (nnc_hip_init on that thread, or any
+ * earlier nnc_* call there): NNC_HIP_ESTATE otherwise. */
+void nnc_hip_conv_packed_noalloc(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw,
+                                 int sh, int sw, int ph, int pw, int act);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,8 @@ inline hipStream_t cur_stream() { return ts().stream(); }
 // otherwise makes sure the calling thread has its streams and scratch
 // (created on its first call, NNC_HIP_EDEVICE / ENOMEM if that fails).
 bool ready(const char* who);
+// Whether the calling thread already has its state (never creates it).
+bool thread_ready();
 
 // Record an error code + message (printed once to stderr, kept for
 // nnc_hip_last_error()).
@@ -98,8 +100,8 @@ size_t workspace_capacity();
 
 // At least `n` zeroed tile counters, or nullptr if they cannot be provided
 // (inside graph capture the buffer cannot grow; fixed scratch too small).
-// Kernels leave them zero; fixed scratch is cleared by a fill kernel on the
-// current stream first.
+// Kernels leave them zero; counters in fixed scratch are cleared by the
+// caller before the launch that uses them.
 int* tile_counters(size_t n);
 
 // At least `bytes` of scratch for a repacked weight tensor, or nullptr if it

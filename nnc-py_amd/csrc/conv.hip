@@ -1059,6 +1059,13 @@ static void launch_conv_t(ConvArgs& a, const char* entry) {
     if (sk.needs_fixup()) launch_conv_fixup<T>(a, sk);
 }
 
+// Clears tile counters held in fixed scratch, which keeps whatever the last
+// call on the device left there.
+__global__ void __launch_bounds__(256) zero_counters_k(int* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
 template <class T, class L>
 static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) {
     // the in-kernel finish only where it measured faster than the fixup
@@ -1093,6 +1100,9 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
     const int64_t per = sk.total() / sk.G;  // slices per workgroup range (>= 1)
     const bool in_kernel = FIN && sk.needs_fixup() && (sk.iters + per - 1) / per + 1 <= kMaxInKernelParts;
     a.cnt = in_kernel ? tile_counters((size_t)sk.sk_tiles) : nullptr;
+    if (a.cnt && ts().fixed)
+        launch("zero_tile_counters", zero_counters_k, dim3((unsigned)ceil_div(sk.sk_tiles, 256)), dim3(256), 0, a.cnt,
+               (int)sk.sk_tiles);
     set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
     launch(name, kernel, dim3(sk.G), dim3(T::THREADS), lds, a, sk);
     if (sk.needs_fixup() && !a.cnt) launch_conv_fixup<T>(a, sk);
@@ -1339,6 +1349,38 @@ static void conv_proj_run(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* o
     launch_conv_proj<ConvTSmall>(a, name);
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (nnc_hip_conv_packed_noalloc)
+// ---------------------------------------------------------------------------
+// Its stream-K partial tiles and tile counters live in `scratch`, a static
+// device array of which every GPU the library runs on holds its own copy
+// until the process ends: 64 MiB of partials (two 128x128 fp32 slots for each
+// of up to 512 resident workgroups, the largest persistent grid of any conv
+// tile on MI355X's 256 CUs), then 16384 tile counters. Host code never uses
+// the array's name as an address (on the host it is only a stand-in):
+// nnc_hip_init looks up each device's address once, with that device
+// current, and calls take it from there.
+static constexpr size_t kStaticPartialBytes = (size_t)64 << 20;
+static constexpr size_t kStaticCounters = 16384;
+static __device__ __align__(256) unsigned char scratch[kStaticPartialBytes + kStaticCounters * sizeof(int)];
+static constexpr int kMaxDevices = 64;
+static unsigned char* g_scratch_addr[kMaxDevices] = {};
+static std::mutex g_scratch_mutex;
+
+int conv_static_scratch_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) {
+        fail(NNC_HIP_EINVAL, "nnc_hip_init", "device %d beyond the %d the static scratch covers", device, kMaxDevices);
+        return NNC_HIP_EINVAL;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_addr[device]) return NNC_HIP_OK;
+    void* p = nullptr;
+    if (!hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "nnc_hip_init", "hipGetSymbolAddress(scratch)"))
+        return NNC_HIP_EDEVICE;
+    g_scratch_addr[device] = static_cast<unsigned char*>(p);
+    return NNC_HIP_OK;
+}
+
 }  // namespace nnc
 
 using namespace nnc;
@@ -1423,6 +1465,37 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
     if (res && (!res->data || !res->shape)) return fail(NNC_HIP_EINVAL, name, "NULL residual data");
     if (act < kActNone || act > kActSigmoid) return fail(NNC_HIP_EINVAL, name, "act must be 0, 1 or 2");
     conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, act, name, res, true);
+}
+
+// No reference counterpart: nnc_hip_conv_packed for callers that cannot
+// allocate (code under graph capture, serving loops). Same arguments, the
+// same kernels and stream-K plan (same results to the bit), but partials and
+// counters in the device's static scratch (64 MiB + 16384 counters) instead
+// of the grow-only workspace; shapes needing more fail with NNC_HIP_EUNSUPP
+// before anything is launched. The counters a launch uses are cleared by a
+// fill kernel just before it; calls are not timed in the profiling table. Calls that overlap on one device - from several threads or streams -
+// share the one array and race. The calling thread must already have its
+// library state (nnc_hip_init or any earlier call on that thread), which
+// this entry point never creates (NNC_HIP_ESTATE otherwise).
+void nnc_hip_conv_packed_noalloc(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,
+                                 int sw, int ph, int pw, int act) {
+    const char* name = "nnc_hip_conv_packed_noalloc";
+    if (!thread_ready()) return fail(NNC_HIP_ESTATE, name, "no library state on this thread: call nnc_hip_init first");
+    const int d = dev().device;
+    unsigned char* base = d >= 0 && d < kMaxDevices ? g_scratch_addr[d] : nullptr;
+    if (!base) return fail(NNC_HIP_ESTATE, name, "static scratch not set up on device %d", d);
+    if (!conv_check_packed(in, w, out, name)) return;
+    if (res && (!res->data || !res->shape)) return fail(NNC_HIP_EINVAL, name, "NULL residual data");
+    if (act < kActNone || act > kActSigmoid) return fail(NNC_HIP_EINVAL, name, "act must be 0, 1 or 2");
+    FixedScratch fs;
+    fs.ws = reinterpret_cast<float*>(base);
+    fs.ws_bytes = kStaticPartialBytes;
+    fs.cnt = reinterpret_cast<int*>(base + kStaticPartialBytes);
+    fs.cnt_n = kStaticCounters;
+    ThreadState& t = ts();
+    t.fixed = &fs;
+    conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, act, name, res, true);
+    t.fixed = nullptr;
 }
 
 }  // extern "C"

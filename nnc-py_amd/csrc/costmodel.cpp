@@ -495,6 +495,13 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
     (void)sh, (void)sw, (void)ph, (void)pw, (void)act;
     conv("nnc_hip_conv_packed", in, w, b, res, out, kh, kw, true);
 }
+// the allocation-free variant launches the same kernels (plus a counter fill
+// where the in-kernel finish runs, priced as free here)
+void nnc_hip_conv_packed_noalloc(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,
+                                 int sw, int ph, int pw, int act) {
+    (void)sh, (void)sw, (void)ph, (void)pw, (void)act;
+    conv("nnc_hip_conv_packed_noalloc", in, w, b, res, out, kh, kw, true);
+}
 
 // ---- GEMM ---------------------------------------------------------------------
 void nnc_matmul(Tensor* a, Tensor* b, Tensor* out) { matmul("nnc_matmul", a, b, nullptr, out); }

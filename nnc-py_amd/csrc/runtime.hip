@@ -35,6 +35,9 @@ static thread_local int t_gen = -1;
 
 Device& dev() { return g_dev; }
 static int last_code() { return g_last_error.load(); }
+// conv.hip: looks up the device address of its static scratch on the
+// current device (once per device)
+int conv_static_scratch_setup(int device);
 ThreadState& ts() { return *t_state; }
 
 static bool sync_thread(const char* who) {
@@ -171,6 +174,8 @@ static bool attach_thread(const char* who) {
     return true;
 }
 
+bool thread_ready() { return t_state && t_gen == g_gen.load(); }
+
 bool ready(const char* who) {
     if (t_state && t_gen == g_gen.load()) return true;
     if (g_dev.device < 0) {
@@ -229,21 +234,9 @@ float* repack_buffer(size_t bytes) {
     return t.repack[k];
 }
 
-__global__ void __launch_bounds__(256) zero_ints_k(int* p, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) p[i] = 0;
-}
-
 int* tile_counters(size_t n) {
     ThreadState& t = ts();
-    if (t.fixed) {
-        // fixed scratch keeps whatever the last call on this device left:
-        // clear the counters this launch uses (a fill kernel, also under capture)
-        if (n > t.fixed->cnt_n) return nullptr;
-        launch("zero_tile_counters", zero_ints_k, dim3((unsigned)ceil_div((int64_t)n, 256)), dim3(256), 0,
-               t.fixed->cnt, (int64_t)n);
-        return t.fixed->cnt;
-    }
+    if (t.fixed) return n <= t.fixed->cnt_n ? t.fixed->cnt : nullptr;
     const int k = t.cur;
     if (n <= t.counters_n[k]) return t.counters[k];
     if (t.capturing) return nullptr;
@@ -308,7 +301,8 @@ TimedScope::TimedScope(const char* n) : name(n) {
     flops = t.next_flops;
     bytes = t.next_bytes;
     t.next_flops = t.next_bytes = 0.0;
-    if (!g_profiling.load() || t.capturing) return;
+    // no events under capture, nor in an allocation-free call (creating one allocates)
+    if (!g_profiling.load() || t.capturing || t.fixed) return;
     start = take_event();
     stop = take_event();
     (void)hipEventRecord(start, t.stream());
@@ -368,6 +362,7 @@ int nnc_hip_init(int device) {
     hipDeviceProp_t prop;
     if (hip_ok(hipGetDeviceProperties(&prop, device), "nnc_hip_init", "hipGetDeviceProperties"))
         g_dev.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    if (conv_static_scratch_setup(device) != NNC_HIP_OK) return last_code();
     g_dev.device = device;
     if (!ready("nnc_hip_init")) {
         const int code = last_code();

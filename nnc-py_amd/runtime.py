@@ -68,6 +68,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_conv_packed": (abi.TARGET_SIGNATURES["nnc_hip_conv_packed"], None),
     "nnc_hip_transfer": (abi.TARGET_SIGNATURES["nnc_hip_transfer"], None),
     "nnc_hip_conv_proj": (abi.TARGET_SIGNATURES["nnc_hip_conv_proj"], None),
+    "nnc_hip_conv_packed_noalloc": (abi.TARGET_SIGNATURES["nnc_hip_conv_packed_noalloc"], None),
 }
 
 
