@@ -17,8 +17,8 @@ from collections.abc import Mapping
 from pathlib import Path
 from typing import Any
 
-from . import codegen
-from .executor import Program, build_program
+from .backend import CodeGenResult, CompileContext, Mi355xBackend
+from .executor import Program
 from .ir import Graph
 
 REPO_ROOT = Path(__file__).resolve().parents[2]
@@ -56,6 +56,7 @@ class Compiler:
         self.default_metadata = dict(metadata or {})
         self._check_target(target)
         self.last_program: Program | None = None
+        self.last_artifacts: CodeGenResult | None = None
 
     @staticmethod
     def _check_target(target: str) -> None:
@@ -66,6 +67,12 @@ class Compiler:
         if target == "x86":
             raise ValueError("target 'x86' is the reference nnc-py backend; this package provides 'mi355x'")
         raise ValueError(f"Unknown target: {target}")
+
+    def _create_backend(self, target: str) -> Mi355xBackend:
+        """The backend for `target` (compiler.py:266-285 of the reference,
+        whose _create_backend gains the same "mi355x" branch)."""
+        self._check_target(target)
+        return Mi355xBackend(debug_mode=self.debug_mode, repo_root=REPO_ROOT)
 
     def _load(self, model) -> Graph:
         if isinstance(model, Graph):
@@ -79,18 +86,33 @@ class Compiler:
     def compile(self, model, output_dir: str, entry_point: str = "nnc_run", max_memory: str | None = None,
                 memory_strategy: str | None = None, cost_model_cli_command=None,
                 metadata: Mapping[str, Any] | None = None) -> Program:
+        """Same stages as the reference's compile (compiler.py:128-264): load,
+        a CompileContext with entry_point / max_memory / memory_strategy in its
+        metadata, then the backend's generate(ctx) - here Mi355xBackend, which
+        also runs this target's passes - and the files written out."""
         graph = self._load(model)
         strategy = memory_strategy or self.memory_strategy
-        if strategy not in (None, "basic", "cost_aware"):
-            raise ValueError(f"unknown memory strategy {strategy!r} (basic, cost_aware)")
-        prog = build_program(graph, self.opt_level, strategy, parse_memory_size(max_memory))
+        md = dict(self.default_metadata)
+        md.update(dict(metadata or {}))
+        if cost_model_cli_command is not None:
+            md["cost_model_cli_command"] = cost_model_cli_command
+        md["entry_point"] = entry_point
+        if max_memory is not None:
+            md["max_memory"] = parse_memory_size(max_memory)
+        if strategy is not None:
+            md["memory_strategy"] = strategy
+        ctx = CompileContext(graph, self.target, self.opt_level, self.debug_mode, md)
+        backend = self._create_backend(self.target)
+        artifacts = backend.generate(ctx)
         out = Path(output_dir)
         out.mkdir(parents=True, exist_ok=True)
-        for art in codegen.generate(prog, entry_point, str(REPO_ROOT), debug_mode=self.debug_mode):
+        for art in artifacts.files:
             path = out / art.filename
             if art.file_type == "binary":
                 path.write_bytes(art.content)
             else:
                 path.write_text(art.content)
-        self.last_program = prog
-        return prog
+        artifacts.metadata.update({"entry_point": entry_point, "target": self.target, "opt_level": self.opt_level})
+        self.last_artifacts = artifacts
+        self.last_program = backend.last_program
+        return backend.last_program
