@@ -111,11 +111,28 @@ def kernel_table(ex, runtime, steps: int) -> list[dict]:
     return rows
 
 
-def cpu_baseline(pkg, iters: int) -> dict | None:
-    """ResNet-18 batch 1 through a CPU implementation of the same ABI: the
-    reference runtime (runtime/x86/ops.c compiled by oracle/Makefile into
-    oracle/_ref/) when present, else the oracle restatement; one thread."""
+def _cpu_rate(lib, batch: int, warmup: int, iters: int) -> float:
+    """Seconds per nnc_run() of the reference's own O3 call sequence for
+    ResNet-18 at `batch` on a CPU implementation of the ABI (the mi355x
+    target's fused and packed-weight entry points do not exist there)."""
     from nnc_py_amd.compiler import Executor, build_program, zoo
+    prog = build_program(zoo.resnet18(batch=batch, seed=1), opt_level=3, target_passes=False)
+    ex = Executor(prog, device=False, lib=lib)
+    ex.set_input("input", np.random.default_rng(0).standard_normal((batch, 3, 224, 224)).astype(np.float32))
+    for _ in range(warmup):
+        ex.run()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        ex.run()
+    return (time.perf_counter() - t0) / iters
+
+
+def cpu_baseline(pkg, iters_b1: int, iters_b32: int, batch: int) -> dict | None:
+    """ResNet-18 through a CPU implementation of the same ABI, one thread:
+    the reference runtime (runtime/x86/ops.c compiled by oracle/Makefile into
+    oracle/_ref/) when present, else the oracle restatement. `value` at the
+    benchmark's batch in the reference harness's quick mode (1 warmup + 3
+    timed runs, benchmarks/harness.py:17-18), batch 1 beside it."""
     from nnc_py_amd import abi
     ref = ROOT / "oracle" / "_ref" / "libref_ops.so"
     port = ROOT / "oracle" / "liboracle.so"
@@ -126,16 +143,11 @@ def cpu_baseline(pkg, iters: int) -> dict | None:
     else:
         return None
     lib = abi.bind(ctypes.CDLL(str(path)))
-    # the reference's own O3 call sequence (the mi355x target's fused and
-    # packed-weight entry points do not exist in the reference runtime)
-    prog = build_program(zoo.resnet18(batch=1, seed=1), opt_level=3, target_passes=False)
-    ex = Executor(prog, device=False, lib=lib)
-    ex.set_input("input", np.random.default_rng(0).standard_normal((1, 3, 224, 224)).astype(np.float32))
-    ex.run()  # warmup
-    t0 = time.perf_counter()
-    for _ in range(iters):
-        ex.run()
-    dt = (time.perf_counter() - t0) / iters
+    # the oracle's convolution uses OpenMP threads: pin it to one for a
+    # one-thread figure (the reference's ops.c is single-threaded)
+    os.environ["OMP_NUM_THREADS"] = "1"
+    dt1 = _cpu_rate(lib, 1, 1, iters_b1)
+    dtb = _cpu_rate(lib, batch, 1, iters_b32) if iters_b32 > 0 else None
     cpu = "unknown"
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -144,10 +156,16 @@ def cpu_baseline(pkg, iters: int) -> dict | None:
                 break
     except OSError:
         pass
-    return {"value": round(1.0 / dt, 4), "unit": "images/s", "cores": 1, "kind": kind,
-            "sample": (f"ResNet-18 fp32 batch 1, the reference's O3 call sequence, 1 warmup + {iters} timed "
-                       f"nnc_run() ({dt:.2f} s each), {path.relative_to(ROOT)} gcc -O2, 1 thread; "
-                       f"host {cpu}, nproc {os.cpu_count()}")}
+    where = f"{path.relative_to(ROOT)} gcc -O2, 1 thread; host {cpu}, nproc {os.cpu_count()}"
+    b1 = {"value": round(1.0 / dt1, 4), "unit": "images/s",
+          "sample": f"batch 1: 1 warmup + {iters_b1} timed nnc_run() ({dt1:.2f} s each)"}
+    if dtb is None:
+        return {"value": b1["value"], "unit": "images/s", "cores": 1, "kind": kind,
+                "sample": f"ResNet-18 fp32, the reference's O3 call sequence, {b1['sample']}, {where}"}
+    return {"value": round(batch / dtb, 4), "unit": "images/s", "cores": 1, "kind": kind,
+            "sample": (f"ResNet-18 fp32 batch {batch}, the reference's O3 call sequence, 1 warmup + {iters_b32} "
+                       f"timed nnc_run() ({dtb:.2f} s each), {where}"),
+            "b1": b1}
 
 
 COPY_PROBE_BYTES = 256 << 20
@@ -412,7 +430,9 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-graph", action="store_true", help="launch each nnc_* call instead of a hipGraph")
     ap.add_argument("--profile-steps", type=int, default=5)
-    ap.add_argument("--cpu-iters", type=int, default=25)
+    ap.add_argument("--cpu-iters", type=int, default=10, help="timed batch-1 runs of the CPU baseline")
+    ap.add_argument("--cpu-iters-batch", type=int, default=3,
+                    help="timed runs of the CPU baseline at the benchmark batch (0: batch 1 only)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--no-b1", action="store_true", help="measure batch 32 only (profiling runs)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
@@ -501,8 +521,9 @@ def main() -> int:
 
     cpu = None
     if not args.skip_cpu:
-        log(f"CPU baseline: ResNet-18 batch 1, {args.cpu_iters} timed runs")
-        cpu = cpu_baseline(pkg, args.cpu_iters)
+        log(f"CPU baseline: ResNet-18 batch 1 ({args.cpu_iters} timed runs) and batch {args.batch} "
+            f"({args.cpu_iters_batch} timed runs), one thread")
+        cpu = cpu_baseline(pkg, args.cpu_iters, args.cpu_iters_batch, args.batch)
 
     b = results[args.batch]
     line = {

@@ -202,6 +202,20 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
 void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
                        int ph, int pw, int psh, int psw, int act);
 
+/* nnc_hip_gap_gemm_nt: GlobalAveragePool -> Flatten -> Gemm(transB = 1) in
+ * one kernel, the pooled [N, C] tensor never leaving the workgroup:
+ *   out[n][o] = alpha * sum_c mean_hw(in[n][c]) * w[o][c] + beta * c
+ * with in [N][C][H][W], w [O][C], c [O] or [N][O] or NULL, out [N][O]. The
+ * means are nnc_avgpool2d's over the whole plane, bit for bit; the dot
+ * products are nnc_gemm_nt's exact float products summed in double in
+ * another fixed order (per-lane sums and a shuffle tree instead of one
+ * chain: the float result differs only where the double sums straddle a
+ * float rounding boundary). Needs C % 4 == 0, C <= 1024, C * (H*W + 2)
+ * floats <= 128 KB, at most 65535 images and 16-byte aligned in and w
+ * (NNC_HIP_EUNSUPP otherwise). Emitted by the mi355x target's O3 tile-streaming pass. No
+ * counterpart in the reference ABI. */
+void nnc_hip_gap_gemm_nt(Tensor* in, Tensor* w, Tensor* c, Tensor* out, float alpha, float beta);
+
 /* nnc_hip_conv_packed_noalloc: nnc_hip_conv_packed for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference ABI.

@@ -24,7 +24,7 @@ from .ir import Graph, Node
 from .lower import Call, lower
 from .passes import (SPILL_OPS, Branch, MemoryPlan, branch_calls, check_plan, eliminate_dead_code,
                      eliminate_identity, find_branches, fit_memory, fuse_matmul_bias, fuse_patterns, fuse_projection,
-                     fuse_residual, pack_conv_weights, plan_memory, prepack_lowering)
+                     fuse_residual, pack_conv_weights, plan_memory, prepack_lowering, stream_tiles)
 
 
 @dataclass
@@ -44,6 +44,10 @@ PACK_CONV_WEIGHTS = True
 # a residual block's 1x1 projection folded into its last 3x3 conv
 # (nnc_hip_conv_proj) at O3 (mi355x target).
 PROJECTION_FUSION = True
+# producer -> consumer tile streaming through a workgroup's on-chip memory
+# at O3 (mi355x target): GlobalAveragePool -> Flatten -> Gemm as
+# nnc_hip_gap_gemm_nt.
+STREAM_TILES = True
 # independent side branches (ResNet's downsample convolutions) on the second
 # library stream at O3 (mi355x target), while the main branch's convolutions
 # total at most BRANCH_MAX_FLOPS: two kernels overlap only while neither fills
@@ -81,6 +85,8 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
                 if PROJECTION_FUSION and RESIDUAL_FUSION and not use_branches:
                     fuse_projection(graph)
         prepack_lowering(graph)
+        if target_passes and STREAM_TILES:
+            stream_tiles(graph)
     order = graph.topological_sort()
     branches = find_branches(graph, order, BRANCH_MAX_FLOPS) if use_branches else []
     groups = [[b.side] + b.main for b in branches]

@@ -158,6 +158,10 @@ def lower_node(g: Graph, node: Node) -> Call:
         if node.metadata.get("lowering", {}).get("weight_pack") == "rhs_transposed_constant" and ta == 0 and tb == 1:
             return Call("nnc_gemm_nt", args, node.name)
         return Call("nnc_gemm", args + [("i", ta), ("i", tb)], node.name)
+    if op == "FusedGapGemm":  # GAP streamed into the classifier (include/nnc_hip.h)
+        return Call("nnc_hip_gap_gemm_nt", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0]),
+                                            ("f", float(node.attrs.get("alpha", 1.0))),
+                                            ("f", float(node.attrs.get("beta", 1.0)))], node.name)
     if op == "FusedMatMulRelu":
         return Call("nnc_matmul_relu", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0])], node.name)
     if op == "MaxPool":

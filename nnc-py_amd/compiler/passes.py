@@ -330,6 +330,92 @@ def prepack_lowering(g: Graph) -> None:
 
 
 # ---------------------------------------------------------------------------
+# tile streaming between ops (mi355x O3): the tiling half of the reference's
+# O3 pipeline, ScheduleAnalysis -> LayoutPlanning -> TiledLowering
+# (passes/base.py:113-124), re-targeted from x86 fast memory to a GPU
+# workgroup's on-chip memory
+# ---------------------------------------------------------------------------
+# The reference schedules ops whose working set fits a 1 MiB fast memory
+# (schedule_analysis.py:12) and streams their tiles through it
+# (tiled_lowering.py:44-759). On the MI355X the fast memory of a producer's
+# tile is the workgroup's LDS (128 KiB here, of the CU's 160 KiB) and its
+# registers: a producer -> consumer pair is streamed when the consumer needs
+# only what one workgroup of the fused kernel computes and that fits this
+# budget, and the intermediate tensor then never exists in HBM.
+LDS_BUDGET = 128 * 1024
+# The fused GAP -> Gemm kernel re-reads an image's planes for every group of
+# 16 classes and serialises its loads, means and dot products in one
+# workgroup, so it can only pay where the unfused pair is two launches of
+# little work. Measured on MI355X with ResNet-18's classifier (hipGraph
+# replay of the whole network, hipEvent kernel times): fused 16.4 / 17.4 /
+# 16.9 / 29.4 us at batch 1 / 2 / 4 / 8 against GAP + classifier 12.4 /
+# 21.9 / 23.6 / 21.8 us, whole steps 0.2704 vs 0.2628 ms at batch 1, equal
+# at 2 and 4, 0.598 vs 0.586 ms at 8. It is taken up to this batch: none by
+# default, the pass and the kernel stay for programs where it pays.
+GAP_GEMM_MAX_BATCH = 0
+
+# LDS of the fused GAP -> Gemm kernel (nnc_hip_gap_gemm_nt) per workgroup:
+# one image's planes and its C means (its rows of w are in registers)
+def gap_gemm_lds_bytes(channels: int, plane: int) -> int:
+    return 4 * (channels + channels * (plane + 1))
+
+
+def stream_tiles(g: Graph, lds_budget: int = LDS_BUDGET) -> int:
+    """GlobalAveragePool -> Flatten -> Gemm (transB = 1, constant w [O, C])
+    whose pooled and flattened tensors have no other reader becomes one
+    FusedGapGemm node (inputs: x, w, bias or ""; the Gemm's alpha/beta),
+    lowered to nnc_hip_gap_gemm_nt: each workgroup averages its images'
+    planes into LDS and feeds them straight to the dot products, so the
+    [N, C] pooled tensor is never written. Taken when the workgroup's
+    intermediate (an image's C means, its w blocks and partial sums) fits
+    `lds_budget`, at batches up to GAP_GEMM_MAX_BATCH. The decision and its
+    footprint are recorded in the node's metadata["tile_stream"]."""
+    fused = 0
+    for gap in list(g.nodes):
+        if gap.op_type != "GlobalAveragePool" or len(gap.inputs) != 1:
+            continue
+        x, pooled = gap.inputs[0], gap.outputs[0]
+        xs = g.tensors[x].shape
+        if len(xs) != 4 or pooled in g.outputs or g.tensors[x].dtype != "float32" or xs[0] > GAP_GEMM_MAX_BATCH:
+            continue
+        if xs[1] % 4 or xs[1] > 1024:
+            continue
+        users = g.consumers(pooled)
+        if len(users) != 1 or users[0].op_type != "Flatten" or int(users[0].attrs.get("axis", 1)) != 1:
+            continue
+        flat = users[0]
+        flat_out = flat.outputs[0]
+        gemms = g.consumers(flat_out)
+        if flat_out in g.outputs or len(gemms) != 1 or gemms[0].op_type != "Gemm":
+            continue
+        gm = gemms[0]
+        if gm.inputs[0] != flat_out or int(gm.attrs.get("transA", 0)) != 0 or int(gm.attrs.get("transB", 0)) != 1:
+            continue
+        w = g.tensors[gm.inputs[1]]
+        if not w.is_constant or len(w.shape) != 2 or w.shape[1] != xs[1]:
+            continue
+        need = gap_gemm_lds_bytes(int(xs[1]), int(xs[2]) * int(xs[3]))
+        if need > lds_budget:
+            continue
+        bias = gm.inputs[2] if len(gm.inputs) > 2 else ""
+        if bias and g.tensors[bias].numel not in (int(w.shape[0]), int(xs[0]) * int(w.shape[0])):
+            continue
+        gap.op_type = "FusedGapGemm"
+        gap.inputs = [x, gm.inputs[1], bias]
+        gap.outputs = list(gm.outputs)
+        gap.attrs = {"alpha": float(gm.attrs.get("alpha", 1.0)), "beta": float(gm.attrs.get("beta", 1.0))}
+        gap.metadata["fused_from"] = [gap.name, flat.name, gm.name]
+        gap.metadata["tile_stream"] = {"intermediate": pooled, "lds_bytes": need, "budget": lds_budget,
+                                       "hbm_bytes_saved": 2 * g.tensors[pooled].nbytes}
+        g.nodes.remove(flat)
+        g.nodes.remove(gm)
+        g.tensors.pop(pooled, None)
+        g.tensors.pop(flat_out, None)
+        fused += 1
+    return fused
+
+
+# ---------------------------------------------------------------------------
 # liveness and the arena plan
 # ---------------------------------------------------------------------------
 @dataclass

@@ -544,6 +544,20 @@ void nnc_avgpool2d(Tensor* in, Tensor* out, int kh, int kw, int sh, int sw, int 
     stream_kernel("nnc_avgpool2d", global ? "nnc_avgpool2d_global" : "nnc_avgpool2d", nbytes(in) + nbytes(out), 0.5);
 }
 
+// the global average pool streamed into the classifier: one launch whose
+// time is its bytes (input planes, w read by every image group) at a low
+// streaming efficiency, or its sequential per-lane dot products, whichever
+// is longer (about 2 us for 512 channels)
+void nnc_hip_gap_gemm_nt(Tensor* in, Tensor* w, Tensor* c, Tensor* out, float alpha, float beta) {
+    (void)alpha, (void)beta;
+    if (!in || !w || !out || !in->shape || !w->shape || in->ndim != 4 || w->ndim != 2) return;
+    const double groups = (double)ceil_div(in->shape[0], 4);
+    const double bytes = nbytes(in) + nbytes(w) * groups + nbytes(c) + nbytes(out);
+    const double dot_us = 4.0e-3 * (double)w->shape[1];
+    record("nnc_hip_gap_gemm_nt", "nnc_hip_gap_gemm_nt", kLaunchUs + fmax(bytes / (kHbm * 0.25) * 1e6, dot_us),
+           2.0 * (double)in->shape[0] * (double)w->shape[0] * (double)w->shape[1], bytes);
+}
+
 // ---- element-wise -----------------------------------------------------------------
 void nnc_add(Tensor* a, Tensor* b, Tensor* out) { binary("nnc_add", a, b, out); }
 void nnc_mul(Tensor* a, Tensor* b, Tensor* out) { binary("nnc_mul", a, b, out); }

@@ -310,6 +310,114 @@ static void pool_entry(const char* name, Tensor* in, Tensor* out, int kh, int kw
         launch(name, pool2d_k<MAX>, dim3((unsigned)ceil_div((int64_t)a.Ho * a.Wo, 256), gy), dim3(256), 0, a);
 }
 
+// ---------------------------------------------------------------------------
+// Global average pool streamed into the classifier GEMM (nnc_hip_gap_gemm_nt)
+// ---------------------------------------------------------------------------
+// out[n][o] = alpha * sum_c mean[n][c] * w[o][c] + beta * c_o, with mean the
+// global average pool of in[n] - the reference's nnc_avgpool2d over the whole
+// plane followed by nnc_gemm_nt on the flattened [N, C] result (ops.c:393-461,
+// 1843-1886) - without the pooled tensor ever leaving the workgroup.
+//
+// Built for small batches, where the two reference ops are two launches of
+// little work each and the time goes to memory round trips: every load of a
+// workgroup is issued before it waits for any. Grid (ceil(O / 16), N), 256
+// threads: a workgroup takes one image and 16 classes. Wave q first loads
+// its 4 rows of w into registers (lane l: channels l, l + 64, ...; coalesced
+// along c), then the whole workgroup copies the image's planes into LDS
+// (coalesced, rows padded by one float) - both in flight together. Thread t
+// sums planes t, t + 256, ... sequentially in the reference's h-major order
+// and divides by H*W: the reference's float means, bit for bit. Each row's
+// dot product: exact float products summed in double per lane, the 64 lane
+// sums by a shuffle tree, times alpha, plus beta * c, rounded once to float.
+// The reference adds the same exact products in one sequential double chain:
+// another order of double additions, below float rounding almost always.
+static constexpr int GG_OT = 16, GG_ROWS = GG_OT / 4;
+static constexpr int GG_F4 = 4;   // float4 of a row per lane: C <= 1024
+static constexpr int GG_U = 28;   // float4 of the image per thread in flight at once
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+    return v;
+}
+
+// Needs C % 4 == 0 and 16-byte aligned x and w (checked on the host).
+__global__ void __launch_bounds__(256) gap_gemm_nt_k(const float* __restrict__ x, const float* __restrict__ w,
+                                                     const float* __restrict__ cv, float* __restrict__ out, int C,
+                                                     int HW, int O, int c_mode, float alpha, float beta) {
+    extern __shared__ float sm[];
+    float* mean = sm;        // C floats
+    float* stage = sm + C;   // C planes of HW + 1 floats
+    const int n = blockIdx.y;
+    const int tid = threadIdx.x, q = tid >> 6, lane = tid & 63;
+    const int o0 = blockIdx.x * GG_OT + q * GG_ROWS;
+    // this wave's rows of w: lane l holds channels 4l .. 4l + 3 (+ 256 m)
+    float4 wr[GG_ROWS][GG_F4];
+#pragma unroll
+    for (int r = 0; r < GG_ROWS; ++r)
+#pragma unroll
+        for (int m = 0; m < GG_F4; ++m) {
+            const int c = 4 * lane + 256 * m;
+            wr[r][m] = (o0 + r < O && c < C) ? *reinterpret_cast<const float4*>(w + (int64_t)(o0 + r) * C + c)
+                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    // the image's planes into LDS, GG_U float4 per thread in flight
+    const int ld = HW + 1;
+    const float4* img = reinterpret_cast<const float4*>(x + (int64_t)n * C * HW);
+    const int run4 = C * HW / 4;
+    for (int base = tid; base < run4; base += 256 * GG_U) {
+        float4 v[GG_U];
+#pragma unroll
+        for (int u = 0; u < GG_U; ++u) {
+            const int i = base + 256 * u;
+            v[u] = i < run4 ? img[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < GG_U; ++u) {
+            const int i = base + 256 * u;
+            if (i >= run4) break;
+            const float e4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 4 * i + j, pl = e / HW;
+                stage[pl * ld + (e - pl * HW)] = e4[j];
+            }
+        }
+    }
+    __syncthreads();
+    for (int pl = tid; pl < C; pl += 256) {
+        const float* plane = stage + pl * ld;
+        float acc = 0.0f;
+        for (int k = 0; k < HW; ++k) acc += plane[k];
+        mean[pl] = acc / (float)HW;
+    }
+    __syncthreads();
+    double mv[GG_F4][4];
+#pragma unroll
+    for (int m = 0; m < GG_F4; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 4 * lane + 256 * m + j;
+            mv[m][j] = c < C ? (double)mean[c] : 0.0;
+        }
+#pragma unroll
+    for (int r = 0; r < GG_ROWS; ++r) {
+        double acc = 0.0;
+#pragma unroll
+        for (int m = 0; m < GG_F4; ++m)
+            acc += mv[m][0] * (double)wr[r][m].x + mv[m][1] * (double)wr[r][m].y + mv[m][2] * (double)wr[r][m].z +
+                   mv[m][3] * (double)wr[r][m].w;
+        acc = wave_sum_f64(acc);
+        const int o = o0 + r;
+        if (lane == 0 && o < O) {
+            acc *= (double)alpha;
+            if (c_mode == 1) acc += (double)beta * (double)cv[o];
+            else if (c_mode == 2) acc += (double)beta * (double)cv[(int64_t)n * O + o];
+            out[(int64_t)n * O + o] = (float)acc;
+        }
+    }
+}
+
 }  // namespace nnc
 
 using namespace nnc;
@@ -322,6 +430,47 @@ void nnc_maxpool2d(Tensor* in, Tensor* out, int kh, int kw, int sh, int sw, int 
 
 void nnc_avgpool2d(Tensor* in, Tensor* out, int kh, int kw, int sh, int sw, int ph, int pw) {
     pool_entry<false>("nnc_avgpool2d", in, out, kh, kw, sh, sw, ph, pw);
+}
+
+// No reference counterpart: GlobalAveragePool -> Flatten -> Gemm (transB) as
+// one kernel, emitted by the mi355x target at O3 when the pooled tensor only
+// feeds the classifier. in [N][C][H][W], w [O][C], c [O] or [N][O] or NULL,
+// out [N][O]; nnc_avgpool2d over the whole plane followed by
+// nnc_gemm_nt(pooled as [N, C], w, c, out, alpha, beta), the double sums of
+// the second in another fixed order (gap_gemm_nt_k).
+void nnc_hip_gap_gemm_nt(Tensor* in, Tensor* w, Tensor* c, Tensor* out, float alpha, float beta) {
+    const char* name = "nnc_hip_gap_gemm_nt";
+    if (!ready(name)) return;
+    if (!has_data(in) || !has_data(w) || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
+    if (in->ndim != 4 || w->ndim != 2) return fail(NNC_HIP_EINVAL, name, "expected in [N][C][H][W] and w [O][C]");
+    const int64_t N = in->shape[0], C = in->shape[1], HW = in->shape[2] * in->shape[3], O = w->shape[0];
+    if (w->shape[1] != C) return fail(NNC_HIP_EINVAL, name, "w has %lld columns for %lld channels",
+                                      (long long)w->shape[1], (long long)C);
+    if (numel(out) < N * O) return fail(NNC_HIP_EINVAL, name, "output smaller than N x O");
+    int c_mode = 0;
+    if (c && c->data) {
+        if (numel(c) == O && c->ndim == 1) c_mode = 1;
+        else if (numel(c) >= N * O) c_mode = 2;
+        else return fail(NNC_HIP_EINVAL, name, "c is neither [O] nor [N][O]");
+    }
+    if (N == 0 || O == 0) return;
+    // the means and every plane of one image in LDS (at most 128 KB); the rows
+    // of w in registers, GG_F4 float4 per lane (C <= 1024)
+    const int64_t lds_floats = C + C * (HW + 1);
+    if (HW <= 0 || C <= 0 || C % 4 || C > 256 * GG_F4 || lds_floats > 32768 || N > 65535 ||
+        !aligned16(in->data) || !aligned16(w->data))
+        return fail(NNC_HIP_EUNSUPP, name, "needs C %% 4 == 0, C <= %d, C * (H*W + 2) floats <= 128 KB, aligned data",
+                    256 * GG_F4);
+    const size_t lds = (size_t)lds_floats * sizeof(float);
+    // more than 64 KB of dynamic LDS needs the attribute (once, thread-safe)
+    static const bool big_lds = hipFuncSetAttribute((const void*)gap_gemm_nt_k,
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize, 32768 * 4) ==
+                                hipSuccess;
+    if (!big_lds && lds > 65536) return fail(NNC_HIP_EDEVICE, name, "hipFuncSetAttribute failed");
+    set_work(2.0 * N * O * C, 4.0 * (double)(N * C * HW + O * C + N * O + (c_mode ? O : 0)));
+    launch(name, gap_gemm_nt_k, dim3((unsigned)ceil_div(O, GG_OT), (unsigned)N), dim3(256), lds,
+           (const float*)in->data, (const float*)w->data, c_mode ? (const float*)c->data : nullptr, (float*)out->data,
+           (int)C, (int)HW, (int)O, c_mode, alpha, beta);
 }
 
 }  // extern "C"

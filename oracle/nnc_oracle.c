@@ -1066,3 +1066,25 @@ void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out,
     free(wp);
     free(proj);
 }
+
+/* ------------------------------------------------------------------------
+ * Global average pool streamed into the classifier (include/nnc_hip.h), no
+ * reference counterpart: restated as the composition it replaces,
+ * nnc_avgpool2d over the whole plane into a temporary [N][C][1][1]
+ * (ops.c:393-461), then nnc_gemm_nt of that temporary viewed as [N, C] with
+ * w [O][C] (ops.c:1843-1886). Pinned by composition of two pinned entry
+ * points (tests/test_oracle.py checks it against float64 numpy too).
+ * ---------------------------------------------------------------------- */
+void nnc_hip_gap_gemm_nt(Tensor* in, Tensor* w, Tensor* c, Tensor* out, float alpha, float beta) {
+    if (!in || !w || !out || !in->data || !w->data || !out->data || in->ndim != 4 || w->ndim != 2) return;
+    const int64_t N = in->shape[0], C = in->shape[1];
+    float* pooled = (float*)malloc((size_t)(N * C > 0 ? N * C : 1) * sizeof(float));
+    if (!pooled) return;
+    int64_t shape4[4] = {N, C, 1, 1}, shape2[2] = {N, C};
+    Tensor t4 = {pooled, NNC_DTYPE_FLOAT32, shape4, 4, (int64_t)(N * C * 4)};
+    Tensor t2 = {pooled, NNC_DTYPE_FLOAT32, shape2, 2, (int64_t)(N * C * 4)};
+    const int H = (int)in->shape[2], W = (int)in->shape[3];
+    nnc_avgpool2d(in, &t4, H, W, H, W, 0, 0);
+    nnc_gemm_nt(&t2, w, c, out, alpha, beta);
+    free(pooled);
+}

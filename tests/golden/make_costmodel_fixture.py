@@ -7,7 +7,7 @@ ResNet-18 (batch 1, 8, 32) and the transformer encoder (batch 8, sequence
 graph-replay milliseconds per step printed beside them:
 
     rocprofv3 --kernel-trace --output-format csv -d <dir>/<cfg> -o trace -- \\
-        python3 <script that builds the program, runs it once, captures it and replays it 23 times> <cfg>
+        python3 tests/golden/costmodel_trace_run.py <cfg>
 
 Output per configuration: the replayed step time, and per kernel (demangled
 name without template arguments) the launches per step and the median

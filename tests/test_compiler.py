@@ -277,3 +277,28 @@ def test_fused_conv_never_writes_over_its_own_image(pkg):
     from nnc_py_amd.compiler import zoo
     r18 = build_program(zoo.resnet18(batch=1, seed=0), opt_level=3)
     assert any(n.op_type in ("FusedConvAddRelu",) and n.outputs[0] in r18.plan.inplace for n in r18.order)
+
+
+def test_gap_gemm_tile_streaming_pass(pkg):
+    """stream_tiles at a batch it is allowed for: GlobalAveragePool ->
+    Flatten -> Gemm(transB) becomes one FusedGapGemm lowered to
+    nnc_hip_gap_gemm_nt, the pooled tensors gone, the decision and its LDS
+    footprint in the node's metadata; above the batch limit, or over the LDS
+    budget, the pair stays."""
+    from nnc_py_amd.compiler import build_program, passes, zoo
+    old = passes.GAP_GEMM_MAX_BATCH
+    passes.GAP_GEMM_MAX_BATCH = 2
+    try:
+        prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
+        ops = [c.op for c in prog.calls]
+        assert ops[-1] == "nnc_hip_gap_gemm_nt" and "nnc_avgpool2d" not in ops and len(ops) == 19
+        node = next(n for n in prog.order if n.op_type == "FusedGapGemm")
+        ts = node.metadata["tile_stream"]
+        assert ts["lds_bytes"] == 4 * (512 + 512 * 50) <= ts["budget"] and ts["hbm_bytes_saved"] == 2 * 2 * 512 * 4
+        assert prog.calls[-1].args[4:] == [("f", 1.0), ("f", 1.0)]
+        big = [c.op for c in build_program(zoo.resnet18(batch=4, seed=0), opt_level=3).calls]
+        assert big[-2:] == ["nnc_avgpool2d", "nnc_gemm_nt"]
+        g = zoo.resnet18(batch=2, seed=0)
+        assert passes.stream_tiles(g, lds_budget=4 * 512 * 50) == 0  # over the budget
+    finally:
+        passes.GAP_GEMM_MAX_BATCH = old

@@ -105,7 +105,8 @@ def test_generated_debug_build_matches_the_executor_dump(tmp_path, pkg, oracle_l
 def test_resnet18_layerwise_against_oracle(tmp_path, hip, oracle_lib):
     from nnc_py_amd.compiler import Executor, build_program, zoo
     x = np.random.default_rng(0).standard_normal((1, 3, 224, 224)).astype(np.float32)
-    ex = Executor(build_program(zoo.resnet18(batch=1, seed=1), opt_level=3), device=True)
+    prog = build_program(zoo.resnet18(batch=1, seed=1), opt_level=3)
+    ex = Executor(prog, device=True)
     ex.set_input("input", x)
     ex.run_debug(tmp_path / "gpu.txt")
     ex.close()
@@ -114,7 +115,7 @@ def test_resnet18_layerwise_against_oracle(tmp_path, hip, oracle_lib):
     dc = _tools()
     res = dc.DebugComparator(tmp_path / "gpu.txt", tmp_path / "ref.txt", rtol=1.5e-2, atol=3e-3).compare()
     assert not res["mismatched"] and not res["shape_mismatch"] and not res["missing_in_nnc"], res
-    assert len(res["matched"]) >= 20
+    assert len(res["matched"]) == len(prog.order)  # every node's output (the O3 program has 19 nodes)
 
 
 @pytest.mark.gpu

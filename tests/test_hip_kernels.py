@@ -417,3 +417,56 @@ def test_row_kernels_many_rows(shape, hip, dmem, abi, oracle_lib):
         exp = caserun.run_case(oracle_lib, case, abi)["out"]
         got = caserun.run_case(hip, case, abi, dmem)["out"]
         _check(got, exp, f"{case['name']} {shape}")
+
+
+GAP_GEMM_SHAPES = [
+    (1, 512, 7, 7, 1000, "o", 1.0, 1.0),    # ResNet-18 classifier, batch 1
+    (32, 512, 7, 7, 1000, "o", 1.0, 1.0),   # batch 32
+    (5, 100, 3, 5, 70, "no", 0.5, -2.0),    # image / class tails, [N][O] bias, alpha, beta
+    (3, 40, 1, 1, 9, None, 1.0, 1.0),       # 1x1 planes, no bias
+    (6, 1024, 5, 5, 130, "o", 1.0, 1.0),    # the most channels (four float4 per lane), several staging rounds
+    (2, 300, 9, 9, 17, "o", 1.0, 1.0),      # channels not a multiple of 256
+]
+
+
+@pytest.mark.parametrize("shape", GAP_GEMM_SHAPES, ids=[str(s[:5]) for s in GAP_GEMM_SHAPES])
+def test_gap_gemm_nt_bit_exact(shape, hip, dmem, abi, oracle_lib):
+    """nnc_hip_gap_gemm_nt against the oracle's nnc_avgpool2d + nnc_gemm_nt:
+    the same float means and exact products, the double sums in another
+    order, so every output is within one float ulp of the oracle's (and
+    within the 1e-4 / 1e-3 bar)."""
+    n, c, h, w, o, bias, alpha, beta = shape
+    rng = np.random.default_rng(n * 7 + c)
+    tensors = {"x": rng.standard_normal((n, c, h, w)).astype(np.float32),
+               "w": (rng.standard_normal((o, c)) / np.sqrt(c)).astype(np.float32),
+               "out": np.zeros((n, o), np.float32)}
+    if bias == "o":
+        tensors["c"] = (rng.standard_normal(o) * 0.01).astype(np.float32)
+    elif bias == "no":
+        tensors["c"] = rng.standard_normal((n, o)).astype(np.float32)
+    case = {"name": f"gap_gemm_{shape}", "op": "nnc_hip_gap_gemm_nt", "tensors": tensors,
+            "args": [("t", "x"), ("t", "w"), ("t", "c") if bias else ("null",), ("t", "out"), ("f", alpha),
+                     ("f", beta)], "outputs": ["out"]}
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    from nnc_py_amd import runtime
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    assert caserun.fp_violations(got, exp, 1e-4, 1e-3).size == 0
+    ulp = np.spacing(np.abs(exp).astype(np.float32))
+    assert (np.abs(got - exp) <= ulp).all(), f"max diff {np.abs(got - exp).max():.3g}"
+    print(f"{(got != exp).sum()} of {got.size} outputs one ulp off", flush=True)
+
+
+def test_gap_gemm_nt_rejections(hip, dmem, abi):
+    from nnc_py_amd import runtime
+    rng = np.random.default_rng(3)
+    bad = {"x": rng.standard_normal((2, 8, 4, 4)).astype(np.float32),
+           "w": rng.standard_normal((5, 7)).astype(np.float32),  # 7 columns for 8 channels
+           "out": np.zeros((2, 5), np.float32)}
+    runtime.clear_error()
+    out = caserun.run_case(hip, {"name": "bad", "op": "nnc_hip_gap_gemm_nt", "tensors": bad,
+                                 "args": [("t", "x"), ("t", "w"), ("null",), ("t", "out"), ("f", 1.0), ("f", 1.0)],
+                                 "outputs": ["out"]}, abi, dmem)["out"]
+    assert runtime.last_error()[0] == 1 and not out.any()
+    runtime.clear_error()

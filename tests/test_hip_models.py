@@ -281,3 +281,27 @@ def test_concurrent_host_threads_match_serial(hip):
         assert not failures, failures[0]
     for ex in exes:
         ex.close()
+
+
+def test_gap_gemm_streamed_program_matches_unfused(hip):
+    """ResNet-18 batch 2 with the classifier tile-streamed from the global
+    average pool (nnc_hip_gap_gemm_nt, chosen by the O3 pass when allowed)
+    gives the unfused program's logits within one float ulp."""
+    from nnc_py_amd.compiler import Executor, build_program, passes, zoo
+    x = np.random.default_rng(8).standard_normal((2, 3, 224, 224)).astype(np.float32)
+    outs = {}
+    old = passes.GAP_GEMM_MAX_BATCH
+    for limit in (0, 2):
+        passes.GAP_GEMM_MAX_BATCH = limit
+        try:
+            prog = build_program(zoo.resnet18(batch=2, seed=1), opt_level=3)
+        finally:
+            passes.GAP_GEMM_MAX_BATCH = old
+        assert (prog.calls[-1].op == "nnc_hip_gap_gemm_nt") == (limit == 2)
+        ex = Executor(prog, device=True)
+        ex.set_input("input", x)
+        ex.run()
+        outs[limit] = ex.get("output")
+        ex.close()
+    diff = np.abs(outs[2] - outs[0])
+    assert (diff <= np.spacing(np.abs(outs[0]))).all(), diff.max()

@@ -384,3 +384,33 @@ def test_oracle_matmul_relu_composition(bias_shape, oracle_lib, abi):
     got = caserun.run_case(oracle_lib, {"name": "mmr", "op": "nnc_matmul_relu", "tensors": t, "args": args,
                                         "outputs": ["out"]}, abi)["out"]
     assert caserun.same_bits(got, _relu(want))
+
+
+@pytest.mark.parametrize("n,c,h,w,o,bias", [(2, 16, 7, 7, 10, "o"), (3, 5, 3, 4, 7, "no"), (1, 8, 1, 1, 3, None)])
+def test_oracle_gap_gemm_nt_composition(n, c, h, w, o, bias, oracle_lib, abi):
+    """nnc_hip_gap_gemm_nt: the plane means are the sequential float sums
+    (numpy cumsum is sequential) divided by H*W, bit for bit; the outputs
+    the float64 dot products with w, times alpha, plus beta * c, rounded to
+    float."""
+    rng = np.random.default_rng(41 + c)
+    x = rng.standard_normal((n, c, h, w)).astype(F32)
+    wt = rng.standard_normal((o, c)).astype(F32)
+    tensors = {"x": x, "w": wt, "out": np.zeros((n, o), F32)}
+    args = [("t", "x"), ("t", "w")]
+    if bias == "o":
+        tensors["c"] = rng.standard_normal(o).astype(F32)
+    elif bias == "no":
+        tensors["c"] = rng.standard_normal((n, o)).astype(F32)
+    args += [("t", "c") if bias else ("null",), ("t", "out"), ("f", 0.75), ("f", -1.5)]
+    got = caserun.run_case(oracle_lib, {"name": "gapgemm", "op": "nnc_hip_gap_gemm_nt", "tensors": tensors,
+                                        "args": args, "outputs": ["out"]}, abi)["out"]
+    mean = np.cumsum(x.reshape(n, c, h * w), axis=-1, dtype=F32)[..., -1] / F32(h * w)
+    pooled = caserun.run_case(oracle_lib, {"name": "gap", "op": "nnc_avgpool2d",
+                                           "tensors": {"x": x, "p": np.zeros((n, c, 1, 1), F32)},
+                                           "args": [("t", "x"), ("t", "p"), ("i", h), ("i", w), ("i", h), ("i", w),
+                                                    ("i", 0), ("i", 0)], "outputs": ["p"]}, abi)["p"]
+    assert caserun.same_bits(pooled.reshape(n, c), mean.astype(F32))
+    ref = mean.astype(np.float64) @ wt.astype(np.float64).T * 0.75
+    if bias:
+        ref = ref + -1.5 * tensors["c"].astype(np.float64)
+    np.testing.assert_allclose(got, ref.astype(F32), rtol=1e-6, atol=1e-6)
