@@ -202,6 +202,20 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
 void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out, int kh, int kw, int sh, int sw,
                        int ph, int pw, int psh, int psw, int act);
 
+/* nnc_hip_conv_maxpool: ResNet's stem - convolution on packed [Co][Kp]
+ * rows (3 channels, 7x7), bias, relu - streamed into the 3x3 / stride 2 /
+ * pad 1 max pool that follows it:
+ *   out = maxpool(relu(conv(in, w) + b)), out [N][Co][Ho/2][Wo/2]
+ * with Ho, Wo the convolution's output size from in, the kernel, stride and
+ * pads. The convolution output never reaches HBM: each workgroup pools the
+ * rows it computes. Same convolution (within the conv bar of the reference's
+ * double sums) and the same max (bit for bit on that convolution) as
+ * nnc_hip_conv_packed + nnc_maxpool2d. Needs Co <= 64, Ho and Wo even,
+ * Wo <= 128 (NNC_HIP_EUNSUPP otherwise). Emitted by the mi355x target's O3
+ * tile-streaming pass. No counterpart in the reference ABI. */
+void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw, int ph,
+                          int pw);
+
 /* nnc_hip_gap_gemm_nt: GlobalAveragePool -> Flatten -> Gemm(transB = 1) in
  * one kernel, the pooled [N, C] tensor never leaving the workgroup:
  *   out[n][o] = alpha * sum_c mean_hw(in[n][c]) * w[o][c] + beta * c

@@ -122,6 +122,7 @@ TARGET_SIGNATURES = {
     "nnc_hip_conv_proj": [TP, TP, TP, TP, TP] + [c_int] * 9,
     "nnc_hip_conv_packed_noalloc": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
     "nnc_hip_gap_gemm_nt": [TP, TP, TP, TP, c_float, c_float],
+    "nnc_hip_conv_maxpool": [TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int],
 }
 
 

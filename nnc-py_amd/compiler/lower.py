@@ -158,6 +158,12 @@ def lower_node(g: Graph, node: Node) -> Call:
         if node.metadata.get("lowering", {}).get("weight_pack") == "rhs_transposed_constant" and ta == 0 and tb == 1:
             return Call("nnc_gemm_nt", args, node.name)
         return Call("nnc_gemm", args + [("i", ta), ("i", tb)], node.name)
+    if op == "FusedConvMaxPool":  # stem conv + relu streamed into its max pool (include/nnc_hip.h)
+        kh, kw = node.attrs.get("kernel_shape", [7, 7])
+        sh, sw = (list(node.attrs.get("strides", [1, 1])) + [1])[:2]
+        ph, pw = (list(node.attrs.get("pads", [0, 0, 0, 0])) + [0, 0])[:2]
+        return Call("nnc_hip_conv_maxpool", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0])]
+                    + [("i", int(v)) for v in (kh, kw, sh, sw, ph, pw)], node.name)
     if op == "FusedGapGemm":  # GAP streamed into the classifier (include/nnc_hip.h)
         return Call("nnc_hip_gap_gemm_nt", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0]),
                                             ("f", float(node.attrs.get("alpha", 1.0))),

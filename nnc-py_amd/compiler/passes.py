@@ -360,8 +360,68 @@ def gap_gemm_lds_bytes(channels: int, plane: int) -> int:
     return 4 * (channels + channels * (plane + 1))
 
 
+# The stem streamed into its max pool (nnc_hip_conv_maxpool) computes each
+# conv row as one 128-pixel tile of which 112 pixels are used and holds two
+# workgroups per CU (its running maxima beside the accumulators), against the
+# unfused stem's three; its gather loads bound both kernels. Measured on
+# MI355X (hipGraph replay, the stem conv + max pool of ResNet-18): fused
+# 35.4 / 57.6 / 170.8 us at batch 1 / 8 / 32 against 15.1 / 53.6 / 149.4 us
+# unfused, although the fused kernel never writes the 103 MB (batch 32)
+# activation. Taken from this batch on: none by default.
+CONV_POOL_MIN_BATCH: int | None = None
+
+
+def conv_pool_lds_bytes() -> int:
+    """LDS of the fused stem + pool kernel per workgroup: two operand stages
+    of the 64 x 128 tile, the stem's 256-entry tap table, a wave-boundary
+    exchange row and the bias."""
+    return 4 * (2 * (64 * 32 + 128 * 32) + 2 * 256 + 4 * 2 * 32 + 64)
+
+
+def _stream_conv_pool(g: Graph, lds_budget: int) -> int:
+    """The packed RGB 7x7 stem conv + relu (FusedConvRelu on [Co][Kp] rows)
+    whose output only feeds a 3x3 / stride 2 / pad 1 MaxPool becomes one
+    FusedConvMaxPool node (inputs: x, w, bias or ""; the conv's attrs),
+    lowered to nnc_hip_conv_maxpool: each workgroup pools the conv rows it
+    computes. Needs Co <= 64, even conv output sizes, rows of at most 128
+    pixels, batch >= CONV_POOL_MIN_BATCH."""
+    if CONV_POOL_MIN_BATCH is None:
+        return 0
+    fused = 0
+    for conv in list(g.nodes):
+        if conv.op_type != "FusedConvRelu" or len(conv.inputs) < 2:
+            continue
+        w = g.tensors[conv.inputs[1]]
+        x = g.tensors[conv.inputs[0]]
+        mid = conv.outputs[0]
+        if len(w.shape) != 2 or len(x.shape) != 4 or x.shape[1] != 3 or mid in g.outputs:
+            continue
+        if list(conv.attrs.get("kernel_shape", [])) != [7, 7] or w.shape[0] > 64 or x.shape[0] < CONV_POOL_MIN_BATCH:
+            continue
+        users = g.consumers(mid)
+        if len(users) != 1 or users[0].op_type != "MaxPool":
+            continue
+        pool = users[0]
+        if (list(pool.attrs.get("kernel_shape", [])) != [3, 3] or list(pool.attrs.get("strides", [])) != [2, 2]
+                or list(pool.attrs.get("pads", [0, 0, 0, 0])) != [1, 1, 1, 1]):
+            continue
+        _, _, ho, wo = g.tensors[mid].shape
+        if ho % 2 or wo % 2 or wo > 128 or conv_pool_lds_bytes() > lds_budget:
+            continue
+        conv.op_type = "FusedConvMaxPool"
+        conv.outputs = list(pool.outputs)
+        conv.metadata["fused_from"] = conv.metadata.get("fused_from", [conv.name]) + [pool.name]
+        conv.metadata["tile_stream"] = {"intermediate": mid, "lds_bytes": conv_pool_lds_bytes(),
+                                        "budget": lds_budget, "hbm_bytes_saved": 2 * g.tensors[mid].nbytes}
+        g.nodes.remove(pool)
+        g.tensors.pop(mid, None)
+        fused += 1
+    return fused
+
+
 def stream_tiles(g: Graph, lds_budget: int = LDS_BUDGET) -> int:
-    """GlobalAveragePool -> Flatten -> Gemm (transB = 1, constant w [O, C])
+    """Stem conv + relu -> MaxPool as FusedConvMaxPool (_stream_conv_pool),
+    and GlobalAveragePool -> Flatten -> Gemm (transB = 1, constant w [O, C])
     whose pooled and flattened tensors have no other reader becomes one
     FusedGapGemm node (inputs: x, w, bias or ""; the Gemm's alpha/beta),
     lowered to nnc_hip_gap_gemm_nt: each workgroup averages its images'
@@ -370,7 +430,7 @@ def stream_tiles(g: Graph, lds_budget: int = LDS_BUDGET) -> int:
     intermediate (an image's C means, its w blocks and partial sums) fits
     `lds_budget`, at batches up to GAP_GEMM_MAX_BATCH. The decision and its
     footprint are recorded in the node's metadata["tile_stream"]."""
-    fused = 0
+    fused = _stream_conv_pool(g, lds_budget)
     for gap in list(g.nodes):
         if gap.op_type != "GlobalAveragePool" or len(gap.inputs) != 1:
             continue

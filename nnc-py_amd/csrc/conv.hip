@@ -20,6 +20,7 @@
 // ResNet-18 scale stays inside 1e-4 abs / 1e-3 rel of the reference's fp64
 // sum); shared tiles add their segments in fixed workgroup order.
 #include <math.h>
+#include <stdlib.h>
 
 #include "mfma_tile.h"
 
@@ -863,6 +864,179 @@ __global__ void __launch_bounds__(T::THREADS, DmaStage<T>::MIN_WAVES) conv_dma_k
     }
 }
 
+// ---------------------------------------------------------------------------
+// Convolution + relu streamed into a 3x3 / stride 2 / pad 1 max pool
+// (nnc_hip_conv_maxpool): ResNet's stem without its 103 MB (batch 32)
+// activation in HBM.
+// ---------------------------------------------------------------------------
+// The convolution output is viewed with rows of 128 pixels (a.Wo = 128, the
+// real width pb.Wr <= 128 pixels used), so one 64 x 128 tile is one output
+// row of 64 channels. The conv rows of all images, in order, are split into
+// G contiguous ranges of whole pool-row pairs (rows 2p, 2p + 1), one per
+// workgroup of a persistent grid (G = resident workgroups): workgroup g
+// computes its rows one after the other, the next row's first slice loaded
+// during the current row's last (as in conv_dma_k). For each row: bias +
+// relu (the conv epilogue's rounding), then the max over conv columns 2j-1,
+// 2j, 2j+1 by lane shuffles (consecutive pixels are consecutive lanes of a
+// wave; a wave's first pixel takes its left neighbour from the previous wave
+// through LDS), held by the lane of pixel 2j; then down the rows in
+// registers: row 2p starts pool row p (with row 2p-1's maxima unless p = 0),
+// row 2p + 1 completes it and it is stored. A range's first pool row p > 0
+// is missing row 2p - 1, which the previous range ends with: that range
+// writes its last row's maxima to pb.side, and conv_pool_fixup_k takes the
+// max of the two. Relu values are never NaN or -0, so the max is exact and
+// order-free: the same bits as nnc_maxpool2d's scan of the same convolution.
+struct PoolBand {
+    float* out;   // [N][Co][Hp][Wp]
+    float* side;  // [G][Co][Wp]: a range's last-row maxima for the next range's first pool row
+    int Wr, Hp, Wp;
+    int pairs;    // N * Hp: pool rows of all images, two conv rows each
+};
+
+__device__ __forceinline__ int pool_range_begin(int g, int G, int pairs) { return (int)((int64_t)g * pairs / G); }
+
+// Two waves per SIMD: the running maxima of a row stay in registers beside
+// the accumulators, more than the three-wave budget of conv_dma_k holds.
+template <class T, class L>
+__global__ void __launch_bounds__(T::THREADS, 2) conv_pool_k(ConvArgs a, PoolBand pb) {
+    static_assert(T::BM == 64 && T::BN == 128 && T::WM == 1 && T::WN == 4 && T::TM == 2 && T::TN == 1,
+                  "one 64-channel row of 128 pixels per tile, 32 pixels per wave");
+    typedef DmaStage<T> D;
+    extern __shared__ __align__(16) float lds[];
+    __shared__ float xch[T::NW][2][32];  // each wave's last pixel (per lane half) for the next wave
+    __shared__ float bias_s[T::BM];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wi = (wave / T::WN) * T::WAVE_M, wj = (wave % T::WN) * T::WAVE_N;
+    const int a_row = wi + (lane & 31);
+    const int a_sw = (4 * (lane >> 5)) ^ (lane & 7);
+    const int b_off = D::A_FLOATS + 16 * (lane >> 5) * T::BN + wj + (lane & 31);
+    L ld;
+    ld.init(a, wave, lane);
+    if (L::EXTRA_LDS_FLOATS) {
+        ld.prepare(lds + 2 * D::STAGE, a);
+        __syncthreads();
+    }
+    const int G = gridDim.x;
+    const int g = xcd_remap(blockIdx.x, G);
+    const int t0 = 2 * pool_range_begin(g, G, pb.pairs), t1 = 2 * pool_range_begin(g + 1, G, pb.pairs);
+    if (t0 >= t1) return;  // uniform over the workgroup; never with G <= pairs
+    const int iters = (a.K + T::BK - 1) / T::BK;
+    const int q = lane & 31, half = lane >> 5;
+    const int px = wj + q;  // pixel of the row (virtual width 128)
+    if (threadIdx.x < T::BM) bias_s[threadIdx.x] = (a.bias && (int)threadIdx.x < a.Co) ? a.bias[threadIdx.x] : 0.f;
+    ld.tile(a, 0, t0 * T::BN, lane);
+    ld.begin(0);
+    ld.issue(lds, true, 0);
+    ld.issue(lds, true, 1);
+    wait_dma();
+    __syncthreads();
+    f32x4 a0[T::TM], b0[T::TN], a1[T::TM], b1[T::TN];
+    read_quad_dma<T>(lds, a_row, a_sw, lds + b_off, 0, a0, b0);
+    int stage = 0;
+    float run[T::TM][16];
+    for (int t = t0; t < t1; ++t) {
+        const int n = t / a.Ho, y = t - n * a.Ho;
+        floatx16 sum[T::TM][T::TN];
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sum[tm][0][r] = 0.f;
+        const bool have_next = t + 1 < t1;
+        for (int it = 0; it < iters; ++it) {
+            const bool last = it + 1 == iters;
+            if (last) {
+                if (have_next) {
+                    ld.tile(a, 0, (t + 1) * T::BN, lane);
+                    ld.begin(0);
+                }
+            } else {
+                ld.step(true);
+            }
+            const bool more = !last || have_next;
+            float* next = lds + (stage ^ 1) * D::STAGE;
+            const float* S = lds + stage * D::STAGE;
+            ld.issue(next, more, 0);
+            read_quad_dma<T>(S, a_row, a_sw, S + b_off, 1, a1, b1);
+            mfma_quad<T>(a0, b0, sum);
+            ld.issue(next, more, 1);
+            read_quad_dma<T>(S, a_row, a_sw, S + b_off, 2, a0, b0);
+            mfma_quad<T>(a1, b1, sum);
+            read_quad_dma<T>(S, a_row, a_sw, S + b_off, 3, a1, b1);
+            mfma_quad<T>(a0, b0, sum);
+            wait_dma();
+            __syncthreads();
+            read_quad_dma<T>(next, a_row, a_sw, next + b_off, 0, a0, b0);
+            mfma_quad<T>(a1, b1, sum);
+            stage ^= 1;
+        }
+        // bias + relu (in the accumulators), then the max over columns
+        // 2j-1 .. 2j+1 at the lane of 2j
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float x = sum[tm][0][r];  // copied out of the vector first
+                const float v = activate(x + bias_s[acc_row<T>(tm, r)], kActRelu);
+                sum[tm][0][r] = v;
+                if (q == 31) xch[wave][half][tm * 16 + r] = v;
+            }
+        __syncthreads();
+        const bool has_left = px >= 1, has_right = px + 1 < pb.Wr;
+        const bool store = (q & 1) == 0 && px < pb.Wr;
+        const bool fresh = (y & 1) == 0 && (t == t0 || y == 0);  // pool row without its row 2p - 1 here
+        const int j = px >> 1, p = y >> 1;
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float v = sum[tm][0][r];
+                const float right = __shfl(v, (lane + 1) & 63);
+                float left = __shfl(v, (lane - 1) & 63);
+                if (q == 0) left = wave > 0 ? xch[wave - 1][half][tm * 16 + r] : 0.f;
+                float m = v;
+                if (has_right) m = fmaxf(m, right);
+                if (has_left) m = fmaxf(m, left);
+                // down the rows: y = 2p starts pool row p, y = 2p + 1 completes it
+                if ((y & 1) == 0) {
+                    run[tm][r] = fresh ? m : fmaxf(run[tm][r], m);
+                } else {
+                    const int co = acc_row<T>(tm, r);
+                    if (store && co < a.Co)
+                        pb.out[(((int64_t)n * a.Co + co) * pb.Hp + p) * pb.Wp + j] = fmaxf(run[tm][r], m);
+                    run[tm][r] = m;
+                }
+            }
+    }
+    // the last row's maxima: the top row of the next range's first pool row
+    const int y_last = (t1 - 1) % a.Ho;
+    if (y_last + 1 < a.Ho) {
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int co = acc_row<T>(tm, r);
+                if ((q & 1) == 0 && px < pb.Wr && co < a.Co)
+                    pb.side[((int64_t)g * a.Co + co) * pb.Wp + (px >> 1)] = run[tm][r];
+            }
+    }
+}
+
+// Completes each range's first pool row (when it is not an image's first)
+// with the previous range's last-row maxima. Grid (ceil(Co * Wp / 256),
+// ranges - 1): one thread per (channel, column) of range g = blockIdx.y + 1.
+__global__ void __launch_bounds__(256) conv_pool_fixup_k(PoolBand pb, int Co, int Ho, int G) {
+    const int g = blockIdx.y + 1;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= Co * pb.Wp) return;
+    const int t0 = 2 * pool_range_begin(g, G, pb.pairs);
+    const int n = t0 / Ho, y0 = t0 - n * Ho;
+    if (y0 == 0) return;  // an image's first pool row is complete
+    const int co = i / pb.Wp, j = i - co * pb.Wp;
+    float* o = pb.out + (((int64_t)n * Co + co) * pb.Hp + y0 / 2) * pb.Wp + j;
+    *o = fmaxf(*o, pb.side[((int64_t)(g - 1) * Co + co) * pb.Wp + j]);
+}
+
 // Grid (chunks, stream-K tiles): workgroup (c, t) finishes chunk c of tile t
 // (256 float4 of the BM x BN tile). Tiles covered by a single workgroup were
 // written by it; shared tiles sum their partials in workgroup order, then
@@ -1279,6 +1453,74 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
         launch_conv<ConvTSmall>(a, avec, dma, name);
 }
 
+// nnc_hip_conv_maxpool: maxpool3x3/s2/p1(relu(conv(in, w) + b)) for the
+// packed 3-channel stem ([Co][Kp] rows, Co <= 64) with conv rows of at most
+// 128 pixels and even conv output sizes.
+static void conv_maxpool_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw, int ph,
+                             int pw, const char* name) {
+    typedef ConvT64 T;
+    typedef DmaSmallC<T, 7, 7, 3> L;
+    if (!ready(name)) return;
+    if (!has_data(in) || !has_data(w) || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
+    if (in->ndim != 4 || w->ndim != 2 || out->ndim != 4) return fail(NNC_HIP_EINVAL, name, "expected 4D in/out, [Co][Kp] w");
+    ConvArgs a{};
+    a.in = (const float*)in->data;
+    a.w = (const float*)w->data;
+    a.bias = (b && b->data) ? (const float*)b->data : nullptr;
+    a.N = (int)in->shape[0];
+    a.Ci = (int)in->shape[1];
+    a.H = (int)in->shape[2];
+    a.W = (int)in->shape[3];
+    a.Co = (int)w->shape[0];
+    a.kh = kh, a.kw = kw, a.sh = sh, a.sw = sw, a.ph = ph, a.pw = pw;
+    a.act = kActRelu;
+    if (!(kh == 7 && kw == 7 && a.Ci == 3)) return fail(NNC_HIP_EUNSUPP, name, "only the 3-channel 7x7 stem");
+    if (sh <= 0 || sw <= 0 || ph < 0 || pw < 0) return fail(NNC_HIP_EINVAL, name, "bad stride/pad");
+    const int Ho = (a.H + 2 * ph - kh) / sh + 1, Wr = (a.W + 2 * pw - kw) / sw + 1;
+    const int64_t K = (int64_t)a.Ci * kh * kw, kp = (K + 31) / 32 * 32;
+    if (w->shape[1] != kp) return fail(NNC_HIP_EINVAL, name, "packed weight row is not K rounded up to 32");
+    if (a.Co < 1 || a.Co > 64 || Ho < 2 || Wr < 2 || Ho % 2 || Wr % 2 || Wr > 128)
+        return fail(NNC_HIP_EUNSUPP, name, "needs Co <= 64 and even conv output sizes with rows of at most 128");
+    const int Hp = Ho / 2, Wp = Wr / 2;
+    if (out->shape[0] != a.N || out->shape[1] != a.Co || out->shape[2] != Hp || out->shape[3] != Wp)
+        return fail(NNC_HIP_EINVAL, name, "output is not [N][Co][%d][%d]", Hp, Wp);
+    if (a.bias && numel(b) < a.Co) return fail(NNC_HIP_EINVAL, name, "bias smaller than Co");
+    if (!aligned16(a.w)) return fail(NNC_HIP_EUNSUPP, name, "weights not 16-byte aligned");
+    const int64_t in_bytes = (int64_t)a.N * a.Ci * a.H * a.W * 4;
+    const int64_t npix = (int64_t)a.N * Ho * 128;
+    if (in_bytes >= ((int64_t)1 << 31) || npix >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "input of 2 GiB or more");
+    if (a.N == 0) return;
+    a.Ho = Ho;
+    a.Wo = 128;  // rows of 128 pixels: one tile per conv row
+    a.K = (int)K;
+    a.ldw = (int)kp;
+    a.Npix = (int)npix;
+    auto kernel = conv_pool_k<T, L>;
+    const size_t lds = (size_t)(DmaStage<T>::LDS_FLOATS + L::EXTRA_LDS_FLOATS) * sizeof(float);
+    static const int slots = [&] {
+        if (hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+            return -1;
+        return resident_groups(kernel, lds, T::THREADS);
+    }();
+    if (slots < 0) return fail(NNC_HIP_EDEVICE, name, "hipFuncSetAttribute failed");
+    PoolBand pb{};
+    pb.out = (float*)out->data;
+    pb.Wr = Wr, pb.Hp = Hp, pb.Wp = Wp;
+    pb.pairs = a.N * Hp;
+    const int G = slots < pb.pairs ? slots : pb.pairs;
+    const size_t side_bytes = (size_t)G * a.Co * Wp * sizeof(float);
+    pb.side = workspace(side_bytes);
+    if (!pb.side) return partials_fail(name, side_bytes);
+    set_work(2.0 * a.Co * (double)a.N * Ho * Wr * K, 0.0);
+    launch("conv_igemm_64x128_k7x7c3_pool", kernel, dim3((unsigned)G), dim3(T::THREADS), lds, a, pb);
+    if (G > 1) {
+        set_work(0.0, 12.0 * (double)(G - 1) * a.Co * Wp);
+        launch("conv_pool_fixup", conv_pool_fixup_k, dim3((unsigned)ceil_div((int64_t)a.Co * Wp, 256), G - 1),
+               dim3(256), 0, pb, a.Co, Ho, G);
+    }
+}
+
 template <class T>
 static void launch_conv_proj(ConvArgs& a, const char* entry) {
     a.tiles_m = (int)ceil_div(a.Co, T::BM);
@@ -1465,6 +1707,16 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
     if (res && (!res->data || !res->shape)) return fail(NNC_HIP_EINVAL, name, "NULL residual data");
     if (act < kActNone || act > kActSigmoid) return fail(NNC_HIP_EINVAL, name, "act must be 0, 1 or 2");
     conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, act, name, res, true);
+}
+
+// No reference counterpart: ResNet's stem convolution (packed [Co][Kp]
+// rows, 3 channels, 7x7) with its relu and the 3x3 / stride 2 / pad 1 max
+// pool that follows, in one kernel (conv_pool_k) plus a small fixup; the
+// convolution output never reaches HBM. out = maxpool(relu(conv(in, w) +
+// b)) of shape [N][Co][Ho/2][Wo/2]; Co <= 64, Ho and Wo even, Wo <= 128.
+void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw, int ph,
+                          int pw) {
+    conv_maxpool_run(in, w, b, out, kh, kw, sh, sw, ph, pw, "nnc_hip_conv_maxpool");
 }
 
 // No reference counterpart: nnc_hip_conv_packed for callers that cannot

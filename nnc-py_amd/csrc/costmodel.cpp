@@ -495,6 +495,39 @@ void nnc_hip_conv_packed(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* 
     (void)sh, (void)sw, (void)ph, (void)pw, (void)act;
     conv("nnc_hip_conv_packed", in, w, b, res, out, kh, kw, true);
 }
+// the stem streamed into its max pool: bands of whole conv rows (64 x 128
+// tiles of which the row's pixels are used, no stream-K split), two
+// workgroups per CU, then the band-boundary fixup
+const MfmaKind kStemPool = {"stem_pool_64x128", 64, 128, 2, 0.50, 1.26};
+void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw, int ph,
+                          int pw) {
+    if (!in || !w || !out || !in->shape || !w->shape || !out->shape || in->ndim != 4 || out->ndim != 4) return;
+    if (sh <= 0 || sw <= 0) return;
+    const int64_t N = in->shape[0], Ci = in->shape[1], Co = w->shape[0];
+    const int64_t Ho = (in->shape[2] + 2 * ph - kh) / sh + 1, Wo = (in->shape[3] + 2 * pw - kw) / sw + 1;
+    const int64_t K = Ci * kh * kw, Hp = out->shape[2], Wp = out->shape[3];
+    if (N == 0 || Co == 0 || Ho <= 0 || Wo <= 0) return;
+    const double bytes = nbytes(in) + nbytes(w) + nbytes(b) + nbytes(out);
+    const int tiles = (int)(N * Ho);  // one conv row per tile: whole tiles, one band's rows per workgroup
+    const int iters = (int)ceil_div(K, kBK);
+    const double cu_rate = kMfmaF32 / kCUs;
+    const int slots = kStemPool.per_cu * kCUs;
+    int R = 1;
+    for (int c : {14, 8, 7, 4, 2, 1})
+        if (N * ceil_div(Hp, c) >= slots) {
+            R = c;
+            break;
+        }
+    const int64_t bands = N * ceil_div(Hp, R);
+    const double rows_per_cu = (double)ceil_div(bands, kCUs) * 2.0 * R;
+    const double slice = kStemPool.per_cu * 2.0 * kStemPool.bm * kStemPool.bn * kBK / (cu_rate * kStemPool.eff) * 1e6;
+    const double us = kLaunchUs + fmax(rows_per_cu / kStemPool.per_cu * iters * slice,
+                                       bytes / (kHbm * kStreamEff) * 1e6);
+    record("nnc_hip_conv_maxpool", "conv_igemm_64x128_k7x7c3_pool", us, 2.0 * Co * (double)N * Ho * Wo * K, bytes);
+    (void)tiles;
+    if (bands > N) stream_kernel("nnc_hip_conv_maxpool", "conv_pool_fixup", 12.0 * (double)(bands - N) * Co * Wp);
+}
+
 // the allocation-free variant launches the same kernels (plus a counter fill
 // where the in-kernel finish runs, priced as free here)
 void nnc_hip_conv_packed_noalloc(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,

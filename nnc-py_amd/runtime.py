@@ -70,6 +70,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_conv_proj": (abi.TARGET_SIGNATURES["nnc_hip_conv_proj"], None),
     "nnc_hip_conv_packed_noalloc": (abi.TARGET_SIGNATURES["nnc_hip_conv_packed_noalloc"], None),
     "nnc_hip_gap_gemm_nt": (abi.TARGET_SIGNATURES["nnc_hip_gap_gemm_nt"], None),
+    "nnc_hip_conv_maxpool": (abi.TARGET_SIGNATURES["nnc_hip_conv_maxpool"], None),
 }
 
 

@@ -1088,3 +1088,27 @@ void nnc_hip_gap_gemm_nt(Tensor* in, Tensor* w, Tensor* c, Tensor* out, float al
     nnc_gemm_nt(&t2, w, c, out, alpha, beta);
     free(pooled);
 }
+
+/* ------------------------------------------------------------------------
+ * ResNet's stem streamed into its max pool (include/nnc_hip.h), no
+ * reference counterpart: restated as the composition it replaces, the
+ * packed-weight convolution with relu (nnc_hip_conv_packed above, act 1:
+ * nnc_conv_relu, ops.c:720-1050) into a temporary [N][Co][Ho][Wo] with Ho,
+ * Wo from the input, kernel, stride and pad, then nnc_maxpool2d 3x3 /
+ * stride 2 / pad 1 (ops.c:316-391). Pinned by composition of pinned entry
+ * points.
+ * ---------------------------------------------------------------------- */
+void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw, int ph,
+                          int pw) {
+    if (!in || !w || !out || !in->data || !w->data || !out->data || in->ndim != 4 || sh <= 0 || sw <= 0) return;
+    const int64_t N = in->shape[0], Co = w->shape[0];
+    const int64_t Ho = (in->shape[2] + 2 * ph - kh) / sh + 1, Wo = (in->shape[3] + 2 * pw - kw) / sw + 1;
+    const int64_t n = N * Co * Ho * Wo;
+    float* tmp = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    if (!tmp) return;
+    int64_t shape[4] = {N, Co, Ho, Wo};
+    Tensor t = {tmp, NNC_DTYPE_FLOAT32, shape, 4, (int64_t)(n * 4)};
+    nnc_hip_conv_packed(in, w, b, NULL, &t, kh, kw, sh, sw, ph, pw, 1);
+    nnc_maxpool2d(&t, out, 3, 3, 2, 2, 1, 1);
+    free(tmp);
+}

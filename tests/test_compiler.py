@@ -302,3 +302,34 @@ def test_gap_gemm_tile_streaming_pass(pkg):
         assert passes.stream_tiles(g, lds_budget=4 * 512 * 50) == 0  # over the budget
     finally:
         passes.GAP_GEMM_MAX_BATCH = old
+
+
+def test_conv_pool_tile_streaming_pass(pkg, oracle_lib):
+    """stream_tiles with the stem fusion allowed: the packed stem conv +
+    relu and its 3x3 / s2 / p1 max pool become one FusedConvMaxPool lowered
+    to nnc_hip_conv_maxpool (the 112 x 112 activation gone); on the oracle
+    the program computes the unfused program's bits (the same conv, relu and
+    max). Below the batch limit, or by default, the pair stays."""
+    from nnc_py_amd.compiler import Executor, build_program, passes, zoo
+    assert build_program(zoo.resnet18(batch=2, seed=0), opt_level=3).calls[0].op == "nnc_hip_conv_packed"
+    old = passes.CONV_POOL_MIN_BATCH
+    passes.CONV_POOL_MIN_BATCH = 2
+    try:
+        prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
+        small = build_program(zoo.resnet18(batch=1, seed=0), opt_level=3)
+    finally:
+        passes.CONV_POOL_MIN_BATCH = old
+    ops = [c.op for c in prog.calls]
+    assert ops[0] == "nnc_hip_conv_maxpool" and "nnc_maxpool2d" not in ops and len(ops) == 19
+    assert [a[1] for a in prog.calls[0].args[4:]] == [7, 7, 2, 2, 3, 3]
+    node = prog.order[0]
+    assert node.op_type == "FusedConvMaxPool" and node.metadata["tile_stream"]["hbm_bytes_saved"] == 2 * 2 * 64 * 112 * 112 * 4
+    assert small.calls[0].op == "nnc_hip_conv_packed"
+    x = np.random.default_rng(4).standard_normal((2, 3, 224, 224)).astype(np.float32)
+    outs = []
+    for p in (prog, build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)):
+        ex = Executor(p, device=False, lib=oracle_lib)
+        ex.set_input("input", x)
+        ex.run()
+        outs.append(ex.get("output"))
+    assert outs[0].tobytes() == outs[1].tobytes()

@@ -470,3 +470,49 @@ def test_gap_gemm_nt_rejections(hip, dmem, abi):
                                  "outputs": ["out"]}, abi, dmem)["out"]
     assert runtime.last_error()[0] == 1 and not out.any()
     runtime.clear_error()
+
+
+def _conv_maxpool_case(rng, n, h, w, co=64, bias=True):
+    """nnc_hip_conv_maxpool case: the packed RGB 7x7 / stride 2 / pad 3 stem
+    ([Co][160] rows) with relu, into the 3x3 / stride 2 / pad 1 max pool."""
+    wr = (rng.standard_normal((co, 3, 7, 7)) * np.sqrt(2.0 / 147)).astype(np.float32)
+    rows = np.zeros((co, 160), np.float32)
+    rows[:, :147] = wr.transpose(0, 2, 3, 1).reshape(co, 147)
+    ho, wo = (h + 6 - 7) // 2 + 1, (w + 6 - 7) // 2 + 1
+    tensors = {"x": rng.standard_normal((n, 3, h, w)).astype(np.float32), "w": rows,
+               "out": np.zeros((n, co, ho // 2, wo // 2), np.float32)}
+    if bias:
+        tensors["b"] = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    return {"name": f"conv_maxpool_{n}x{h}x{w}_{co}", "op": "nnc_hip_conv_maxpool", "tensors": tensors,
+            "args": [("t", "x"), ("t", "w"), ("t", "b") if bias else ("null",), ("t", "out")]
+            + [("i", v) for v in (7, 7, 2, 2, 3, 3)], "outputs": ["out"]}
+
+
+@pytest.mark.parametrize("n,h,w,co,bias", [(1, 224, 224, 64, True), (2, 64, 100, 64, True), (8, 224, 224, 64, True),
+                                           (3, 32, 255, 40, False)])
+def test_conv_maxpool_stem(n, h, w, co, bias, hip, dmem, abi, oracle_lib):
+    """The stem streamed into its max pool against the oracle's packed conv
+    + relu + nnc_maxpool2d: within the conv bar of the oracle's double sums
+    (the max itself is exact). Covers one-row and two-row bands with their
+    band-boundary fixup, a full 128-pixel row (w = 255), Co < 64."""
+    case = _conv_maxpool_case(np.random.default_rng(n + h + w), n, h, w, co, bias)
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    from nnc_py_amd import runtime
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    _check(got, exp, case["name"])
+    assert (got >= 0).all()
+
+
+def test_conv_maxpool_rejections(hip, dmem, abi):
+    """Odd conv output sizes and conv rows over 128 pixels are refused
+    before any launch; the output is untouched."""
+    from nnc_py_amd import runtime
+    for n, h, w in ((1, 37, 64), (1, 64, 270)):
+        case = _conv_maxpool_case(np.random.default_rng(1), n, h, w)
+        case["tensors"]["out"] = np.zeros_like(case["tensors"]["out"])
+        runtime.clear_error()
+        out = caserun.run_case(hip, case, abi, dmem)["out"]
+        assert runtime.last_error()[0] == 4 and not out.any(), (h, w)
+    runtime.clear_error()
