@@ -138,6 +138,37 @@ inline void launch(const char* name, Kernel kernel, dim3 grid, dim3 block, size_
     hip_ok(hipGetLastError(), name, "launch");
 }
 
+// Streaming stores. An output of at least kNtStoreBytes cannot stay
+// cache-resident for its reader anyway (MI355X's Infinity Cache is 256 MB,
+// shared with the inputs being streamed), so the streaming kernels write it
+// with non-temporal stores, which go to HBM without displacing the inputs:
+// a 205 MB device copy measured 5.2 TB/s with ordinary stores and 7.2 TB/s
+// with non-temporal ones; copies under the cache's size ran at the same
+// speed either way.
+static constexpr int64_t kNtStoreBytes = (int64_t)64 << 20;
+typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ void store_f4(float* p, float4 v) {
+    if (NT) {
+        nt_f32x4 w = {v.x, v.y, v.z, v.w};
+        __builtin_nontemporal_store(w, reinterpret_cast<nt_f32x4*>(p));
+    } else {
+        *reinterpret_cast<float4*>(p) = v;
+    }
+}
+
+template <bool NT>
+__device__ __forceinline__ void store_u4(uint4* p, uint4 v) {
+    if (NT) {
+        nt_u32x4 w = {v.x, v.y, v.z, v.w};
+        __builtin_nontemporal_store(w, reinterpret_cast<nt_u32x4*>(p));
+    } else {
+        *p = v;
+    }
+}
+
 // Copy `bytes` bytes device-to-device on the library stream with a kernel
 // (16-byte vector path when aligned; no memset/memcpy nodes under capture).
 // src == dst is a no-op. Defined in movement.hip.

@@ -71,7 +71,7 @@ __global__ void __launch_bounds__(256) binary_scalar_k(const float* __restrict__
 
 // n4 float4 groups starting at element 0; a modulo period must be a multiple
 // of 4 so a group never wraps.
-template <int OP, int AM, int BM>
+template <int OP, int AM, int BM, bool NT>
 __global__ void __launch_bounds__(256) binary_vec4_k(const float* __restrict__ a,
                                                      const float* __restrict__ b, float* out,
                                                      uint32_t n4, uint32_t an, uint32_t bn) {
@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256) binary_vec4_k(const float* __restrict__ a
         z.y = binop<OP>(x.y, y.y);
         z.z = binop<OP>(x.z, y.z);
         z.w = binop<OP>(x.w, y.w);
-        *reinterpret_cast<float4*>(out + i) = z;
+        store_f4<NT>(out + i, z);
     }
 }
 
@@ -108,8 +108,12 @@ static void launch_binary(const char* name, const float* a, const float* b, floa
     uint32_t done = 0;
     if (vec && cnt >= 4) {
         const uint32_t n4 = (uint32_t)(cnt / 4);
-        launch(name, binary_vec4_k<OP, AM, BM>, dim3(grid_for(n4, 4)), dim3(256), 0, a, b, out, n4,
-               (uint32_t)an, (uint32_t)bn);
+        if (4 * cnt >= kNtStoreBytes)
+            launch(name, binary_vec4_k<OP, AM, BM, true>, dim3(grid_for(n4, 4)), dim3(256), 0, a, b, out, n4,
+                   (uint32_t)an, (uint32_t)bn);
+        else
+            launch(name, binary_vec4_k<OP, AM, BM, false>, dim3(grid_for(n4, 4)), dim3(256), 0, a, b, out, n4,
+                   (uint32_t)an, (uint32_t)bn);
         done = n4 * 4;
     }
     if (done < cnt)
@@ -178,7 +182,7 @@ __device__ __forceinline__ float unop(float v, float lo, float hi) {
     return ref_fminf(ref_fmaxf(v, lo), hi);  // kClip
 }
 
-template <int OP>
+template <int OP, bool NT>
 __global__ void __launch_bounds__(256) unary_vec4_k(const float* x, float* out, uint32_t n4,
                                                     float lo, float hi) {
     const uint32_t stride = gridDim.x * blockDim.x;
@@ -188,7 +192,7 @@ __global__ void __launch_bounds__(256) unary_vec4_k(const float* x, float* out, 
         v.y = unop<OP>(v.y, lo, hi);
         v.z = unop<OP>(v.z, lo, hi);
         v.w = unop<OP>(v.w, lo, hi);
-        reinterpret_cast<float4*>(out)[g] = v;
+        store_f4<NT>(out + 4 * (size_t)g, v);
     }
 }
 
@@ -220,7 +224,10 @@ static void unary_entry(const char* name, Tensor* in, Tensor* out, float lo = 0.
     uint32_t done = 0;
     if (aligned16(x) && aligned16(z) && n >= 4) {
         const uint32_t n4 = (uint32_t)(n / 4);
-        launch(name, unary_vec4_k<OP>, dim3(grid_for(n4, 4)), dim3(256), 0, x, z, n4, lo, hi);
+        if (4 * n >= kNtStoreBytes)
+            launch(name, unary_vec4_k<OP, true>, dim3(grid_for(n4, 4)), dim3(256), 0, x, z, n4, lo, hi);
+        else
+            launch(name, unary_vec4_k<OP, false>, dim3(grid_for(n4, 4)), dim3(256), 0, x, z, n4, lo, hi);
         done = n4 * 4;
     }
     if (done < n)

@@ -7,14 +7,17 @@
 // Copies are kernels (not hipMemcpy) so they time like every other op and
 // record as kernel nodes under graph capture. HBM-bound: 16-byte loads and
 // stores where source, destination and size allow.
+#include <type_traits>
+
 #include "common.h"
 
 namespace nnc {
 
+template <bool NT>
 __global__ void __launch_bounds__(256) copy16_k(const uint4* src, uint4* dst, int64_t n16) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
-        dst[i] = src[i];
+        store_u4<NT>(dst + i, src[i]);
 }
 
 __global__ void __launch_bounds__(256) copy1_k(const uint8_t* src, uint8_t* dst, int64_t n) {
@@ -31,7 +34,10 @@ void device_copy(const char* name, const void* src, void* dst, size_t bytes) {
     size_t done = 0;
     if (aligned16(s) && aligned16(d) && bytes >= 16) {
         const int64_t n16 = (int64_t)(bytes / 16);
-        launch(name, copy16_k, dim3(grid_for(n16, 2)), dim3(256), 0, (const uint4*)s, (uint4*)d, n16);
+        if ((int64_t)bytes >= kNtStoreBytes)
+            launch(name, copy16_k<true>, dim3(grid_for(n16, 2)), dim3(256), 0, (const uint4*)s, (uint4*)d, n16);
+        else
+            launch(name, copy16_k<false>, dim3(grid_for(n16, 2)), dim3(256), 0, (const uint4*)s, (uint4*)d, n16);
         done = (size_t)n16 * 16;
     }
     if (done < bytes)
@@ -89,42 +95,54 @@ __global__ void __launch_bounds__(256) transpose2d_k(const float* in, float* out
 // ---------------------------------------------------------------------------
 // grid (ceil(slab / 256), rows): one element per thread, 32-bit index
 // within a row, rows strided by grid.y; no per-element division
-template <typename E>
+template <typename E, bool NT>
 __global__ void __launch_bounds__(256) slab_copy_k(const E* src, int64_t src_row, E* dst,
                                                    int64_t dst_row, int64_t outer, uint32_t slab) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= slab) return;
-    for (int64_t o = blockIdx.y; o < outer; o += gridDim.y) dst[o * dst_row + i] = src[o * src_row + i];
+    for (int64_t o = blockIdx.y; o < outer; o += gridDim.y) {
+        if constexpr (NT && std::is_same<E, uint4>::value)
+            store_u4<true>(dst + o * dst_row + i, src[o * src_row + i]);
+        else
+            dst[o * dst_row + i] = src[o * src_row + i];
+    }
 }
 
+// `nt`: non-temporal stores (a large total output, kNtStoreBytes)
 template <typename E>
 static void slab_launch(const char* name, const E* src, int64_t src_row, E* dst, int64_t dst_row, int64_t outer,
-                        int64_t slab) {
+                        int64_t slab, bool nt) {
     if (slab >= ((int64_t)1 << 32) - 256) {
         // rows longer than 2^32 elements: one launch per 2^31-element chunk
         const int64_t chunk = (int64_t)1 << 31;
         for (int64_t c = 0; c < slab; c += chunk)
-            slab_launch(name, src + c, src_row, dst + c, dst_row, outer, slab - c < chunk ? slab - c : chunk);
+            slab_launch(name, src + c, src_row, dst + c, dst_row, outer, slab - c < chunk ? slab - c : chunk, nt);
         return;
     }
     const int64_t gy = outer < 65535 ? outer : 65535;
-    launch(name, slab_copy_k<E>, dim3((unsigned)ceil_div(slab, 256), (unsigned)gy), dim3(256), 0, src, src_row,
-           dst, dst_row, outer, (uint32_t)slab);
+    const dim3 grid((unsigned)ceil_div(slab, 256), (unsigned)gy);
+    if (nt)
+        launch(name, slab_copy_k<E, true>, grid, dim3(256), 0, src, src_row, dst, dst_row, outer, (uint32_t)slab);
+    else
+        launch(name, slab_copy_k<E, false>, grid, dim3(256), 0, src, src_row, dst, dst_row, outer, (uint32_t)slab);
 }
 
+// `total_out_bytes`: the whole output the caller's copies fill (a concat's
+// or a split's), which decides the store kind
 template <typename E>
 static void slab_copy(const char* name, const void* src, int64_t src_row, void* dst, int64_t dst_row,
-                      int64_t outer, int64_t slab) {
+                      int64_t outer, int64_t slab, int64_t total_out_bytes) {
     if (outer * slab == 0) return;
     set_work(0.0, 2.0 * (double)(outer * slab) * sizeof(E));
+    const bool nt = total_out_bytes >= kNtStoreBytes;
     // 16-byte granules when every row start stays aligned
     const int64_t per16 = 16 / (int64_t)sizeof(E);
     if (aligned16(src) && aligned16(dst) && slab % per16 == 0 && src_row % per16 == 0 &&
         dst_row % per16 == 0) {
-        slab_launch(name, (const uint4*)src, src_row / per16, (uint4*)dst, dst_row / per16, outer, slab / per16);
+        slab_launch(name, (const uint4*)src, src_row / per16, (uint4*)dst, dst_row / per16, outer, slab / per16, nt);
         return;
     }
-    slab_launch(name, (const E*)src, src_row, (E*)dst, dst_row, outer, slab);
+    slab_launch(name, (const E*)src, src_row, (E*)dst, dst_row, outer, slab, false);
 }
 
 // ---------------------------------------------------------------------------
@@ -376,8 +394,9 @@ void nnc_concat(Tensor** ins, Tensor* out, int n_in, int axis) {
         const int64_t slab = ins[t]->shape[axis] * inner;
         if (col + slab > out_row) return fail(NNC_HIP_EINVAL, name, "inputs exceed the output axis");
         char* dst = (char*)out->data + col * (i64 ? 8 : 4);
-        if (i64) slab_copy<int64_t>(name, ins[t]->data, slab, dst, out_row, outer, slab);
-        else slab_copy<float>(name, ins[t]->data, slab, dst, out_row, outer, slab);
+        const int64_t total = outer * out_row * (i64 ? 8 : 4);
+        if (i64) slab_copy<int64_t>(name, ins[t]->data, slab, dst, out_row, outer, slab, total);
+        else slab_copy<float>(name, ins[t]->data, slab, dst, out_row, outer, slab, total);
         col += slab;
     }
 }
@@ -397,8 +416,9 @@ void nnc_split(Tensor* in, Tensor** outs, int n_out, int axis) {
         if (!has_data(outs[t])) return fail(NNC_HIP_EINVAL, name, "bad output %d", t);
         if (numel(outs[t]) < outer * part * inner) return fail(NNC_HIP_EINVAL, name, "output %d too small", t);
         const char* src = (const char*)in->data + t * part * inner * (i64 ? 8 : 4);
-        if (i64) slab_copy<int64_t>(name, src, dim * inner, outs[t]->data, part * inner, outer, part * inner);
-        else slab_copy<float>(name, src, dim * inner, outs[t]->data, part * inner, outer, part * inner);
+        const int64_t total = outer * dim * inner * (i64 ? 8 : 4);
+        if (i64) slab_copy<int64_t>(name, src, dim * inner, outs[t]->data, part * inner, outer, part * inner, total);
+        else slab_copy<float>(name, src, dim * inner, outs[t]->data, part * inner, outer, part * inner, total);
     }
 }
 
