@@ -91,7 +91,7 @@ def kernel_table(ex, runtime, steps: int) -> list[dict]:
     rows = []
     for r in table:
         avg_ms = r["ms"] / r["launches"]
-        if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma")):
+        if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma", "gemm_dma")):
             bound, unit, peak = "mfma", "TFLOP/s", PEAK_FP32_MFMA_TF
             achieved = r["flops"] / (r["ms"] * 1e-3) / 1e12
         elif r["name"].endswith("_fixup"):
@@ -189,6 +189,9 @@ def conv_symbol_pattern(name: str) -> re.Pattern | None:
     m = re.fullmatch(r"gemm_mfma_(\d+)x(\d+)_\w+", name)
     if m:
         return re.compile(rf"gemm_streamk_k<nnc::Tile<{m.group(1)}, {m.group(2)},")
+    m = re.fullmatch(r"gemm_dma_(\d+)x(\d+)_\w+", name)
+    if m:
+        return re.compile(rf"gemm_dma_k<nnc::Tile<{m.group(1)}, {m.group(2)},")
     return None
 
 
@@ -286,7 +289,7 @@ def _op_roofline(runtime, fn, reps: int = 10, warmup: int = 3) -> dict:
     nbytes = sum(r["bytes"] for r in table) / reps
     mfma = False
     for r in table:
-        if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma")):
+        if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma", "gemm_dma")):
             achieved, unit, peak = r["flops"] / (r["ms"] * 1e-3) / 1e12, "TFLOP/s", PEAK_FP32_MFMA_TF
             mfma = True
         else:

@@ -210,18 +210,6 @@ __device__ __forceinline__ void fixup_store(const ConvArgs& a, int co, int p0, f
     fixup_apply(a, co, p0, v, fixup_load(a, co, p0));
 }
 
-// Partial tiles are written and read with device-scope coherence (the
-// buffer instructions' sc1 bit: stores write through the XCD's L2, loads do
-// not hit a stale L2 line), so the workgroup that finishes a tile on another
-// XCD sees them once their writers' stores have completed - without an L2
-// writeback or invalidate.
-static constexpr int kDeviceScope = 16;
-
-template <class T>
-__device__ __forceinline__ uint32_t slot_byte_offset(int g, int which) {
-    return (uint32_t)((g * 2 + which) * (T::BM * T::BN)) * 4u;
-}
-
 // Shared stream-K tile t finished inside the kernel by the workgroup whose
 // partial arrived last: partials summed in workgroup order g0..g1 (the
 // order of conv_fixup_k, so the result is the same to the bit), then bias
@@ -470,24 +458,6 @@ struct DmaStage {
     static_assert(T::NW % PX_GROUPS == 0 && B_LOADS % 2 == 0, "B rows split evenly over the waves");
     static_assert(T::BM % 32 == 0 && (T::BN == 64 || T::BN == 128) && T::BK == 32, "dma tile");
 };
-
-typedef __attribute__((address_space(3))) void* lds_ptr;
-__device__ __forceinline__ void dma_load4(__amdgpu_buffer_rsrc_t r, float* lds_dst, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_dst, 4, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, float* lds_dst, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_dst, 16, voff, soff, 0, 0);
-}
-
-// s_waitcnt vmcnt(0): the direct-to-LDS loads of this wave have landed
-__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// `addr` if `keep`, else exactly kOutOfRange (adding an SGPR offset below
-// 2^31 cannot wrap it back into range); without branches
-__device__ __forceinline__ uint32_t keep_or_oob(uint32_t addr, bool keep) {
-    const uint32_t m = 0u - (uint32_t)keep;
-    return (addr & m) | (kOutOfRange & ~m);
-}
 
 // Per-tile pixel data of the B loaders: this lane's pixel (one per wave's
 // 64-pixel group), element offset of its tap (0, 0) at channel 0, and the
@@ -1186,16 +1156,11 @@ __global__ void __launch_bounds__(256) repack_taps_k(const float* w, float* wp, 
 static constexpr bool kInKernelFixup = true;
 // reference-layout 3x3 convolutions from this much work on are repacked
 static constexpr double kRepackMinFlops = 1e9;
-#ifndef NNC_CONV_FIN_MAX_PARTS
-#define NNC_CONV_FIN_MAX_PARTS 4
-#endif
-static constexpr int kMaxInKernelParts = NNC_CONV_FIN_MAX_PARTS;
+static constexpr int kMaxInKernelParts = 4;
 // 128x128 direct-to-LDS tiles finish shared tiles in-kernel too (off: on
 // ResNet-18's batch-32 layers it measured 62.0 -> 69.0 us per launch, the
 // finishing workgroups' partial reads sit on the kernel's critical path)
-#ifndef NNC_CONV_FIN128
-#define NNC_CONV_FIN128 0
-#endif
+static constexpr bool kFinish128 = false;
 
 typedef Tile<128, 128, 32, 2, 2> ConvT128;  // Co >= 128: 2x2 blocks per wave
 typedef Tile<64, 128, 32, 1, 4> ConvT64;    // Co == 64, many pixels: 2x1 blocks per wave
@@ -1246,7 +1211,7 @@ static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) 
     // kernel (64x128 tiles: ResNet's 64-channel layers and the stem);
     // elsewhere its code costs the main loop registers
     constexpr bool FIN = kInKernelFixup && L::kFinishInKernel && T::NW == 4 &&
-                         ((T::BM == 64 && T::BN == 128) || (NNC_CONV_FIN128 && T::BM == 128 && T::BN == 128));
+                         ((T::BM == 64 && T::BN == 128) || (kFinish128 && T::BM == 128 && T::BN == 128));
     auto kernel = conv_dma_k<T, L, FIN>;
     const size_t lds = (size_t)(DmaStage<T>::LDS_FLOATS + L::EXTRA_LDS_FLOATS) * sizeof(float);
     // once per kernel, thread-safe (C++ static initialisation): the LDS limit

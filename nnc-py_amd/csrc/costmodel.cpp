@@ -71,8 +71,9 @@ const MfmaKind kStem64 = {"stem_64", 64, 64, 4, 0.30, 1.43};
 const MfmaKind kGather128 = {"conv_gather_128", 128, 128, 2, 0.60, 0.6};
 const MfmaKind kGather64x128 = {"conv_gather_64x128", 64, 128, 3, 0.52, 4.0};
 const MfmaKind kGather64 = {"conv_gather_64", 64, 64, 4, 0.48, 1.2};
-const MfmaKind kGemm128 = {"gemm_128", 128, 128, 2, 0.75, 0.47};
-const MfmaKind kGemm64 = {"gemm_64", 64, 64, 4, 0.60, 1.0};
+const MfmaKind kGemm128 = {"gemm_128", 128, 128, 2, 0.75, 0.47};  // direct-to-LDS, two stages
+const MfmaKind kGemmDma64 = {"gemm_dma_64", 64, 64, 2, 0.60, 1.0};  // direct-to-LDS, four stages
+const MfmaKind kGemm64 = {"gemm_64", 64, 64, 4, 0.60, 1.0};         // register-staged
 constexpr double kColdUsPerMB = 0.061;  // weights (B operand) arriving from HBM, per MB
 constexpr double kFixupUsPerMB = 0.073; // fixup kernel: partial tiles read + finished tiles written, per MB
 constexpr double kFixupUsPerPart = 0.069; // fixup kernel: each partial summed into a tile (sequential)
@@ -164,10 +165,12 @@ struct MfmaResult {
     double us;
 };
 
-MfmaResult mfma_kernel(const MfmaKind& k, int tiles, int64_t K, double hbm_bytes, double weight_bytes) {
+// `slots`: the persistent grid's cap (0: k.per_cu workgroups per CU)
+MfmaResult mfma_kernel(const MfmaKind& k, int tiles, int64_t K, double hbm_bytes, double weight_bytes,
+                       int slots = 0) {
     const int iters = K > 0 ? (int)ceil_div(K, kBK) : 1;
     const nnc::StreamK sk =
-        nnc::plan_streamk(tiles, iters, k.per_cu * kCUs, nnc::fixup_slices_for(k.bm, k.bn));
+        nnc::plan_streamk(tiles, iters, slots > 0 ? slots : k.per_cu * kCUs, nnc::fixup_slices_for(k.bm, k.bn));
     const int G = sk.G < 1 ? 1 : sk.G;
     const int r = (int)ceil_div(G, kCUs);
     const double cu_rate = kMfmaF32 / kCUs;
@@ -266,10 +269,25 @@ void gemm(const char* op, int M, int N, int K, int batches, bool a_kc, bool b_kc
     const bool a4 = a_kc ? K % 4 == 0 : M % 4 == 0;  // 16-byte loads along the contiguous axis
     const bool b4 = b_kc ? K % 4 == 0 : N % 4 == 0;
     const bool big = (int64_t)M * N * batches >= (int64_t)128 * 128 * 2 * kCUs / 4 && M >= 128 && N >= 128;
-    const MfmaKind& k = (big && a4 && b4) ? kGemm128 : kGemm64;
     static const char* kinds[4] = {"k4", "k1", "x4", "x1"};
     const int ak = a_kc ? (a4 ? 0 : 1) : (a4 ? 2 : 3), bk = b_kc ? (b4 ? 0 : 1) : (b4 ? 2 : 3);
     char name[64];
+    if (a4 && b4) {
+        // direct-to-LDS: 128x128 or 64x64 tiles (one workgroup per CU over
+        // 16 or more K slices); shared tiles of at most four partials are
+        // finished in-kernel
+        const MfmaKind& k = big ? kGemm128 : kGemmDma64;
+        snprintf(name, sizeof name, "gemm_dma_%dx%d_%s%s", k.bm, k.bn, kinds[ak], kinds[bk]);
+        const int tiles = (int)(ceil_div(M, k.bm) * ceil_div(N, k.bn) * batches);
+        const int iters = (int)ceil_div(K, kBK);
+        MfmaResult m = mfma_kernel(k, tiles, K, bytes, b_bytes, !big && iters >= 16 ? kCUs : 0);
+        record(op, name, m.us, flops, bytes);
+        if (!m.sk.needs_fixup()) return;
+        const int64_t per = m.sk.total() / m.sk.G;
+        if ((m.sk.iters + per - 1) / per + 1 <= kMaxInKernelParts) return;
+        return record(op, "gemm_streamk_fixup", fixup_us(k, m.sk), 0.0, 0.0);
+    }
+    const MfmaKind& k = kGemm64;
     snprintf(name, sizeof name, "gemm_mfma_%dx%d_%s%s", k.bm, k.bn, kinds[ak], kinds[bk]);
     const int tiles = (int)(ceil_div(M, k.bm) * ceil_div(N, k.bn) * batches);
     MfmaResult m = mfma_kernel(k, tiles, K, bytes, b_bytes);
@@ -566,9 +584,10 @@ void nnc_gemm_nt(Tensor* a, Tensor* b, Tensor* c, Tensor* out, float alpha, floa
 // ---- pools ----------------------------------------------------------------------
 void nnc_maxpool2d(Tensor* in, Tensor* out, int kh, int kw, int sh, int sw, int ph, int pw) {
     (void)kh, (void)kw, (void)sh, (void)sw, (void)ph, (void)pw;
-    // one wave walks 8 output rows: about 5 us of dependent loads at any size
+    // streaming (MI355X: 4.7 us at ResNet-18 batch 1, 8.4 at batch 8, 26.4 at
+    // batch 32)
     if (in && out && numel(out) > 0)
-        stream_kernel("nnc_maxpool2d", "nnc_maxpool2d", nbytes(in) + nbytes(out), kStreamEff, 5.0);
+        stream_kernel("nnc_maxpool2d", "nnc_maxpool2d", nbytes(in) + nbytes(out), kStreamEff, 1.0);
 }
 void nnc_avgpool2d(Tensor* in, Tensor* out, int kh, int kw, int sh, int sw, int ph, int pw) {
     (void)sh, (void)sw, (void)ph, (void)pw;

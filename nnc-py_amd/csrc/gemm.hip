@@ -1,10 +1,14 @@
 // Gemm, Gemm_nt and MatMul of the nnc ABI (runtime/x86/ops.c:1607-1886).
 //
-// Dense products run on the fp32 MFMA tile engine (mfma_tile.h) with one of
-// four operand layouts per side (k-contiguous or x-contiguous, 16-byte or
-// scalar loads), stream-K scheduled over batches x tiles x K slices (a
-// fixup kernel applies the epilogue to tiles shared between workgroups, in
-// fixed workgroup order). Products with one
+// Dense products run on the fp32 MFMA tile engine (mfma_tile.h), stream-K
+// scheduled over batches x tiles x K slices. Operands whose rows are 16-byte
+// aligned on both sides (k-contiguous or x-contiguous) go straight from
+// global memory into LDS (gemm_dma_k: 64x64 tiles with four LDS stages,
+// 128x128 tiles with two); shared tiles are finished inside the kernel by
+// the last workgroup to arrive, or by a fixup kernel when split further.
+// Other layouts (unaligned rows, K or M/N not a multiple of 4) stage through
+// registers (gemm_streamk_k, scalar loads where needed). Both sum a shared
+// tile's partials in fixed workgroup order. Products with one
 // output row or column are HBM-bound and use dedicated kernels:
 //   gemv_xc_k  out[j] = sum_k a[k] * B[k][j]   (B row-major; float4 columns,
 //              K split across workgroups, deterministic partial reduction)
@@ -12,13 +16,18 @@
 //              wave per output, shuffle reduction)
 //
 // The reference accumulates Gemm in fp64 and MatMul with a Kahan fp32 sum;
-// here every product accumulates in fp32 (two-level for MFMA tiles), within
-// the 1e-4 absolute / 1e-3 relative bar.
+// here every product accumulates in fp32 (two-level in the register-staged
+// kernel), within the 1e-4 absolute / 1e-3 relative bar.
 //
 // DIVERGES: batched MatMul steps A by M*K and B by K*N per batch (numpy /
 // ONNX semantics). The reference steps by the batch count (ops.c:1687-1704),
 // which is only correct for a single batch.
 #include "mfma_tile.h"
+
+#include <stdlib.h>
+
+#include <algorithm>
+#include <type_traits>
 
 namespace nnc {
 
@@ -34,6 +43,7 @@ struct GemmArgs {
     int c_mode;  // 0 none, 1 C[j], 2 C[i*N + j]
     int relu;
     int tiles_m, tiles_n, splits;  // splits: K-split count of the GEMV path
+    int* cnt;  // stream-K tile counters of the in-kernel finish, or null
     int out32;  // one batch of out (and C) below 2 GiB: whole tiles use 32-bit buffer offsets
 };
 
@@ -197,6 +207,337 @@ __global__ void __launch_bounds__(256) gemm_fixup_k(GemmArgs g, StreamK sk) {
         if (j + q < g.N) o[j + q] = gemm_finish(g, i, j + q, vals[q]);
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS GEMM: operands go from global memory straight into LDS
+// (`buffer_load ... lds`), 16 bytes per lane: no VGPR staging and no LDS
+// store instructions. A stage holds the A operand (BM x 32 k) then the B
+// operand (BN x 32 k), each in one of two layouts:
+//   KC  (element (x, k) at base[x*ld + k]: A row-major, B stored [N][K])
+//       [X rows][32 k], 16-byte chunks XOR-swizzled: chunk kc of row x sits
+//       at position kc ^ (x & 7). One load instruction covers 8 rows (lane
+//       l: row l / 8, global chunk (l % 8) ^ (row % 8)); an MFMA lane reads
+//       its four k of a quad as one ds_read_b128, eight consecutive rows on
+//       eight different bank groups.
+//   XC  (element (x, k) at base[k*ld + x]: B row-major [K][N], A stored
+//       [K][M]) [32 k][X]: one load instruction covers 256 / X rows of k
+//       (lane l: row l / (X/4), four consecutive x); an MFMA lane reads its k
+//       one ds_read_b32 at a time, 32 lanes on 32 consecutive floats.
+// Both need 16-byte aligned rows (ld % 4 == 0, aligned base and batch
+// stride); KC needs K % 4 == 0 and XC needs the tile's x extent (M or N) %
+// 4 == 0, so a 16-byte chunk is wholly inside or wholly outside the matrix
+// and out-of-range chunks get an out-of-range offset (the hardware writes 0
+// to LDS). Checked by the host.
+// ---------------------------------------------------------------------------
+template <class T, int NS>
+struct GemmDma {
+    static constexpr int A_FLOATS = T::BM * 32, B_FLOATS = T::BN * 32;
+    static constexpr int STAGE = A_FLOATS + B_FLOATS;
+    static constexpr int LDS_FLOATS = NS * STAGE;  // NS stages: NS - 1 slices in flight
+    // waves per SIMD that the LDS stages allow (160 KB per CU), at most 4:
+    // the register budget the kernel is compiled for
+    static constexpr int LDS_WAVES = (160 * 1024 / (LDS_FLOATS * 4)) * T::NW / 4;
+    static constexpr int MIN_WAVES = LDS_WAVES < 2 ? 2 : (LDS_WAVES > 4 ? 4 : LDS_WAVES);
+    static_assert(T::BK == 32 && T::NW == 4 && NS >= 2, "direct-to-LDS gemm tile");
+};
+
+template <class T, int X, int OFF>
+struct KcOperand {
+    static constexpr int LOADS = X / (8 * T::NW);  // load instructions per wave per slice
+    static_assert(X % (8 * T::NW) == 0, "rows split evenly over the waves");
+    static __device__ int64_t origin(int x0, int64_t ld) { return (int64_t)x0 * ld; }
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t vo[LOADS];  // this lane's byte offset from the tile origin, or kOutOfRange
+    int kc4;             // k of this lane's chunk within a slice
+    int rb, sw;          // read side: LDS offset of this lane's row, swizzle of its k-half
+    __device__ void init_read(int xw, int lane) {
+        rb = OFF + (xw + (lane & 31)) * 32;
+        sw = (4 * (lane >> 5)) ^ (lane & 7);
+    }
+    __device__ void tile(const float* base, int64_t ld, int xlim, int wave, int lane) {
+        r = make_rsrc(base);
+        const int kc = (lane & 7) ^ ((lane >> 3) & 7);
+        kc4 = 4 * kc;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int x = (wave + T::NW * i) * 8 + (lane >> 3);
+            vo[i] = keep_or_oob((uint32_t)(x * ld) * 4u + (uint32_t)kc * 16u, x < xlim);
+        }
+    }
+    __device__ void issue(float* S, int wave, int k0, int K, bool on) const {
+        const bool in = on && k0 + kc4 < K;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i)
+            dma_load16(r, S + OFF + (wave + T::NW * i) * 8 * 32, in ? vo[i] : kOutOfRange, (uint32_t)k0 * 4u);
+    }
+    template <int N>
+    __device__ void read(const float* S, int q, f32x4 (&v)[N]) const {
+#pragma unroll
+        for (int t = 0; t < N; ++t) v[t] = *reinterpret_cast<const f32x4*>(S + rb + t * 32 * 32 + ((sw ^ q) << 2));
+    }
+};
+
+template <class T, int X, int OFF>
+struct XcOperand {
+    static constexpr int RP = 256 / X;                // k rows per load instruction
+    static constexpr int LOADS = 32 / (RP * T::NW);  // load instructions per wave per slice
+    static_assert(32 % (RP * T::NW) == 0, "k rows split evenly over the waves");
+    static __device__ int64_t origin(int x0, int64_t) { return x0; }
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t vo[LOADS];
+    uint32_t ld4;  // row pitch in bytes
+    int kr0;       // this lane's k row (within a slice) in its first load
+    int rb;        // read side: LDS offset of this lane's column in its k-half
+    __device__ void init_read(int xw, int lane) { rb = OFF + 16 * (lane >> 5) * X + xw + (lane & 31); }
+    __device__ void tile(const float* base, int64_t ld, int xlim, int wave, int lane) {
+        r = make_rsrc(base);
+        ld4 = (uint32_t)ld * 4u;
+        const int xx = 4 * (lane % (X / 4));
+        kr0 = wave * LOADS * RP + lane / (X / 4);
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i)
+            vo[i] = keep_or_oob((uint32_t)(kr0 + i * RP) * ld4 + (uint32_t)xx * 4u, xx < xlim);
+    }
+    __device__ void issue(float* S, int wave, int k0, int K, bool on) const {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const bool in = on && k0 + kr0 + i * RP < K;
+            dma_load16(r, S + OFF + (wave * LOADS + i) * RP * X, in ? vo[i] : kOutOfRange, (uint32_t)k0 * ld4);
+        }
+    }
+    template <int N>
+    __device__ void read(const float* S, int q, f32x4 (&v)[N]) const {
+#pragma unroll
+        for (int t = 0; t < N; ++t)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) v[t][s] = S[rb + (4 * q + s) * X + t * 32];
+    }
+};
+
+// Shared stream-K tile t finished by the workgroup whose partial arrived
+// last: partials summed in workgroup order g0..g1 (the order of
+// gemm_fixup_k, so the result is the same to the bit), then alpha / beta * C
+// / relu. Each thread handles 4 consecutive columns of a tile row.
+template <class T>
+__device__ void gemm_finish_tile(const GemmArgs& g, int t, int g0, int g1, int first_slot) {
+    constexpr int E = T::BM * T::BN / 1024;  // float4 per thread
+    constexpr int CH = E < 4 ? E : 4;         // float4 in flight per partial (register budget)
+    const __amdgpu_buffer_rsrc_t rws = make_rsrc(g.ws);
+    const int per_batch = g.tiles_m * g.tiles_n;
+    const int batch = t / per_batch, rem = t - batch * per_batch;
+    const int i0 = (rem % g.tiles_m) * T::BM, j0 = (rem / g.tiles_m) * T::BN;
+    const uint32_t first = slot_byte_offset<T>(g0, first_slot);
+    for (int e0 = 0; e0 < E; e0 += CH) {
+        f32x4 v[CH];
+#pragma unroll
+        for (int e = 0; e < CH; ++e)
+            v[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rws, (int)(first + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u), 0,
+                                                 kDeviceScope));
+        for (int w = g0 + 1; w <= g1; ++w) {
+            const uint32_t base = slot_byte_offset<T>(w, 0);
+            f32x4 p[CH];
+#pragma unroll
+            for (int e = 0; e < CH; ++e)
+                p[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rws, (int)(base + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u),
+                                                     0, kDeviceScope));
+#pragma unroll
+            for (int e = 0; e < CH; ++e) v[e] += p[e];
+        }
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            const int e4 = (e0 + e) * 256 + threadIdx.x;
+            const int i = i0 + (e4 * 4) / T::BN;
+            const int j = j0 + (e4 * 4) % T::BN;
+            if (i >= g.M || j >= g.N) continue;
+            float* o = g.out + batch * g.so + (int64_t)i * g.N;
+            const f32x4 x = v[e];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (j + q < g.N) o[j + q] = gemm_finish(g, i, j + q, x[q]);
+        }
+    }
+}
+
+// A finished segment: a whole tile to the output, or a partial tile to the
+// workgroup's slot. With tile counters (g.cnt) each writer of a partial then
+// counts itself in, and the last to arrive finishes the tile (no workgroup
+// waits for another) and returns the counter to zero.
+template <class T, bool FIN>
+__device__ __forceinline__ void gemm_segment_out(const GemmArgs& g, const StreamK& sk, const Segment& seg, int wg,
+                                                 int batch, int i0, int j0, const floatx16 (&sum)[T::TM][T::TN]) {
+    if (T::BM * T::BN < 128 * 128 && seg.slot < 0 && g.out32) {
+        gemm_store_tile<T>(g, batch, i0, j0, sum);
+        return;
+    }
+    if (seg.slot < 0) {
+#pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn) {
+            const int j = j0 + acc_col<T>(tn);
+            if (j >= g.N) continue;
+#pragma unroll
+            for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int i = i0 + acc_row<T>(tm, r);
+                    if (i < g.M) g.out[batch * g.so + (int64_t)i * g.N + j] = gemm_finish(g, i, j, sum[tm][tn][r]);
+                }
+        }
+        return;
+    }
+    if (!FIN || !g.cnt) {  // the fixup kernel reads the partials after this kernel
+        float* slot = partial_slot<T>(g.ws, wg, seg.slot);
+#pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) slot[acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)] = sum[tm][tn][r];
+        return;
+    }
+    if constexpr (FIN) {
+        const __amdgpu_buffer_rsrc_t rws = make_rsrc(g.ws);
+        const uint32_t base = slot_byte_offset<T>(wg, seg.slot);
+#pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float x = sum[tm][tn][r];
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(x), rws,
+                        (int)(base + (uint32_t)(acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)) * 4u), 0, kDeviceScope);
+                }
+        __shared__ int last;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int g0, g1, first_slot;
+            tile_partials(sk, seg.tile, g0, g1, first_slot);
+            const int old = __hip_atomic_fetch_add(g.cnt + seg.tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = old == g1 - g0;
+            if (last) __hip_atomic_store(g.cnt + seg.tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (last) {
+            int g0, g1, first_slot;
+            tile_partials(sk, seg.tile, g0, g1, first_slot);
+            gemm_finish_tile<T>(g, seg.tile, g0, g1, first_slot);
+        }
+    }
+}
+
+// A workgroup's slices in order, across its segments (stream-K range, then
+// whole tiles).
+struct SliceCursor {
+    SegmentWalker walk;
+    Segment seg;
+    int it;
+    bool valid;
+    __device__ SliceCursor(const StreamK& sk, int wg) : walk(sk, wg) {
+        valid = walk.next(sk, seg);
+        it = seg.kb;
+    }
+    // to the next slice; true if it starts a new segment
+    __device__ bool advance(const StreamK& sk) {
+        if (++it < seg.ke) return false;
+        valid = walk.next(sk, seg);
+        it = seg.kb;
+        return valid;
+    }
+};
+
+// Stream-K over batches x tiles x K slices, NS LDS stages: the loads run
+// NS - 1 slices ahead of the MFMAs, across segment boundaries (a load cursor
+// walks the workgroup's slices ahead of the compute cursor, so a new tile
+// starts with its first slices already in LDS). Each slice is one wait and
+// one barrier: the wait leaves at most (NS - 2) x L vector memory operations
+// outstanding. Loads complete in issue order, so at least the oldest slice's
+// L loads have landed even with an epilogue's stores among the outstanding
+// operations (the count can reach the bound only after L + (stores) of them
+// completed, and at most (stores) of those were stores). Products accumulate
+// in fp32 straight into the tile's accumulators.
+template <class T, int NS, class OA, class OB, bool FIN>
+__global__ void __launch_bounds__(T::THREADS, (GemmDma<T, NS>::MIN_WAVES)) gemm_dma_k(GemmArgs g, StreamK sk) {
+    typedef GemmDma<T, NS> D;
+    constexpr int L = OA::LOADS + OB::LOADS;  // load instructions per wave per slice
+    extern __shared__ __align__(16) float lds[];
+    const int wg = xcd_remap(blockIdx.x, sk.G);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int per_batch = g.tiles_m * g.tiles_n;
+    OA oa;
+    OB ob;
+    oa.init_read((wave / T::WN) * T::WAVE_M, lane);
+    ob.init_read((wave % T::WN) * T::WAVE_N, lane);
+    auto set_tile = [&](int tile) {
+        const int batch = tile / per_batch, rem = tile - batch * per_batch;
+        const int i0 = (rem % g.tiles_m) * T::BM, j0 = (rem / g.tiles_m) * T::BN;
+        oa.tile(g.A + batch * g.sa + OA::origin(i0, g.lda), g.lda, g.M - i0, wave, lane);
+        ob.tile(g.B + batch * g.sb + OB::origin(j0, g.ldb), g.ldb, g.N - j0, wave, lane);
+    };
+    SliceCursor lc(sk, wg);  // load cursor
+    if (!lc.valid) return;
+    SegmentWalker walk(sk, wg);  // compute cursor
+    Segment seg;
+    walk.next(sk, seg);
+    set_tile(lc.seg.tile);
+    // slices 0 .. NS-2 into stages 0 .. NS-2 (past the end: out-of-range
+    // loads, which keep the wait counts uniform)
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+        oa.issue(lds + s * D::STAGE, wave, lc.it * T::BK, g.K, lc.valid);
+        ob.issue(lds + s * D::STAGE, wave, lc.it * T::BK, g.K, lc.valid);
+        if (lc.valid && lc.advance(sk)) set_tile(lc.seg.tile);
+    }
+    dma_barrier<(NS - 2) * L>();
+    // operands of quads 0 and 2 in set 0, quads 1 and 3 in set 1
+    f32x4 a0[T::TM], b0[T::TN], a1[T::TM], b1[T::TN];
+    oa.read(lds, 0, a0);
+    ob.read(lds, 0, b0);
+    int cs = 0, ls = NS - 1;  // stages being computed and loaded
+    while (true) {
+        const int batch = seg.tile / per_batch, rem = seg.tile - batch * per_batch;
+        const int i0 = (rem % g.tiles_m) * T::BM, j0 = (rem / g.tiles_m) * T::BN;
+        floatx16 sum[T::TM][T::TN];
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sum[tm][tn][r] = 0.f;
+        for (int it = seg.kb; it < seg.ke; ++it) {
+            float* ld_stage = lds + ls * D::STAGE;
+            const float* S = lds + cs * D::STAGE;
+            const int cn = cs + 1 == NS ? 0 : cs + 1;
+            oa.issue(ld_stage, wave, lc.it * T::BK, g.K, lc.valid);
+            oa.read(S, 1, a1);
+            ob.read(S, 1, b1);
+            mfma_quad<T>(a0, b0, sum);
+            ob.issue(ld_stage, wave, lc.it * T::BK, g.K, lc.valid);
+            if (lc.valid && lc.advance(sk)) set_tile(lc.seg.tile);
+            oa.read(S, 2, a0);
+            ob.read(S, 2, b0);
+            mfma_quad<T>(a1, b1, sum);
+            oa.read(S, 3, a1);
+            ob.read(S, 3, b1);
+            mfma_quad<T>(a0, b0, sum);
+            dma_barrier<(NS - 2) * L>();
+            oa.read(lds + cn * D::STAGE, 0, a0);
+            ob.read(lds + cn * D::STAGE, 0, b0);
+            mfma_quad<T>(a1, b1, sum);
+            cs = cn;
+            ls = ls + 1 == NS ? 0 : ls + 1;
+        }
+        gemm_segment_out<T, FIN>(g, sk, seg, wg, batch, i0, j0, sum);
+        if (!walk.next(sk, seg)) break;
+    }
+    // the loads issued past the last slice (out of range: they write zeros to
+    // LDS) land before the workgroup ends and its LDS is handed on
+    wait_dma();
+}
+
 // out[j] partials: thread owns 4 consecutive columns (VEC) or 1.
 template <bool VEC>
 __global__ void __launch_bounds__(256) gemv_xc_k(const float* a, int64_t a_stride, const float* B,
@@ -337,6 +678,89 @@ static void launch_mfma(GemmArgs& g, int batches, const char* name) {
     }
 }
 
+// Shared tiles with at most this many partials are finished inside the
+// direct-to-LDS kernel by the last workgroup to arrive; tiles split further
+// by gemm_fixup_k, which spreads the sum over many workgroups.
+static constexpr int kMaxInKernelParts = 4;
+
+// Clears tile counters held in fixed scratch, which keeps whatever the last
+// call on the device left there.
+__global__ void __launch_bounds__(256) gemm_zero_counters_k(int* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+// LDS stages of the direct-to-LDS kernel: 64x64 tiles have short slices
+// (16 MFMAs per wave) and keep three slices in flight; 128x128 tiles one
+template <class T>
+constexpr int dma_stages() {
+    return T::BM * T::BN < 128 * 128 ? 4 : 2;
+}
+
+// Direct-to-LDS stream-K launch; OA / OB: KcOperand or XcOperand.
+// 64x64 tiles over 16 or more K slices run one workgroup per CU: whole
+// tiles then need no partials (Gemm 1024^3 on MI355X: 29.5 us against
+// 33.6 us with two workgroups per CU, each tile split in two and finished
+// in-kernel, and 33.5 us with the separate fixup kernel); over fewer slices
+// the second workgroup per CU hides the tile's load latency (1024x768x256:
+// 10.3 against 11.3 us).
+template <class T, class OA, class OB>
+static void launch_gemm_dma(GemmArgs& g, int batches, const char* name, const char* kname) {
+    constexpr int NS = dma_stages<T>();
+    auto kernel = gemm_dma_k<T, NS, OA, OB, true>;
+    const size_t lds = (size_t)GemmDma<T, NS>::LDS_FLOATS * sizeof(float);
+    // once per kernel, thread-safe (C++ static initialisation): the LDS limit
+    // and the persistent grid size; -1 if the attribute could not be set
+    static const int slots = [&] {
+        if (hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+            return -1;
+        return resident_groups(kernel, lds, T::THREADS);
+    }();
+    if (slots < 0) return fail(NNC_HIP_EDEVICE, name, "hipFuncSetAttribute failed");
+    g.tiles_m = (int)ceil_div(g.M, T::BM);
+    g.tiles_n = (int)ceil_div(g.N, T::BN);
+    if ((int64_t)g.tiles_m * g.tiles_n * batches >= (1 << 30))
+        return fail(NNC_HIP_EUNSUPP, name, "too many output tiles");
+    const int iters = (int)ceil_div(g.K, T::BK);
+    const int use_slots = (T::BM * T::BN < 128 * 128 && iters >= 16) ? std::min(slots, cu_count()) : slots;
+    const StreamK sk = plan_streamk(g.tiles_m * g.tiles_n * batches, iters, use_slots, fixup_slices<T>());
+    if (sk.G < 1) return;
+    const size_t ws_bytes = (size_t)sk.G * 2 * T::BM * T::BN * sizeof(float);
+    g.ws = workspace(ws_bytes);
+    if (!g.ws) return partials_fail(name, ws_bytes);
+    const int64_t per = sk.total() / sk.G;  // slices per workgroup range (>= 1)
+    const bool in_kernel = sk.needs_fixup() && (sk.iters + per - 1) / per + 1 <= kMaxInKernelParts;
+    g.cnt = in_kernel ? tile_counters((size_t)sk.sk_tiles) : nullptr;
+    if (g.cnt && ts().fixed)
+        launch("zero_tile_counters", gemm_zero_counters_k, dim3((unsigned)ceil_div(sk.sk_tiles, 256)), dim3(256), 0,
+               g.cnt, (int)sk.sk_tiles);
+    set_work(2.0 * g.M * (double)g.N * g.K * batches, 0.0);
+    launch(kname, kernel, dim3(sk.G), dim3(T::THREADS), lds, g, sk);
+    if (sk.needs_fixup() && !g.cnt) {
+        set_work(0.0, 0.0);
+        launch("gemm_streamk_fixup", gemm_fixup_k<T>, dim3(T::BM * T::BN / 1024, sk.sk_tiles), dim3(256), 0, g, sk);
+    }
+}
+
+template <class T, bool A_KC, bool B_KC>
+static void launch_gemm_dma_kinds(GemmArgs& g, int batches, const char* name) {
+    typedef typename std::conditional<A_KC, KcOperand<T, T::BM, 0>, XcOperand<T, T::BM, 0>>::type OA;
+    typedef typename std::conditional<B_KC, KcOperand<T, T::BN, T::BM * 32>, XcOperand<T, T::BN, T::BM * 32>>::type
+        OB;
+    char kname[64];
+    snprintf(kname, sizeof kname, "gemm_dma_%dx%d_%s%s", T::BM, T::BN, A_KC ? "k4" : "x4", B_KC ? "k4" : "x4");
+    launch_gemm_dma<T, OA, OB>(g, batches, name, kname);
+}
+
+template <class T>
+static void dispatch_dma(GemmArgs& g, bool a_kc, bool b_kc, int batches, const char* name) {
+    if (a_kc && b_kc) return launch_gemm_dma_kinds<T, true, true>(g, batches, name);
+    if (a_kc) return launch_gemm_dma_kinds<T, true, false>(g, batches, name);
+    if (b_kc) return launch_gemm_dma_kinds<T, false, true>(g, batches, name);
+    return launch_gemm_dma_kinds<T, false, false>(g, batches, name);
+}
+
 template <int AK, int BKIND>
 static void launch_mfma_small(GemmArgs& g, int batches, const char* name) {
     launch_mfma<GemmT64, AK, BKIND>(g, batches, name);
@@ -447,11 +871,10 @@ static void gemm_run(const GemmProblem& p, const char* name) {
     const int bkind = p.b_kc ? ((b_al && p.K % 4 == 0) ? kKC4 : kKC) : ((b_al && p.N % 4 == 0) ? kXC4 : kXC);
     const bool big = (int64_t)p.M * p.N * p.batches >= (int64_t)128 * 128 * 2 * cu_count() / 4 &&
                      p.M >= 128 && p.N >= 128;
-    if (big && (akind == kKC4 || akind == kXC4) && (bkind == kKC4 || bkind == kXC4)) {
-        if (akind == kKC4 && bkind == kKC4) return launch_mfma<GemmT128, kKC4, kKC4>(g, p.batches, name);
-        if (akind == kKC4 && bkind == kXC4) return launch_mfma<GemmT128, kKC4, kXC4>(g, p.batches, name);
-        if (akind == kXC4 && bkind == kKC4) return launch_mfma<GemmT128, kXC4, kKC4>(g, p.batches, name);
-        return launch_mfma<GemmT128, kXC4, kXC4>(g, p.batches, name);
+    // 16-byte rows on both sides: direct-to-LDS staging
+    if ((akind == kKC4 || akind == kXC4) && (bkind == kKC4 || bkind == kXC4)) {
+        if (big) return dispatch_dma<GemmT128>(g, akind == kKC4, bkind == kKC4, p.batches, name);
+        return dispatch_dma<GemmT64>(g, akind == kKC4, bkind == kKC4, p.batches, name);
     }
     switch (akind) {
         case kKC4: return dispatch_b_small<kKC4>(g, bkind, p.batches, name);

@@ -466,4 +466,54 @@ __device__ __forceinline__ float* partial_slot(float* ws, int g, int which) {
     return ws + ((int64_t)g * 2 + which) * (T::BM * T::BN);
 }
 
+// Partial tiles are written and read with device-scope coherence (the
+// buffer instructions' sc1 bit: stores write through the XCD's L2, loads do
+// not hit a stale L2 line), so the workgroup that finishes a tile on another
+// XCD sees them once their writers' stores have completed - without an L2
+// writeback or invalidate.
+static constexpr int kDeviceScope = 16;
+
+template <class T>
+__device__ __forceinline__ uint32_t slot_byte_offset(int g, int which) {
+    return (uint32_t)((g * 2 + which) * (T::BM * T::BN)) * 4u;
+}
+
+// Direct-to-LDS buffer loads: lane l's `size` bytes land at LDS[lds_dst +
+// size * l] (lds_dst wave-uniform), no VGPR staging and no LDS store.
+typedef __attribute__((address_space(3))) void* lds_ptr;
+__device__ __forceinline__ void dma_load4(__amdgpu_buffer_rsrc_t r, float* lds_dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_dst, 4, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, float* lds_dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_dst, 16, voff, soff, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): the direct-to-LDS loads of this wave have landed
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Workgroup barrier for a multi-stage direct-to-LDS pipeline: each wave
+// waits until at most N of its vector memory operations are outstanding
+// (its direct-to-LDS loads complete in issue order, so all but the newest N
+// have written LDS) and its LDS reads and writes are done (lgkmcnt(0)), then
+// s_barrier. __syncthreads cannot be used: its fence makes the compiler wait
+// for every outstanding vector memory operation (vmcnt(0)) - the loads of
+// the slices meant to stay in flight. The signal fences keep the compiler
+// from moving memory accesses across the barrier; gfx950's barrier needs no
+// other wait (the compiler inserts none before it).
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) expcnt(7) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// `addr` if `keep`, else exactly kOutOfRange (adding an SGPR offset below
+// 2^31 cannot wrap it back into range); without branches
+__device__ __forceinline__ uint32_t keep_or_oob(uint32_t addr, bool keep) {
+    const uint32_t m = 0u - (uint32_t)keep;
+    return (addr & m) | (kOutOfRange & ~m);
+}
+
 }  // namespace nnc

@@ -4,17 +4,21 @@ cost-model runtime (libnnc_costmodel.so).
 Input: rocprofv3 kernel traces of libnnc_hip.so running the O3 programs of
 ResNet-18 (batch 1, 8, 32) and the transformer encoder (batch 8, sequence
 128) - one eager run, three graph replays and 20 timed replays each - and the
-graph-replay milliseconds per step printed beside them:
+graph-replay milliseconds per step that the same script prints when it runs
+without the profiler on the same machine (kernel tracing stalls graph
+replays between kernels - up to hundreds of microseconds - while the traced
+kernel durations match the untraced ones):
 
     rocprofv3 --kernel-trace --output-format csv -d <dir>/<cfg> -o trace -- \\
         python3 tests/golden/costmodel_trace_run.py <cfg>
+    python3 tests/golden/costmodel_trace_run.py <cfg>      # ms/step
 
 Output per configuration: the replayed step time, and per kernel (demangled
 name without template arguments) the launches per step and the median
 duration over the timed replays (avg_us: the mean of those medians over the
 kernel's launches in one step).
 
-    python tests/golden/make_costmodel_fixture.py <dir> r18_b1=0.2965 r18_b8=0.6311 r18_b32=1.3447 tf_b8=0.2240
+    python tests/golden/make_costmodel_fixture.py <dir> r18_b1=0.2663 r18_b8=0.6106 r18_b32=1.3374 tf_b8=0.2275
 """
 
 from __future__ import annotations

@@ -34,6 +34,7 @@ FAMILY = [
     (r"conv_igemm_.*_dma$", "conv_dma_k"),
     (r"conv_igemm_", "conv_streamk_k"),
     (r"conv_streamk_fixup$", "conv_fixup_k"),
+    (r"gemm_dma_", "gemm_dma_k"),
     (r"gemm_mfma_", "gemm_streamk_k"),
     (r"gemm_streamk_fixup$", "gemm_fixup_k"),
     (r"dot_rows_", "dot_k"),
@@ -61,10 +62,15 @@ def _program(cfg: str):
     return build_program(g, opt_level=3)
 
 
+# device kernels that one launch name of libnnc_hip.so stands for
+MERGED = {"permute_k": "transpose", "transpose2d_k": "transpose",
+          "conv_fixup_split_k": "conv_fixup_k"}  # both "conv_streamk_fixup"
+
+
 def _measured_families(cfg: str) -> dict:
     fams: dict[str, dict] = {}
     for name, k in FIXTURE[cfg]["kernels"].items():
-        fam = "transpose" if name in ("permute_k", "transpose2d_k") else name
+        fam = MERGED.get(name, name)
         f = fams.setdefault(fam, {"launches": 0, "us": 0.0})
         f["launches"] += k["launches"]
         f["us"] += k["launches"] * k["avg_us"]

@@ -24,7 +24,7 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 def test_streamk_schedule_covers_every_slice_once(tmp_path):
     hipcc = HIPCC
     exe = tmp_path / "streamk_schedule"
-    subprocess.run([hipcc, "-O2", "-std=c++17", "-I", str(ROOT / "include"), "-I", str(ROOT / "nnc-py_amd" / "csrc"),
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O2", "-std=c++17", "-I", str(ROOT / "include"), "-I", str(ROOT / "nnc-py_amd" / "csrc"),
                     str(ROOT / "tests" / "native" / "streamk_schedule.cpp"), "-o", str(exe)],
                    check=True, capture_output=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
