@@ -5,7 +5,7 @@
 //
 // inner == 1 (the reduced / normalised elements are contiguous): one wave64
 // per row. Rows of up to 4096 floats are read once with 16-byte loads into
-// registers; max / sums are combined across the wave with xor shuffles, and
+// registers; max / sums are combined across the wave with DPP lane moves, and
 // the row is written once: one HBM read + one HBM write per element. Longer
 // rows loop over global memory (re-reads come from L2).
 //
@@ -29,19 +29,38 @@
 
 namespace nnc {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+// Wave-wide sum / max through DPP lane moves (no LDS round trips): xor 1
+// and xor 2 within quads, the half-row and row mirrors (every lane then
+// holds its 16-lane row's result), then the four rows read out with
+// v_readlane and combined in a fixed order. The same tree for every wave:
+// deterministic, and the result is wave-uniform.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
+
+__device__ __forceinline__ float row_lane(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_move<kDppXor1>(v);
+    v += dpp_move<kDppXor2>(v);
+    v += dpp_move<kDppRowHalfMirror>(v);
+    v += dpp_move<kDppRowMirror>(v);
+    return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
+}
+
+// max by '>' (callers never pass NaN: their per-lane maxima start at -inf
+// and take only values that compare greater)
+__device__ __forceinline__ float max_gt(float a, float b) { return b > a ? b : a; }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float o = __shfl_xor(v, off, 64);
-        v = o > v ? o : v;
-    }
-    return v;
+    v = max_gt(v, dpp_move<kDppXor1>(v));
+    v = max_gt(v, dpp_move<kDppXor2>(v));
+    v = max_gt(v, dpp_move<kDppRowHalfMirror>(v));
+    v = max_gt(v, dpp_move<kDppRowMirror>(v));
+    return max_gt(max_gt(row_lane(v, 0), row_lane(v, 16)), max_gt(row_lane(v, 32), row_lane(v, 48)));
 }
 
 // ---------------------------------------------------------------------------

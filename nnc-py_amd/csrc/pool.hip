@@ -2,8 +2,12 @@
 //
 // One thread per output element, lanes along the output row so stores
 // coalesce; each window is read straight from HBM/L2 (a 3x3 s2 window
-// re-reads ~2.25x the input, served by L2). Global average pooling has its
-// own kernel that stages whole planes through LDS with coalesced loads. The window is clamped to the
+// re-reads ~2.25x the input, served by L2). The 3x3 / stride 2 / pad 1 max
+// pool (ResNet's stem pool) has its own kernels that read each input row of a
+// band of output rows once (maxpool3s2_v4_k: 16-byte loads, two outputs per
+// lane; maxpool3s2_k: 8-byte loads, for widths not a multiple of 4). Global
+// average pooling has its own kernel that stages whole planes through LDS
+// with coalesced loads. The window is clamped to the
 // input like the reference, scanned in the same h-major order with the same
 // comparisons / float additions, so both kernels are bit-exact with it:
 //   MaxPool: start at -3.402823e38f, take v when no element was seen yet or
@@ -231,6 +235,86 @@ __global__ void __launch_bounds__(256) maxpool3s2_k(PoolArgs a, int nbands, int 
     }
 }
 
+// The same pool with 16-byte loads (W % 4 == 0, 16-byte aligned rows): lane
+// l of a segment owns the output column pair 2p, 2p + 1 (p = chunk * LPS +
+// l) and loads input columns 4p .. 4p + 3 of each row of its band as one
+// 16-byte load; column 4p - 1 is its left neighbour's last element (lane 0
+// of a segment loads it itself). A wave holds 64 / LPS segments of LPS
+// lanes (LPS = 16, 32 or 64, the smallest that covers a row's pairs), each
+// its own (plane, band, chunk): narrow rows do not leave lanes idle. Same
+// scan order and comparisons as maxpool3s2_k - bit-exact. Outputs leave as
+// 8-byte stores.
+template <int R>
+__global__ void __launch_bounds__(256) maxpool3s2_v4_k(PoolArgs a, int nbands, int nchunks, int lps_log2,
+                                                     int64_t items) {
+    const int lane = threadIdx.x & 63;
+    const int lps = 1 << lps_log2;
+    const int seg = lane >> lps_log2, l = lane & (lps - 1);
+    const int64_t item = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 >> lps_log2) + seg;
+    if (item >= items) return;  // uniform over a segment; the shuffles stay inside it
+    const int chunk = (int)(item % nchunks);
+    const int64_t rest = item / nchunks;
+    const int band = (int)(rest % nbands);
+    const int nc = (int)(rest / nbands);
+    const int pr = chunk * lps + l;    // this lane's column pair
+    const int pairs = a.Wo >> 1;       // Wo == W / 2, W % 4 == 0
+    const bool active = pr < pairs;
+    const int oh0 = band * R;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.in);
+    const bool cleft = active && pr >= 1;  // column 4p - 1 inside the image
+    const int hbase = 2 * oh0 - 1;
+    float xl[2 * R + 1], x[2 * R + 1][4];
+#pragma unroll
+    for (int i = 0; i < 2 * R + 1; ++i) {
+        const int h = hbase + i;
+        const bool row_in = h >= 0 && h < a.H;
+        const uint32_t rowoff = row_in ? (uint32_t)((nc * a.H + h) * a.W) * 4u : 0u;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+            rs, (int)(row_in && active ? rowoff + (uint32_t)pr * 16u : kOutOfRange), 0, 0);
+        // element copies first: bit_cast of an ext-vector element is miscompiled
+        const uint32_t e0 = v[0], e1 = v[1], e2 = v[2], e3 = v[3];
+        x[i][0] = __uint_as_float(e0);
+        x[i][1] = __uint_as_float(e1);
+        x[i][2] = __uint_as_float(e2);
+        x[i][3] = __uint_as_float(e3);
+        float left = __shfl_up(x[i][3], 1, lps);
+        if (l == 0 && cleft) left = load_f32(rs, row_in ? rowoff + (uint32_t)(4 * pr - 1) * 4u : kOutOfRange);
+        xl[i] = left;
+    }
+    if (!active) return;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int oh = oh0 + j;
+        if (oh >= a.Ho) break;
+        float best0 = -3.402823e38f, best1 = -3.402823e38f;
+        bool seen0 = false, seen1 = false;
+#pragma unroll
+        for (int r = 0; r < 3; ++r) {
+            const int h = hbase + 2 * j + r;
+            if (h < 0 || h >= a.H) continue;
+            const float* xr = x[2 * j + r];
+            // output 2p: columns 4p - 1, 4p, 4p + 1
+            const float w0[3] = {xl[2 * j + r], xr[0], xr[1]};
+            const bool ok0[3] = {cleft, true, true};
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                if (ok0[c] && (!seen0 || w0[c] > best0)) {
+                    best0 = w0[c];
+                    seen0 = true;
+                }
+            // output 2p + 1: columns 4p + 1, 4p + 2, 4p + 3
+#pragma unroll
+            for (int c = 1; c < 4; ++c)
+                if (!seen1 || xr[c] > best1) {
+                    best1 = xr[c];
+                    seen1 = true;
+                }
+        }
+        float2* o = reinterpret_cast<float2*>(a.out + ((int64_t)nc * a.Ho + oh) * a.Wo) + pr;
+        *o = make_float2(best0, best1);
+    }
+}
+
 template <int R>
 static void maxpool3s2_launch(const char* name, const PoolArgs& a, int64_t nc, int nchunks) {
     const int nbands = (int)ceil_div(a.Ho, R);
@@ -290,6 +374,25 @@ static void pool_entry(const char* name, Tensor* in, Tensor* out, int kh, int kw
         // 8 output rows per wave, fewer where that leaves the GPU short of
         // waves (ResNet-18 stem pool: batch 1 448 waves -> 2 rows, 11.9 ->
         // 6.2 us; batch 8 3584 waves -> 4 rows, 13.4 -> 10.3 us)
+        if (a.W % 4 == 0 && a.Wo * 2 == a.W && aligned16(a.in) && aligned16(a.out)) {
+            // 16-byte loads; bands of 2 output rows, 1 where 2 leave fewer
+            // than 2048 waves (ResNet-18 stem pool on MI355X: batch 32 27.0 ->
+            // 23.8 us, batch 8 8.1 -> 6.2 us, batch 1 3.5 -> 3.0 us against
+            // maxpool3s2_k; bands of 3, 4 and 8 rows measured slower)
+            const int pairs = a.Wo / 2;
+            const int lps_log2 = pairs <= 16 ? 4 : (pairs <= 32 ? 5 : 6);
+            const int nchunks = (int)ceil_div(pairs, 1 << lps_log2);
+            const int64_t items2 = nc * ceil_div(a.Ho, 2) * nchunks;
+            const bool one = ceil_div(items2, 64 >> lps_log2) < 2048;
+            const int nbands = (int)ceil_div(a.Ho, one ? 1 : 2);
+            const int64_t items = nc * nbands * nchunks;
+            const int64_t waves = ceil_div(items, 64 >> lps_log2);
+            if (waves < ((int64_t)1 << 30)) {
+                const dim3 grid((unsigned)ceil_div(waves, 4));
+                if (one) return launch(name, maxpool3s2_v4_k<1>, grid, dim3(256), 0, a, nbands, nchunks, lps_log2, items);
+                return launch(name, maxpool3s2_v4_k<2>, grid, dim3(256), 0, a, nbands, nchunks, lps_log2, items);
+            }
+        }
         const int nchunks = (int)ceil_div(a.Wo, 64);
         const int64_t waves8 = nc * ceil_div(a.Ho, 8) * nchunks;
         if (waves8 < ((int64_t)1 << 28)) {
