@@ -18,7 +18,7 @@ name without template arguments) the launches per step and the median
 duration over the timed replays (avg_us: the mean of those medians over the
 kernel's launches in one step).
 
-    python tests/golden/make_costmodel_fixture.py <dir> r18_b1=0.2663 r18_b8=0.6106 r18_b32=1.3374 tf_b8=0.2275
+    python tests/golden/make_costmodel_fixture.py <dir> r18_b1=0.2661 r18_b8=0.6063 r18_b32=1.3255 tf_b8=0.2260
 """
 
 from __future__ import annotations
