@@ -321,6 +321,13 @@ GEMM_SHAPES = [
     (1024, 1024, 1024, 0, 0, True),
     (1, 1000, 512, 0, 1, True),     # ResNet FC at batch 1
     (32, 1000, 512, 0, 1, True),    # ResNet FC at batch 32
+    # direct-to-LDS layouts: A x-contiguous (transA, M % 4 == 0) with B
+    # x-contiguous and k-contiguous, and K tails that are whole 16-byte
+    # chunks but not whole 32-k slices
+    (256, 192, 100, 1, 0, True),
+    (200, 128, 68, 0, 1, True),
+    (64, 96, 40, 1, 1, False),
+    (1536, 1536, 132, 0, 1, True),  # 128x128 direct-to-LDS tiles, K tail of 4
 ]
 
 
@@ -331,6 +338,23 @@ def test_gemm_layouts_and_streamk(shape, hip, dmem, abi, oracle_lib):
     exp = caserun.run_case(oracle_lib, case, abi)["out"]
     got = caserun.run_case(hip, case, abi, dmem)["out"]
     _check(got, exp, case["name"])
+
+
+def test_batched_matmul_broadcast_b(hip, dmem, abi, oracle_lib):
+    """[12,96,72] x [72,136]: B broadcast over the batch (batch stride 0 on
+    the direct-to-LDS path), each batch against the oracle's 2-D product."""
+    rng = np.random.default_rng(6)
+    a = rng.uniform(-1, 1, (12, 96, 72)).astype(np.float32)
+    b = rng.uniform(-1, 1, (72, 136)).astype(np.float32)
+    case = {"name": "bmm_bcast", "op": "nnc_matmul",
+            "tensors": {"a": a, "b": b, "out": np.zeros((12, 96, 136), np.float32)},
+            "args": [("t", "a"), ("t", "b"), ("t", "out")], "outputs": ["out"], "bar": "fp"}
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    for q in (0, 5, 11):
+        c2 = {"name": "slice", "op": "nnc_matmul",
+              "tensors": {"a": a[q].copy(), "b": b, "out": np.zeros((96, 136), np.float32)},
+              "args": [("t", "a"), ("t", "b"), ("t", "out")], "outputs": ["out"], "bar": "fp"}
+        _check(got[q], caserun.run_case(oracle_lib, c2, abi)["out"], f"batch {q}")
 
 
 def test_batched_matmul_streamk(hip, dmem, abi, oracle_lib):
