@@ -226,17 +226,13 @@ __device__ void conv_finish_tile(const ConvArgs& a, int t, int g0, int g1, int f
         f32x4 v[CH];
 #pragma unroll
         for (int e = 0; e < CH; ++e)
-            v[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                 rws, (int)(first + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u), 0,
-                                                 kDeviceScope));
+            v[e] = load_partial4(rws, first + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u);
         for (int g = g0 + 1; g <= g1; ++g) {
             const uint32_t base = slot_byte_offset<T>(g, 0);
             f32x4 p[CH];
 #pragma unroll
             for (int e = 0; e < CH; ++e)
-                p[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     rws, (int)(base + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u),
-                                                     0, kDeviceScope));
+                p[e] = load_partial4(rws, base + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u);
 #pragma unroll
             for (int e = 0; e < CH; ++e) v[e] += p[e];
         }
@@ -378,26 +374,11 @@ __device__ __forceinline__ void conv_segment_out(const ConvArgs& a, const Stream
                     // copy the element first: this compiler's __builtin_bit_cast of
                     // an ext-vector element reads the wrong element
                     const float x = sum[tm][tn][r];
-                    __builtin_amdgcn_raw_buffer_store_b32(
-                        __float_as_uint(x), rws,
-                        (int)(base + (uint32_t)(acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)) * 4u), 0, kDeviceScope);
+                    store_partial(rws, base + (uint32_t)(acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)) * 4u, x);
                 }
-        __shared__ int last;
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int g0, g1, first_slot;
-            tile_partials(sk, seg.tile, g0, g1, first_slot);
-            const int old = __hip_atomic_fetch_add(a.cnt + seg.tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = old == g1 - g0;
-            if (last) __hip_atomic_store(a.cnt + seg.tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (last) {
-            int g0, g1, first_slot;
-            tile_partials(sk, seg.tile, g0, g1, first_slot);
-            conv_finish_tile<T>(a, seg.tile, g0, g1, first_slot);
-        }
+        int g0, g1, first_slot;
+        tile_partials(sk, seg.tile, g0, g1, first_slot);
+        if (finish_arrive(a.cnt + seg.tile, g1 - g0)) conv_finish_tile<T>(a, seg.tile, g0, g1, first_slot);
     }
 }
 

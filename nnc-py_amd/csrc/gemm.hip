@@ -330,17 +330,13 @@ __device__ void gemm_finish_tile(const GemmArgs& g, int t, int g0, int g1, int f
         f32x4 v[CH];
 #pragma unroll
         for (int e = 0; e < CH; ++e)
-            v[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                 rws, (int)(first + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u), 0,
-                                                 kDeviceScope));
+            v[e] = load_partial4(rws, first + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u);
         for (int w = g0 + 1; w <= g1; ++w) {
             const uint32_t base = slot_byte_offset<T>(w, 0);
             f32x4 p[CH];
 #pragma unroll
             for (int e = 0; e < CH; ++e)
-                p[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     rws, (int)(base + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u),
-                                                     0, kDeviceScope));
+                p[e] = load_partial4(rws, base + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u);
 #pragma unroll
             for (int e = 0; e < CH; ++e) v[e] += p[e];
         }
@@ -405,26 +401,11 @@ __device__ __forceinline__ void gemm_segment_out(const GemmArgs& g, const Stream
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const float x = sum[tm][tn][r];
-                    __builtin_amdgcn_raw_buffer_store_b32(
-                        __float_as_uint(x), rws,
-                        (int)(base + (uint32_t)(acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)) * 4u), 0, kDeviceScope);
+                    store_partial(rws, base + (uint32_t)(acc_row<T>(tm, r) * T::BN + acc_col<T>(tn)) * 4u, x);
                 }
-        __shared__ int last;
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int g0, g1, first_slot;
-            tile_partials(sk, seg.tile, g0, g1, first_slot);
-            const int old = __hip_atomic_fetch_add(g.cnt + seg.tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = old == g1 - g0;
-            if (last) __hip_atomic_store(g.cnt + seg.tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (last) {
-            int g0, g1, first_slot;
-            tile_partials(sk, seg.tile, g0, g1, first_slot);
-            gemm_finish_tile<T>(g, seg.tile, g0, g1, first_slot);
-        }
+        int g0, g1, first_slot;
+        tile_partials(sk, seg.tile, g0, g1, first_slot);
+        if (finish_arrive(g.cnt + seg.tile, g1 - g0)) gemm_finish_tile<T>(g, seg.tile, g0, g1, first_slot);
     }
 }
 

@@ -466,16 +466,70 @@ __device__ __forceinline__ float* partial_slot(float* ws, int g, int which) {
     return ws + ((int64_t)g * 2 + which) * (T::BM * T::BN);
 }
 
-// Partial tiles are written and read with device-scope coherence (the
-// buffer instructions' sc1 bit: stores write through the XCD's L2, loads do
-// not hit a stale L2 line), so the workgroup that finishes a tile on another
-// XCD sees them once their writers' stores have completed - without an L2
-// writeback or invalidate.
-static constexpr int kDeviceScope = 16;
+// In-kernel stream-K finish. Every workgroup that computes part of a split
+// tile stores its partial into its slot and arrives at the tile's counter;
+// the last to arrive sums the tile's partials and writes the tile. The
+// partials cross XCDs (each XCD has its own L2), and the hand-off is the
+// agent-scope release/acquire pair of the AMDGPU memory model (LLVM's
+// AMDGPUUsage, GFX942 memory-model table) with its two whole-L2 cache
+// operations left out, because they have nothing to do here:
+//   release  The model emits `buffer_wbl2 sc1; s_waitcnt vmcnt(0)` before
+//            the atomic. The write-back flushes ordinary stores held in the
+//            XCD's L2; every byte published here is stored with the sc1
+//            (device-scope) bit instead, which writes it through the L2, so
+//            the wait for the stores' completion is the whole release.
+//   acquire  The model emits `s_waitcnt vmcnt(0); buffer_inv sc1` after the
+//            atomic. The invalidate drops stale L2 lines for ordinary loads;
+//            the partials are read back with the sc1 bit, which does not
+//            return a stale L2 line, so the wait for the atomic's return (its
+//            value decides who finishes) is the whole acquire.
+// Written as __ATOMIC_ACQ_REL the compiler emits both cache operations; the
+// write-back of the tile's ordinary output stores and the invalidate of the
+// next tile's operands in L2 then cost the split kernels 9-24% (ResNet-18
+// batch 32 stem 119 -> 147 us, 3x3 64-channel layer 84 -> 106 us, GEMM
+// 2048^3 174 -> 191 us, measured on MI355X). tests/native/finish_order.hip
+// checks the emitted instruction order of this protocol.
+static constexpr int kDeviceScope = 16;  // sc1: device-scope coherent buffer access
 
 template <class T>
 __device__ __forceinline__ uint32_t slot_byte_offset(int g, int which) {
     return (uint32_t)((g * 2 + which) * (T::BM * T::BN)) * 4u;
+}
+
+// One float of a partial, stored with device-scope coherence.
+__device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t ws, uint32_t byte_off, float x) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), ws, (int)byte_off, 0, kDeviceScope);
+}
+
+// Four floats of a partial, loaded with device-scope coherence.
+__device__ __forceinline__ f32x4 load_partial4(__amdgpu_buffer_rsrc_t ws, uint32_t byte_off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ws, (int)byte_off, 0, kDeviceScope));
+}
+
+// Called by every thread of the workgroup after its store_partial calls.
+// `arrivals_before_last` = the number of workgroups that share the tile,
+// minus one. Returns, in every thread, whether this workgroup arrived last;
+// the last one also resets the counter to 0 for the next launch (kernel
+// boundaries order it before that launch's arrivals).
+__device__ __forceinline__ bool finish_arrive(int* counter, int arrivals_before_last) {
+    __shared__ int last;
+    // Release: this thread's sc1 stores have completed (vmcnt(0)), then the
+    // barrier orders every thread's completion before thread 0's atomic.
+    // The signal fences keep the compiler from moving memory operations
+    // across the wait.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Acquire: `old` is used here, so the atomic has returned before the
+        // barrier below and before any thread issues its partial loads.
+        last = old == arrivals_before_last;
+        if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return last;
 }
 
 // Direct-to-LDS buffer loads: lane l's `size` bytes land at LDS[lds_dst +

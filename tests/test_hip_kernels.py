@@ -340,6 +340,41 @@ def test_gemm_layouts_and_streamk(shape, hip, dmem, abi, oracle_lib):
     _check(got, exp, case["name"])
 
 
+# Shapes whose split tiles are finished inside the direct-to-LDS kernel by
+# the last of their 3-4 workgroups (stream-K plan with 256 or 512 resident
+# workgroups): 64 channels 3x3 over 8 x 56x56 (64x128 tiles, 196 tiles of 18
+# slices), GEMM 512x512x288 (64x64 tiles, 64 tiles of 9 slices) and
+# 2048x1024x256 (128x128 tiles, 128 tiles of 8 slices).
+IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "gemm_512x512x288", "gemm_2048x1024x256"]
+
+
+@pytest.mark.parametrize("which", IN_KERNEL_FINISH_CASES)
+def test_in_kernel_finish_alternating_inputs(which, hip, dmem, abi, oracle_lib):
+    """Two inputs in turn, four calls: the partials and tile counters the
+    previous call left in the library's scratch differ from this call's, so
+    a partial read before its writer's stores were visible, or a counter
+    not back at zero, shows up as a wrong tile. Each call matches the
+    oracle, and calls on the same input match each other to the bit."""
+    def make(seed):
+        rng = np.random.default_rng(seed)
+        if which == "conv_b8_64c_56":
+            return _packed_case(rng, 8, 64, 56, 64, 3, 1, 1)
+        m, n, k = {"gemm_512x512x288": (512, 512, 288), "gemm_2048x1024x256": (2048, 1024, 256)}[which]
+        return _gemm_case(rng, m, n, k, 0, 1, True)
+    cases = [make(41), make(42)]
+    exp = [caserun.run_case(oracle_lib, c, abi)["out"] for c in cases]
+    first = [None, None]
+    for call in range(4):
+        q = call % 2
+        print(f"case {which} call {call} input {q}", flush=True)
+        got = caserun.run_case(hip, cases[q], abi, dmem)["out"]
+        _check(got, exp[q], f"{which} call {call}")
+        if first[q] is None:
+            first[q] = got
+        else:
+            assert np.array_equal(got, first[q]), f"{which} call {call}: differs from the first call on this input"
+
+
 def test_batched_matmul_broadcast_b(hip, dmem, abi, oracle_lib):
     """[12,96,72] x [72,136]: B broadcast over the batch (batch stride 0 on
     the direct-to-LDS path), each batch against the oracle's 2-D product."""
