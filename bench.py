@@ -43,6 +43,8 @@ ROOT = Path(__file__).resolve().parent
 METRIC = "ResNet-18 fp32 images/s (b1,b32) on 1 GPU; per-op % HBM/MFMA roofline"
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 PEAK_FP32_MFMA_TF = 157.3  # MI355X dense fp32 matrix
+# kernel-table names of the MFMA kernels (their work is priced in FLOP)
+MFMA_KERNELS = ("conv_igemm", "conv_stem", "gemm_mfma", "gemm_dma")
 
 
 def load_package():
@@ -91,7 +93,7 @@ def kernel_table(ex, runtime, steps: int) -> list[dict]:
     rows = []
     for r in table:
         avg_ms = r["ms"] / r["launches"]
-        if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma", "gemm_dma")):
+        if r["flops"] > 0 and r["name"].startswith(MFMA_KERNELS):
             bound, unit, peak = "mfma", "TFLOP/s", PEAK_FP32_MFMA_TF
             achieved = r["flops"] / (r["ms"] * 1e-3) / 1e12
         elif r["name"].endswith("_fixup"):
@@ -186,6 +188,9 @@ def conv_symbol_pattern(name: str) -> re.Pattern | None:
         kh, kw = ("0", "0") if kh == "any" else (kh, kw)
         return re.compile(rf"conv_streamk_k<nnc::Tile<{bm}, {bn},[^>]*>, {kh}, {kw}, "
                           rf"{'true' if vec == 'v4' else 'false'}>")
+    m = re.fullmatch(r"conv_stem_rows_w(\d+)", name)
+    if m:
+        return re.compile(rf"conv_stem_k<{int(m.group(1)) // 16}>")
     m = re.fullmatch(r"gemm_mfma_(\d+)x(\d+)_\w+", name)
     if m:
         return re.compile(rf"gemm_streamk_k<nnc::Tile<{m.group(1)}, {m.group(2)},")
@@ -289,7 +294,7 @@ def _op_roofline(runtime, fn, reps: int = 10, warmup: int = 3) -> dict:
     nbytes = sum(r["bytes"] for r in table) / reps
     mfma = False
     for r in table:
-        if r["flops"] > 0 and r["name"].startswith(("conv_igemm", "gemm_mfma", "gemm_dma")):
+        if r["flops"] > 0 and r["name"].startswith(MFMA_KERNELS):
             achieved, unit, peak = r["flops"] / (r["ms"] * 1e-3) / 1e12, "TFLOP/s", PEAK_FP32_MFMA_TF
             mfma = True
         else:

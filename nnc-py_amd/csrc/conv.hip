@@ -22,6 +22,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "mfma_tile.h"
 
 namespace nnc {
@@ -1235,6 +1237,183 @@ static void launch_conv_dma(ConvArgs& a, const char* entry) {
     launch_conv_dma_t<T, DmaPacked<T, KH, KW>>(a, entry, name);
 }
 
+// ---------------------------------------------------------------------------
+// The RGB stem (3 channels, 7x7, stride 2, pad 3, H == 2 Ho, W == 2 Wo,
+// Wo = 16 * BPR, Co <= 64) as a persistent kernel over output rows. A tile
+// is one output row of one image: 64 channels x Wo pixels. Its input
+// window, the 7 input rows x 3 channels it reads, goes into LDS with
+// 16-byte direct-to-LDS loads (a row of W floats at offset 4 of an LDS row
+// of W + 8, whose 4 + 4 pad columns stay zero: the left and right image
+// padding), double-buffered: the next tile's window loads while this one
+// computes. The contraction then reads its B operand straight out of the
+// window (im2col on the read side: k = tap * 3 + ci of the packed weight
+// rows -> LDS row (ci, ky), column 2 ox + kx + 1), so the input crosses the
+// memory system once per tile as wide loads instead of one 4-byte gather
+// per k and pixel. MFMA 16x16x4 computing out^T (pixels x channels): wave w
+// owns output channels 16w..16w+15 and all Wo / 16 pixel blocks of the row;
+// its weights (K = 147 in 37 steps of 4) stay in registers for the whole
+// kernel, and each lane ends with 4 consecutive pixels of one channel: one
+// 16-byte store per block.
+//   v_mfma_f32_16x16x4_f32, lane l: A[i = l % 16][k = l / 16] (window: pixel
+//   i), B[k = l / 16][j = l % 16] (weights: channel j), D register r:
+//   D[i = 4 (l / 16) + r][j = l % 16]
+// ---------------------------------------------------------------------------
+struct StemArgs {
+    const float* in;
+    const float* w;  // [Co][ldw], k = tap * 3 + ci, zero past 147
+    const float* bias;
+    float* out;
+    int N, H, W, Co, Ho, Wo, ldw, act, tiles;
+};
+
+static constexpr int kStemK = 147, kStemSteps = 37;  // 3 * 7 * 7, rounded up to steps of 4
+
+// LDS requested per workgroup: at most two workgroups per CU, so that a
+// grid of 2 per CU puts exactly two on every CU (tiles spread evenly)
+static constexpr int kStemLdsBytes = 56 * 1024;
+
+template <int BPR>
+struct StemShape {
+    static constexpr int WO = 16 * BPR, W = 2 * WO, LW = W + 8;  // LDS row: 4 pad, W data, 4 pad
+    static constexpr int CP = 7 * LW, BUF = 3 * CP;              // channel pitch, one window
+    static constexpr int CHUNKS = W / 4;                         // 16-byte pieces per input row
+    static_assert(CHUNKS <= 64, "one load instruction per input row");
+    static_assert(2 * BUF * 4 <= kStemLdsBytes, "two windows in the requested LDS");
+};
+
+// one tile's window: rows (ci, ky) of input row 2 oy - 3 + ky, wave w
+// loading rows w, w + 4, ...; rows outside the image read as zeros
+template <int BPR>
+__device__ __forceinline__ void stem_window(const StemArgs& a, __amdgpu_buffer_rsrc_t rin, float* buf, int t,
+                                            int wave, int lane) {
+    typedef StemShape<BPR> S;
+    const int n = t / a.Ho, oy = t - n * a.Ho;
+    for (int r = wave; r < 21; r += 4) {
+        const int ci = r / 7, ky = r - ci * 7;
+        const int iy = 2 * oy - 3 + ky;
+        const bool in_img = iy >= 0 && iy < a.H;
+        const uint32_t voff =
+            in_img ? (uint32_t)(((n * 3 + ci) * a.H + iy) * a.W) * 4u + (uint32_t)lane * 16u : kOutOfRange;
+        if (lane < S::CHUNKS) dma_load16(rin, buf + ci * S::CP + ky * S::LW + 4, voff, 0);
+    }
+}
+
+template <int BPR>
+__global__ void __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) conv_stem_k(StemArgs a) {
+    typedef StemShape<BPR> S;
+    extern __shared__ __align__(16) float lds[];  // [2][3 ci][7 ky][LW]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, kq = lane >> 4;
+    const int G = gridDim.x;
+    int t = xcd_remap(blockIdx.x, G);
+    if (t >= a.tiles) return;  // the host launches at most `tiles` workgroups
+    const __amdgpu_buffer_rsrc_t rin = make_rsrc(a.in);
+    // zero pad columns of both windows, once (the loads never write them)
+    for (int r = threadIdx.x; r < 2 * 3 * 7; r += 256) {
+        float* lrow = lds + r * S::LW;
+        *reinterpret_cast<float4*>(lrow) = make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4*>(lrow + 4 + S::W) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    stem_window<BPR>(a, rin, lds, t, wave, lane);
+    if (t + G < a.tiles) stem_window<BPR>(a, rin, lds + S::BUF, t + G, wave, lane);
+    // weights of this wave's 16 channels (rows past Co read as zeros) and
+    // the per-step window offsets of this lane's k
+    const int co_a = 16 * wave + j;  // also this lane's output channel
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.w), (short)0, a.Co * a.ldw * 4, 0x00020000);
+    float A[kStemSteps];
+    int koff[kStemSteps];
+#pragma unroll
+    for (int s = 0; s < kStemSteps; ++s) {
+        const int k = 4 * s + kq;
+        A[s] = load_f32(rw, (uint32_t)(co_a * a.ldw + k) * 4u);
+        const int tap = k / 3, ci = k - tap * 3, ky = tap / 7, kx = tap - ky * 7;
+        koff[s] = k < kStemK ? ci * S::CP + ky * S::LW + kx + 1 + 2 * j : 0;
+    }
+    const float bias = a.bias && co_a < a.Co ? a.bias[co_a] : 0.f;
+    dma_barrier<0>();  // both windows landed, pad columns written
+    for (int i = 0; t < a.tiles; ++i, t += G) {
+        const float* B = lds + (i & 1) * S::BUF;
+        f32x4 acc[BPR];
+#pragma unroll
+        for (int b = 0; b < BPR; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // B values one step ahead of the MFMAs that use them
+        float x[BPR];
+#pragma unroll
+        for (int b = 0; b < BPR; ++b) x[b] = B[koff[0] + 32 * b];
+#pragma unroll
+        for (int s = 0; s < kStemSteps; ++s) {
+            float xn[BPR];
+            if (s + 1 < kStemSteps) {
+#pragma unroll
+                for (int b = 0; b < BPR; ++b) xn[b] = B[koff[s + 1] + 32 * b];
+            }
+            if (s == kStemSteps - 1 && 4 * s + kq >= kStemK) {
+#pragma unroll
+                for (int b = 0; b < BPR; ++b) x[b] = 0.f;  // k past K: no input term, not even 0 * inf
+            }
+#pragma unroll
+            for (int b = 0; b < BPR; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b], A[s], acc[b], 0, 0, 0);
+            if (s + 1 < kStemSteps) {
+#pragma unroll
+                for (int b = 0; b < BPR; ++b) x[b] = xn[b];
+                // schedule the next step's LDS reads ahead of this step's
+                // MFMAs (left alone, the scheduler waits on each read right
+                // before its MFMA)
+                __builtin_amdgcn_sched_group_barrier(0x100, (BPR + 1) / 2, 0);  // DS reads (paired)
+                __builtin_amdgcn_sched_group_barrier(0x008, BPR, 0);            // MFMAs
+            }
+        }
+        // the next window landed (loaded a whole tile ago) and every wave is
+        // done with this one: refill it with the tile after next
+        dma_barrier<0>();
+        if (t + 2 * G < a.tiles) stem_window<BPR>(a, rin, lds + (i & 1) * S::BUF, t + 2 * G, wave, lane);
+        const int n = t / a.Ho, oy = t - n * a.Ho;
+        if (co_a < a.Co) {
+            float* orow = a.out + (((int64_t)n * a.Co + co_a) * a.Ho + oy) * a.Wo + 4 * kq;
+#pragma unroll
+            for (int b = 0; b < BPR; ++b) {
+                // element copies first: bit_cast of an ext-vector element is miscompiled
+                const float v0 = acc[b][0], v1 = acc[b][1], v2 = acc[b][2], v3 = acc[b][3];
+                *reinterpret_cast<float4*>(orow + 16 * b) =
+                    make_float4(activate(v0 + bias, a.act), activate(v1 + bias, a.act), activate(v2 + bias, a.act),
+                                activate(v3 + bias, a.act));
+            }
+        }
+    }
+}
+
+template <int BPR>
+static void launch_conv_stem_rows(const ConvArgs& c, const char* entry) {
+    auto kernel = conv_stem_k<BPR>;
+    static const int ok = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              kStemLdsBytes) == hipSuccess;
+    if (!ok) return fail(NNC_HIP_EDEVICE, entry, "hipFuncSetAttribute failed");
+    StemArgs a{c.in, c.w, c.bias, c.out, c.N, c.H, c.W, c.Co, c.Ho, c.Wo, c.ldw, c.act, c.N * c.Ho};
+    // two workgroups on every CU, each taking every G-th row
+    const int G = std::min(a.tiles, 2 * cu_count());
+    set_work(2.0 * c.Co * (double)c.Npix * kStemK, 0.0);
+    char name[64];
+    snprintf(name, sizeof name, "conv_stem_rows_w%d", 16 * BPR);
+    launch(name, kernel, dim3(G), dim3(256), kStemLdsBytes, a);
+}
+
+// The row kernel's shapes: ResNet's 224x224 stem (Wo 112) and 64x64 inputs,
+// once there are at least two rows per CU (ResNet-18 stem on MI355X: batch
+// 32 118.6 -> 90.8 us, batch 8 43.5 -> 32.3 us against the 64x128 tile
+// kernel; batch 1, 112 rows, 9.9 -> 13.5 us, so the tile kernel keeps it).
+// Tiles of two rows (8-wave workgroups, one per CU, one 9-row window for
+// both rows) measured slower: 94.7 / 35.7 / 21.0 us.
+static bool conv_stem_rows(const ConvArgs& a, const char* entry) {
+    if (!(a.sh == 2 && a.sw == 2 && a.ph == 3 && a.pw == 3 && a.H == 2 * a.Ho && a.W == 2 * a.Wo && a.Co <= 64 &&
+          !a.res && a.ldw >= 4 * kStemSteps && aligned16(a.in) && aligned16(a.out) && a.N * a.Ho < (1 << 30) &&
+          a.N * a.Ho >= 2 * cu_count()))
+        return false;
+    if (a.Wo == 112) return launch_conv_stem_rows<7>(a, entry), true;
+    if (a.Wo == 32) return launch_conv_stem_rows<2>(a, entry), true;
+    return false;
+}
+
 template <class T>
 static void launch_conv_stem(ConvArgs& a, const char* entry) {
     a.tiles_m = (int)ceil_div(a.Co, T::BM);
@@ -1380,7 +1559,9 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
             dma = true;
         }
     }
-    if (stem) {  // 64x128 tiles only once there are plenty of them (batch 32: 3136)
+    if (stem) {
+        if (conv_stem_rows(a, name)) return;
+        // 64x128 tiles only once there are plenty of them (batch 32: 3136)
         if (a.Co <= 64 && a.Npix >= 65536)
             return launch_conv_stem<ConvT64>(a, name);
         return launch_conv_stem<ConvTSmall>(a, name);

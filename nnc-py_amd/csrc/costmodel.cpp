@@ -74,6 +74,10 @@ const MfmaKind kGather64 = {"conv_gather_64", 64, 64, 4, 0.48, 1.2};
 const MfmaKind kGemm128 = {"gemm_128", 128, 128, 2, 0.75, 0.47};  // direct-to-LDS, two stages
 const MfmaKind kGemmDma64 = {"gemm_dma_64", 64, 64, 2, 0.60, 1.0};  // direct-to-LDS, four stages
 const MfmaKind kGemm64 = {"gemm_64", 64, 64, 4, 0.60, 1.0};         // register-staged
+// the stem's row kernel (input window in LDS): fraction of a CU's MFMA rate
+// over its 64 channels x Wo pixels x 148 k per row, fitted to ResNet-18's
+// stem at batch 8 and 32
+constexpr double kStemRowsEff = 0.55;
 constexpr double kColdUsPerMB = 0.061;  // weights (B operand) arriving from HBM, per MB
 constexpr double kFixupUsPerMB = 0.073; // fixup kernel: partial tiles read + finished tiles written, per MB
 constexpr double kFixupUsPerPart = 0.069; // fixup kernel: each partial summed into a tile (sequential)
@@ -214,6 +218,17 @@ void conv(const char* op, Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor*
     }
     const MfmaKind* k;
     char name[64];
+    const int64_t H = in->shape[2], W = in->shape[3];
+    if (stem && H == 2 * Ho && W == 2 * Wo && Co <= 64 && !res && (Wo == 112 || Wo == 32) && N * Ho >= 2 * kCUs) {
+        // conv.hip conv_stem_rows (a 7x7 stem with H == 2 Ho is stride 2,
+        // pad 3): two workgroups per CU, each taking every G-th output row
+        const int64_t rows = N * Ho, G = rows < 2 * kCUs ? rows : 2 * kCUs;
+        const double per_cu = (double)ceil_div(rows, G) * (G > kCUs ? 2 : 1);
+        const double row_flops = 2.0 * 64 * Wo * 148;
+        snprintf(name, sizeof name, "conv_stem_rows_w%d", (int)Wo);
+        record(op, name, kLaunchUs + per_cu * row_flops / (kMfmaF32 / kCUs * kStemRowsEff) * 1e6, flops, bytes);
+        return;
+    }
     if (stem) {
         k = (Co <= 64 && npix >= 65536) ? &kStem64x128 : &kStem64;
         snprintf(name, sizeof name, "conv_igemm_%dx%d_k7x7c3_dma", k->bm, k->bn);

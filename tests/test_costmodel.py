@@ -31,6 +31,7 @@ FIXTURE = json.loads((ROOT / "tests" / "golden" / "costmodel_mi355x.json").read_
 # the model's kernel names (those of libnnc_hip.so's profiling table) by the
 # device kernel that runs them
 FAMILY = [
+    (r"conv_stem_rows_", "conv_stem_k"),
     (r"conv_igemm_.*_dma$", "conv_dma_k"),
     (r"conv_igemm_", "conv_streamk_k"),
     (r"conv_streamk_fixup$", "conv_fixup_k"),

@@ -119,7 +119,9 @@ def test_check_rejects_a_missing_wait():
 
 def _library_kernels(lib: Path, tmp_path: Path) -> dict[str, list[str]]:
     fatbin = tmp_path / "fatbin"
-    subprocess.run(["objcopy", "--dump-section", f".hip_fatbin={fatbin}", str(lib)], check=True,
+    # input and output named: with the input alone objcopy also rewrites it
+    # in place (the library this process may have mapped)
+    subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", str(lib), str(fatbin)], check=True,
                    capture_output=True)
     data = fatbin.read_bytes()
     starts = [m.start() for m in re.finditer(re.escape(BUNDLE_MAGIC), data)]
