@@ -556,6 +556,9 @@ def main() -> int:
         "kernel_ms_per_step": round(gpu_ms, 4),
         "per_kernel": [{k: r[k] for k in ("kernel", "launches_per_step", "avg_us", "bound", "achieved", "unit", "frac")}
                        for r in table],
+        "per_kernel_timing": ("hipEvent pair on the library stream around each launch of directly launched nnc_run() "
+                              "calls: a launch of a few microseconds reads about 2.5 us long (event overhead), so "
+                              "small kernels' frac is understated; rocprofv3 kernel durations are in profiles/"),
         "cpu_baseline": cpu,
         "dropin": dropin,
         "host": platform.node(),
