@@ -188,9 +188,10 @@ def conv_symbol_pattern(name: str) -> re.Pattern | None:
         kh, kw = ("0", "0") if kh == "any" else (kh, kw)
         return re.compile(rf"conv_streamk_k<nnc::Tile<{bm}, {bn},[^>]*>, {kh}, {kw}, "
                           rf"{'true' if vec == 'v4' else 'false'}>")
-    m = re.fullmatch(r"conv_stem_rows_w(\d+)", name)
+    m = re.fullmatch(r"conv_stem_(rows|pool)_w(\d+)", name)
     if m:
-        return re.compile(rf"conv_stem_k<{int(m.group(1)) // 16}>")
+        kernel = "conv_stem_k" if m.group(1) == "rows" else "conv_stem_pool_k"
+        return re.compile(rf"{kernel}<{int(m.group(2)) // 16}>")
     m = re.fullmatch(r"gemm_mfma_(\d+)x(\d+)_\w+", name)
     if m:
         return re.compile(rf"gemm_streamk_k<nnc::Tile<{m.group(1)}, {m.group(2)},")

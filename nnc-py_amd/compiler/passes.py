@@ -360,21 +360,26 @@ def gap_gemm_lds_bytes(channels: int, plane: int) -> int:
     return 4 * (channels + channels * (plane + 1))
 
 
-# The stem streamed into its max pool (nnc_hip_conv_maxpool) computes each
-# conv row as one 128-pixel tile of which 112 pixels are used and holds two
-# workgroups per CU (its running maxima beside the accumulators), against the
-# unfused stem's three; its gather loads bound both kernels. Measured on
-# MI355X (hipGraph replay, the stem conv + max pool of ResNet-18): fused
-# 35.4 / 57.6 / 170.8 us at batch 1 / 8 / 32 against 15.1 / 53.6 / 149.4 us
-# unfused, although the fused kernel never writes the 103 MB (batch 32)
-# activation. Taken from this batch on: none by default.
-CONV_POOL_MIN_BATCH: int | None = None
+# The stem streamed into its max pool (nnc_hip_conv_maxpool). On the stem
+# row kernel's shapes (224x224 or 64x64 RGB, stride 2, pad 3) with at least
+# two conv rows per CU the library pools inside that kernel, bit-identical
+# to the unfused pair; measured on MI355X (ResNet-18's stem conv + max pool):
+# fused 96.3 / 41.6 / 36.8 us at batch 32 / 8 / 5 against 116.2 / 42.8 / 36.8
+# us unfused. Elsewhere it runs a 64x128-tile kernel that measured slower
+# than the pair (35.4 / 57.6 us at batch 1 / 8 against 15.1 / 53.6 us).
+# Fused from this many conv output rows (N x Ho) on the row kernel's shapes;
+# None: never (1: always, any shape the entry point takes).
+CONV_POOL_MIN_ROWS: int | None = 768
 
 
-def conv_pool_lds_bytes() -> int:
-    """LDS of the fused stem + pool kernel per workgroup: two operand stages
+def conv_pool_lds_bytes(wo: int | None = None) -> int:
+    """LDS of the fused stem + pool kernel per workgroup: on the row
+    kernel's shapes (conv rows of wo = 112 or 32 pixels) two input windows
+    of 3 channels x 7 rows of 2 wo + 8 floats; otherwise two operand stages
     of the 64 x 128 tile, the stem's 256-entry tap table, a wave-boundary
     exchange row and the bias."""
+    if wo in (112, 32):
+        return 4 * 2 * 3 * 7 * (2 * wo + 8)
     return 4 * (2 * (64 * 32 + 128 * 32) + 2 * 256 + 4 * 2 * 32 + 64)
 
 
@@ -384,8 +389,9 @@ def _stream_conv_pool(g: Graph, lds_budget: int) -> int:
     FusedConvMaxPool node (inputs: x, w, bias or ""; the conv's attrs),
     lowered to nnc_hip_conv_maxpool: each workgroup pools the conv rows it
     computes. Needs Co <= 64, even conv output sizes, rows of at most 128
-    pixels, batch >= CONV_POOL_MIN_BATCH."""
-    if CONV_POOL_MIN_BATCH is None:
+    pixels, N x Ho >= CONV_POOL_MIN_ROWS (unless forced with 1: the row
+    kernel's shapes, 224x224 or 64x64 input)."""
+    if CONV_POOL_MIN_ROWS is None:
         return 0
     fused = 0
     for conv in list(g.nodes):
@@ -396,7 +402,7 @@ def _stream_conv_pool(g: Graph, lds_budget: int) -> int:
         mid = conv.outputs[0]
         if len(w.shape) != 2 or len(x.shape) != 4 or x.shape[1] != 3 or mid in g.outputs:
             continue
-        if list(conv.attrs.get("kernel_shape", [])) != [7, 7] or w.shape[0] > 64 or x.shape[0] < CONV_POOL_MIN_BATCH:
+        if list(conv.attrs.get("kernel_shape", [])) != [7, 7] or w.shape[0] > 64:
             continue
         users = g.consumers(mid)
         if len(users) != 1 or users[0].op_type != "MaxPool":
@@ -406,12 +412,17 @@ def _stream_conv_pool(g: Graph, lds_budget: int) -> int:
                 or list(pool.attrs.get("pads", [0, 0, 0, 0])) != [1, 1, 1, 1]):
             continue
         _, _, ho, wo = g.tensors[mid].shape
-        if ho % 2 or wo % 2 or wo > 128 or conv_pool_lds_bytes() > lds_budget:
+        if ho % 2 or wo % 2 or wo > 128 or conv_pool_lds_bytes(wo) > lds_budget:
             continue
+        if CONV_POOL_MIN_ROWS > 1:
+            row_kernel = (wo in (112, 32) and x.shape[2] == 2 * ho and x.shape[3] == 2 * wo
+                          and list(conv.attrs.get("strides", [])) == [2, 2])
+            if not row_kernel or x.shape[0] * ho < CONV_POOL_MIN_ROWS:
+                continue
         conv.op_type = "FusedConvMaxPool"
         conv.outputs = list(pool.outputs)
         conv.metadata["fused_from"] = conv.metadata.get("fused_from", [conv.name]) + [pool.name]
-        conv.metadata["tile_stream"] = {"intermediate": mid, "lds_bytes": conv_pool_lds_bytes(),
+        conv.metadata["tile_stream"] = {"intermediate": mid, "lds_bytes": conv_pool_lds_bytes(wo),
                                         "budget": lds_budget, "hbm_bytes_saved": 2 * g.tensors[mid].nbytes}
         g.nodes.remove(pool)
         g.tensors.pop(mid, None)

@@ -1414,6 +1414,152 @@ static bool conv_stem_rows(const ConvArgs& a, const char* entry) {
     return false;
 }
 
+// ---------------------------------------------------------------------------
+// The stem's row kernel with the 3x3 / stride 2 / pad 1 max pool of its relu
+// output folded in (nnc_hip_conv_maxpool where the unfused stem runs
+// conv_stem_k): the conv rows of all images, in order, split into G
+// contiguous ranges of two or more rows, one per workgroup, each row
+// computed as in conv_stem_k (the next row's window loading during the
+// current row). Per row: bias + relu, then the max over conv columns 2j-1,
+// 2j, 2j+1 - a lane's four pixels 4q .. 4q+3 give pool columns 2q and 2q+1,
+// pixel 4q-1 comes from the lane 16 below (for the first lane group, the
+// previous block's last), the image's padding column counts as 0 - then down
+// the rows in registers: row 2p starts pool row p (with row 2p-1's maxima
+// when the range holds it), row 2p+1 completes it and it is stored. A
+// range's first pool row lacks the rows before the range unless the range
+// starts an image: the previous range writes its last maxima to pb.side and
+// conv_stem_pool_fixup_k takes the max of the two (with ranges of two or
+// more rows, at most one range boundary falls inside a pool row's three
+// conv rows). Relu values are never NaN or -0 and all are >= 0, so the max
+// is exact: the same bits as nnc_maxpool2d over conv_stem_k's output.
+template <int BPR>
+__global__ void __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
+conv_stem_pool_k(StemArgs a, PoolBand pb) {
+    typedef StemShape<BPR> S;
+    extern __shared__ __align__(16) float lds[];  // [2][3 ci][7 ky][LW]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, kq = lane >> 4;
+    const int G = gridDim.x;
+    const int g = xcd_remap(blockIdx.x, G);
+    const int t0 = (int)((int64_t)g * a.tiles / G), t1 = (int)((int64_t)(g + 1) * a.tiles / G);
+    if (t0 >= t1) return;  // (the host gives every range two or more rows)
+    const __amdgpu_buffer_rsrc_t rin = make_rsrc(a.in);
+    for (int r = threadIdx.x; r < 2 * 3 * 7; r += 256) {
+        float* row = lds + r * S::LW;
+        *reinterpret_cast<float4*>(row) = make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4*>(row + 4 + S::W) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    stem_window<BPR>(a, rin, lds, t0, wave, lane);
+    if (t0 + 1 < t1) stem_window<BPR>(a, rin, lds + S::BUF, t0 + 1, wave, lane);
+    const int co_a = 16 * wave + j;  // also this lane's output channel
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.w), (short)0, a.Co * a.ldw * 4, 0x00020000);
+    float A[kStemSteps];
+    int koff[kStemSteps];
+#pragma unroll
+    for (int s = 0; s < kStemSteps; ++s) {
+        const int k = 4 * s + kq;
+        A[s] = load_f32(rw, (uint32_t)(co_a * a.ldw + k) * 4u);
+        const int tap = k / 3, ci = k - tap * 3, ky = tap / 7, kx = tap - ky * 7;
+        koff[s] = k < kStemK ? ci * S::CP + ky * S::LW + kx + 1 + 2 * j : 0;
+    }
+    const float bias = a.bias && co_a < a.Co ? a.bias[co_a] : 0.f;
+    dma_barrier<0>();
+    float run[BPR][2];  // maxima of the current pool row's rows so far
+    bool have = false;
+    for (int t = t0, i = 0; t < t1; ++t, ++i) {
+        const float* B = lds + (i & 1) * S::BUF;
+        f32x4 acc[BPR];
+#pragma unroll
+        for (int b = 0; b < BPR; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float x[BPR];
+#pragma unroll
+        for (int b = 0; b < BPR; ++b) x[b] = B[koff[0] + 32 * b];
+#pragma unroll
+        for (int s = 0; s < kStemSteps; ++s) {
+            float xn[BPR];
+            if (s + 1 < kStemSteps) {
+#pragma unroll
+                for (int b = 0; b < BPR; ++b) xn[b] = B[koff[s + 1] + 32 * b];
+            }
+            if (s == kStemSteps - 1 && 4 * s + kq >= kStemK) {
+#pragma unroll
+                for (int b = 0; b < BPR; ++b) x[b] = 0.f;
+            }
+#pragma unroll
+            for (int b = 0; b < BPR; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b], A[s], acc[b], 0, 0, 0);
+            if (s + 1 < kStemSteps) {
+#pragma unroll
+                for (int b = 0; b < BPR; ++b) x[b] = xn[b];
+                __builtin_amdgcn_sched_group_barrier(0x100, (BPR + 1) / 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, BPR, 0);
+            }
+        }
+        dma_barrier<0>();
+        if (t + 2 < t1) stem_window<BPR>(a, rin, lds + (i & 1) * S::BUF, t + 2, wave, lane);
+        const int n = t / a.Ho, y = t - n * a.Ho;
+        // bias + relu, then the horizontal maxima
+        float h[BPR][2];
+        float prev3 = 0.f;  // this lane's last pixel of the previous block (0: the padding column)
+#pragma unroll
+        for (int b = 0; b < BPR; ++b) {
+            // element copies first: bit_cast of an ext-vector element is miscompiled
+            const float e0 = acc[b][0], e1 = acc[b][1], e2 = acc[b][2], e3 = acc[b][3];
+            const float v0 = activate(e0 + bias, kActRelu), v1 = activate(e1 + bias, kActRelu);
+            const float v2 = activate(e2 + bias, kActRelu), v3 = activate(e3 + bias, kActRelu);
+            // the pixel left of a lane's four sits in the lane 16 below; the
+            // first lane group's in the last group's previous block
+            const float left = __shfl(kq == 3 ? prev3 : v3, (lane + 48) & 63);
+            prev3 = v3;
+            h[b][0] = fmaxf(fmaxf(left, v0), v1);
+            h[b][1] = fmaxf(fmaxf(v1, v2), v3);
+        }
+        if (y == 0) have = false;  // an image's first row
+        if ((y & 1) == 0) {
+#pragma unroll
+            for (int b = 0; b < BPR; ++b)
+#pragma unroll
+                for (int k = 0; k < 2; ++k) run[b][k] = have ? fmaxf(run[b][k], h[b][k]) : h[b][k];
+        } else {
+            if (co_a < a.Co) {
+                float* o = pb.out + (((int64_t)n * a.Co + co_a) * pb.Hp + (y >> 1)) * pb.Wp + 2 * kq;
+#pragma unroll
+                for (int b = 0; b < BPR; ++b)
+                    *reinterpret_cast<float2*>(o + 8 * b) =
+                        have ? make_float2(fmaxf(run[b][0], h[b][0]), fmaxf(run[b][1], h[b][1]))
+                             : make_float2(h[b][0], h[b][1]);
+            }
+#pragma unroll
+            for (int b = 0; b < BPR; ++b)
+#pragma unroll
+                for (int k = 0; k < 2; ++k) run[b][k] = h[b][k];  // row 2p+1 also starts pool row p+1
+        }
+        have = true;
+    }
+    // the range's last maxima: the rows the next range's first pool row lacks
+    const int y_last = (t1 - 1) % a.Ho;
+    if (t1 < a.tiles && y_last + 1 < a.Ho && co_a < a.Co) {
+        float* sd = pb.side + ((int64_t)g * a.Co + co_a) * pb.Wp + 2 * kq;
+#pragma unroll
+        for (int b = 0; b < BPR; ++b) *reinterpret_cast<float2*>(sd + 8 * b) = make_float2(run[b][0], run[b][1]);
+    }
+}
+
+// Completes each range's first pool row (when the range does not start an
+// image) with the previous range's last maxima. Grid (ceil(Co * Wp / 256),
+// G - 1): one thread per (channel, column) of range g = blockIdx.y + 1.
+__global__ void __launch_bounds__(256) conv_stem_pool_fixup_k(PoolBand pb, int Co, int Ho, int rows, int G) {
+    const int g = blockIdx.y + 1;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= Co * pb.Wp) return;
+    const int t0 = (int)((int64_t)g * rows / G);
+    const int n = t0 / Ho, y0 = t0 - n * Ho;
+    if (y0 == 0) return;
+    const int co = i / pb.Wp, jj = i - co * pb.Wp;
+    float* o = pb.out + (((int64_t)n * Co + co) * pb.Hp + (y0 >> 1)) * pb.Wp + jj;
+    *o = fmaxf(*o, pb.side[((int64_t)(g - 1) * Co + co) * pb.Wp + jj]);
+}
+
 template <class T>
 static void launch_conv_stem(ConvArgs& a, const char* entry) {
     a.tiles_m = (int)ceil_div(a.Co, T::BM);
@@ -1583,6 +1729,33 @@ static void conv_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int 
 // nnc_hip_conv_maxpool: maxpool3x3/s2/p1(relu(conv(in, w) + b)) for the
 // packed 3-channel stem ([Co][Kp] rows, Co <= 64) with conv rows of at most
 // 128 pixels and even conv output sizes.
+template <int BPR>
+static void launch_conv_stem_pool(const ConvArgs& c, float* out, int Hp, int Wp, const char* entry) {
+    auto kernel = conv_stem_pool_k<BPR>;
+    static const int ok = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              kStemLdsBytes) == hipSuccess;
+    if (!ok) return fail(NNC_HIP_EDEVICE, entry, "hipFuncSetAttribute failed");
+    const int rows = c.N * c.Ho;
+    const StemArgs a{c.in, c.w, c.bias, nullptr, c.N, c.H, c.W, c.Co, c.Ho, c.Wo, c.ldw, kActRelu, rows};
+    // two workgroups on every CU, ranges of two or more rows
+    const int G = std::min(2 * cu_count(), rows / 2);
+    PoolBand pb{};
+    pb.out = out;
+    pb.Wr = c.Wo, pb.Hp = Hp, pb.Wp = Wp;
+    const size_t side_bytes = (size_t)G * c.Co * Wp * sizeof(float);
+    pb.side = workspace(side_bytes);
+    if (!pb.side) return partials_fail(entry, side_bytes);
+    set_work(2.0 * c.Co * (double)rows * c.Wo * kStemK, 0.0);
+    char name[64];
+    snprintf(name, sizeof name, "conv_stem_pool_w%d", 16 * BPR);
+    launch(name, kernel, dim3((unsigned)G), dim3(256), kStemLdsBytes, a, pb);
+    if (G > 1) {
+        set_work(0.0, 12.0 * (double)(G - 1) * c.Co * Wp);
+        launch("conv_stem_pool_fixup", conv_stem_pool_fixup_k, dim3((unsigned)ceil_div((int64_t)c.Co * Wp, 256), G - 1),
+               dim3(256), 0, pb, c.Co, c.Ho, rows, G);
+    }
+}
+
 static void conv_maxpool_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw, int ph,
                              int pw, const char* name) {
     typedef ConvT64 T;
@@ -1617,6 +1790,17 @@ static void conv_maxpool_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int 
     const int64_t npix = (int64_t)a.N * Ho * 128;
     if (in_bytes >= ((int64_t)1 << 31) || npix >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "input of 2 GiB or more");
     if (a.N == 0) return;
+    // where the unfused stem runs its row kernel, the pool folds into that
+    // (the same convolution bits)
+    if (sh == 2 && sw == 2 && ph == 3 && pw == 3 && a.H == 2 * Ho && a.W == 2 * Wr && (Wr == 112 || Wr == 32) &&
+        aligned16(a.in) && aligned16(out->data) && kp >= 4 * kStemSteps && (int64_t)a.N * Ho >= 2 * cu_count()) {
+        ConvArgs c = a;
+        c.Ho = Ho;
+        c.Wo = Wr;
+        c.ldw = (int)kp;
+        if (Wr == 112) return launch_conv_stem_pool<7>(c, (float*)out->data, Hp, Wp, name);
+        return launch_conv_stem_pool<2>(c, (float*)out->data, Hp, Wp, name);
+    }
     a.Ho = Ho;
     a.Wo = 128;  // rows of 128 pixels: one tile per conv row
     a.K = (int)K;

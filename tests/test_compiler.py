@@ -312,13 +312,13 @@ def test_conv_pool_tile_streaming_pass(pkg, oracle_lib):
     max). Below the batch limit, or by default, the pair stays."""
     from nnc_py_amd.compiler import Executor, build_program, passes, zoo
     assert build_program(zoo.resnet18(batch=2, seed=0), opt_level=3).calls[0].op == "nnc_hip_conv_packed"
-    old = passes.CONV_POOL_MIN_BATCH
-    passes.CONV_POOL_MIN_BATCH = 2
+    old = passes.CONV_POOL_MIN_ROWS
+    passes.CONV_POOL_MIN_ROWS = 224  # batch 2 of 112 conv rows, not batch 1
     try:
         prog = build_program(zoo.resnet18(batch=2, seed=0), opt_level=3)
         small = build_program(zoo.resnet18(batch=1, seed=0), opt_level=3)
     finally:
-        passes.CONV_POOL_MIN_BATCH = old
+        passes.CONV_POOL_MIN_ROWS = old
     ops = [c.op for c in prog.calls]
     assert ops[0] == "nnc_hip_conv_maxpool" and "nnc_maxpool2d" not in ops and len(ops) == 19
     assert [a[1] for a in prog.calls[0].args[4:]] == [7, 7, 2, 2, 3, 3]

@@ -567,12 +567,14 @@ def _conv_maxpool_case(rng, n, h, w, co=64, bias=True):
 
 
 @pytest.mark.parametrize("n,h,w,co,bias", [(1, 224, 224, 64, True), (2, 64, 100, 64, True), (8, 224, 224, 64, True),
-                                           (3, 32, 255, 40, False)])
+                                           (3, 32, 255, 40, False), (5, 224, 224, 64, True), (16, 64, 64, 40, False)])
 def test_conv_maxpool_stem(n, h, w, co, bias, hip, dmem, abi, oracle_lib):
     """The stem streamed into its max pool against the oracle's packed conv
     + relu + nnc_maxpool2d: within the conv bar of the oracle's double sums
     (the max itself is exact). Covers one-row and two-row bands with their
-    band-boundary fixup, a full 128-pixel row (w = 255), Co < 64."""
+    band-boundary fixup, a full 128-pixel row (w = 255), Co < 64; from 512
+    conv rows on (5 x 224x224, 16 x 64x64) the row kernel's fused pool with
+    ranges of two rows."""
     case = _conv_maxpool_case(np.random.default_rng(n + h + w), n, h, w, co, bias)
     print(f"case {case['name']}", flush=True)
     exp = caserun.run_case(oracle_lib, case, abi)["out"]
@@ -581,6 +583,29 @@ def test_conv_maxpool_stem(n, h, w, co, bias, hip, dmem, abi, oracle_lib):
     assert runtime.last_error()[0] == 0, runtime.last_error()[1]
     _check(got, exp, case["name"])
     assert (got >= 0).all()
+
+
+@pytest.mark.parametrize("n", [8, 20])
+def test_conv_stem_pool_matches_unfused_bits(n, hip, dmem, abi):
+    """The row kernel's fused pool against the same GPU convolution
+    (nnc_hip_conv_packed, the row kernel at these sizes) followed by
+    nnc_maxpool2d: the same bits. 8 images: 448 ranges of two rows; 20
+    images: ranges of four and five rows, so ranges start on odd rows too."""
+    case = _conv_maxpool_case(np.random.default_rng(31 + n), n, 224, 224, 64, True)
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    t = case["tensors"]
+    conv = {"name": "conv", "op": "nnc_hip_conv_packed",
+            "tensors": {"x": t["x"], "w": t["w"], "b": t["b"], "out": np.zeros((n, 64, 112, 112), np.float32)},
+            "args": [("t", "x"), ("t", "w"), ("t", "b"), ("null",), ("t", "out")] + [("i", v) for v in (7, 7, 2, 2, 3, 3, 1)],
+            "outputs": ["out"], "bar": "fp"}
+    mid = caserun.run_case(hip, conv, abi, dmem)["out"]
+    pool = {"name": "pool", "op": "nnc_maxpool2d", "tensors": {"x": mid, "out": np.zeros_like(got)},
+            "args": [("t", "x"), ("t", "out")] + [("i", v) for v in (3, 3, 2, 2, 1, 1)], "outputs": ["out"],
+            "bar": "exact"}
+    exp = caserun.run_case(hip, pool, abi, dmem)["out"]
+    from nnc_py_amd import runtime
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    assert caserun.same_bits(got, exp)
 
 
 def test_conv_maxpool_rejections(hip, dmem, abi):

@@ -316,12 +316,12 @@ def test_conv_pool_streamed_program_matches_oracle(batch, hip, dmem, abi, oracle
     end-to-end bar (the two stems sum their products in different orders)."""
     from nnc_py_amd.compiler import Executor, build_program, passes, zoo
     x = np.random.default_rng(9).standard_normal((batch, 3, 224, 224)).astype(np.float32)
-    old = passes.CONV_POOL_MIN_BATCH
-    passes.CONV_POOL_MIN_BATCH = 1
+    old = passes.CONV_POOL_MIN_ROWS
+    passes.CONV_POOL_MIN_ROWS = 1
     try:
         prog = build_program(zoo.resnet18(batch=batch, seed=1), opt_level=3)
     finally:
-        passes.CONV_POOL_MIN_BATCH = old
+        passes.CONV_POOL_MIN_ROWS = old
     call = prog.calls[0]
     assert call.op == "nnc_hip_conv_maxpool"
     out_name = call.args[3][1]
