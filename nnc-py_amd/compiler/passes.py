@@ -364,12 +364,13 @@ def gap_gemm_lds_bytes(channels: int, plane: int) -> int:
 # row kernel's shapes (224x224 or 64x64 RGB, stride 2, pad 3) with at least
 # two conv rows per CU the library pools inside that kernel, bit-identical
 # to the unfused pair; measured on MI355X (ResNet-18's stem conv + max pool):
-# fused 96.3 / 41.6 / 36.8 us at batch 32 / 8 / 5 against 116.2 / 42.8 / 36.8
+# fused 94.5 / 36.1 / 34.2 us at batch 32 / 8 / 5 against 115.3 / 42.7 / 36.6
 # us unfused. Elsewhere it runs a 64x128-tile kernel that measured slower
 # than the pair (35.4 / 57.6 us at batch 1 / 8 against 15.1 / 53.6 us).
-# Fused from this many conv output rows (N x Ho) on the row kernel's shapes;
-# None: never (1: always, any shape the entry point takes).
-CONV_POOL_MIN_ROWS: int | None = 768
+# Fused from this many conv output rows (N x Ho) on the row kernel's shapes:
+# two rows per CU of MI355X's 256, the row kernel's own floor (batch 5 at
+# 224x224); None: never (1: always, any shape the entry point takes).
+CONV_POOL_MIN_ROWS: int | None = 512
 
 
 def conv_pool_lds_bytes(wo: int | None = None) -> int:

@@ -842,6 +842,7 @@ __global__ void __launch_bounds__(T::THREADS, DmaStage<T>::MIN_WAVES) conv_dma_k
 struct PoolBand {
     float* out;   // [N][Co][Hp][Wp]
     float* side;  // [G][Co][Wp]: a range's last-row maxima for the next range's first pool row
+    int* cnt;     // conv_stem_pool_k: [G] range-boundary arrival counters, zero between launches
     int Wr, Hp, Wp;
     int pairs;    // N * Hp: pool rows of all images, two conv rows each
 };
@@ -1427,11 +1428,15 @@ static bool conv_stem_rows(const ConvArgs& a, const char* entry) {
 // the rows in registers: row 2p starts pool row p (with row 2p-1's maxima
 // when the range holds it), row 2p+1 completes it and it is stored. A
 // range's first pool row lacks the rows before the range unless the range
-// starts an image: the previous range writes its last maxima to pb.side and
-// conv_stem_pool_fixup_k takes the max of the two (with ranges of two or
-// more rows, at most one range boundary falls inside a pool row's three
-// conv rows). Relu values are never NaN or -0 and all are >= 0, so the max
-// is exact: the same bits as nnc_maxpool2d over conv_stem_k's output.
+// starts an image: the previous range writes its last maxima to pb.side
+// (with ranges of two or more rows, at most one range boundary falls inside
+// a pool row's three conv rows). Both ranges of a boundary write their part
+// with device-scope stores and count themselves in on the boundary's
+// counter (pb.cnt) at the end, and the second to arrive takes the max and
+// writes the pool row (the stream-K finish's protocol, finish_arrive_pair).
+// Relu values are never
+// NaN or -0 and all are >= 0, so the max is exact: the same bits as
+// nnc_maxpool2d over conv_stem_k's output.
 template <int BPR>
 __global__ void __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
 conv_stem_pool_k(StemArgs a, PoolBand pb) {
@@ -1467,6 +1472,12 @@ conv_stem_pool_k(StemArgs a, PoolBand pb) {
     dma_barrier<0>();
     float run[BPR][2];  // maxima of the current pool row's rows so far
     bool have = false;
+    // boundaries shared with the neighbouring ranges (counted in at the end)
+    const bool start_shared = g > 0 && t0 % a.Ho != 0;
+    const bool end_shared = t1 < a.tiles && (t1 - 1) % a.Ho + 1 < a.Ho;
+    const __amdgpu_buffer_rsrc_t rout = make_rsrc(pb.out), rside = make_rsrc(pb.side);
+    float first[BPR][2];  // this range's part of its first pool row (start_shared)
+    bool first_pending = start_shared;
     for (int t = t0, i = 0; t < t1; ++t, ++i) {
         const float* B = lds + (i & 1) * S::BUF;
         f32x4 acc[BPR];
@@ -1522,13 +1533,22 @@ conv_stem_pool_k(StemArgs a, PoolBand pb) {
                 for (int k = 0; k < 2; ++k) run[b][k] = have ? fmaxf(run[b][k], h[b][k]) : h[b][k];
         } else {
             if (co_a < a.Co) {
-                float* o = pb.out + (((int64_t)n * a.Co + co_a) * pb.Hp + (y >> 1)) * pb.Wp + 2 * kq;
+                const int64_t oe = (((int64_t)n * a.Co + co_a) * pb.Hp + (y >> 1)) * pb.Wp + 2 * kq;
 #pragma unroll
-                for (int b = 0; b < BPR; ++b)
-                    *reinterpret_cast<float2*>(o + 8 * b) =
-                        have ? make_float2(fmaxf(run[b][0], h[b][0]), fmaxf(run[b][1], h[b][1]))
-                             : make_float2(h[b][0], h[b][1]);
+                for (int b = 0; b < BPR; ++b) {
+                    const float m0 = have ? fmaxf(run[b][0], h[b][0]) : h[b][0];
+                    const float m1 = have ? fmaxf(run[b][1], h[b][1]) : h[b][1];
+                    if (first_pending) {  // the shared pool row: for the finishing range
+                        first[b][0] = m0;
+                        first[b][1] = m1;
+                        store_partial(rout, (uint32_t)(oe + 8 * b) * 4u, m0);
+                        store_partial(rout, (uint32_t)(oe + 8 * b + 1) * 4u, m1);
+                    } else {
+                        *reinterpret_cast<float2*>(pb.out + oe + 8 * b) = make_float2(m0, m1);
+                    }
+                }
             }
+            first_pending = false;
 #pragma unroll
             for (int b = 0; b < BPR; ++b)
 #pragma unroll
@@ -1536,28 +1556,50 @@ conv_stem_pool_k(StemArgs a, PoolBand pb) {
         }
         have = true;
     }
-    // the range's last maxima: the rows the next range's first pool row lacks
-    const int y_last = (t1 - 1) % a.Ho;
-    if (t1 < a.tiles && y_last + 1 < a.Ho && co_a < a.Co) {
-        float* sd = pb.side + ((int64_t)g * a.Co + co_a) * pb.Wp + 2 * kq;
+    // the range's last maxima: the rows the next range's first pool row
+    // lacks (device-scope stores: the next range may read them in-kernel)
+    if (end_shared && co_a < a.Co) {
+        const uint32_t se = (uint32_t)(((int64_t)g * a.Co + co_a) * pb.Wp + 2 * kq) * 4u;
 #pragma unroll
-        for (int b = 0; b < BPR; ++b) *reinterpret_cast<float2*>(sd + 8 * b) = make_float2(run[b][0], run[b][1]);
+        for (int b = 0; b < BPR; ++b) {
+            store_partial(rside, se + 32u * b, run[b][0]);
+            store_partial(rside, se + 32u * b + 4u, run[b][1]);
+        }
     }
-}
-
-// Completes each range's first pool row (when the range does not start an
-// image) with the previous range's last maxima. Grid (ceil(Co * Wp / 256),
-// G - 1): one thread per (channel, column) of range g = blockIdx.y + 1.
-__global__ void __launch_bounds__(256) conv_stem_pool_fixup_k(PoolBand pb, int Co, int Ho, int rows, int G) {
-    const int g = blockIdx.y + 1;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= Co * pb.Wp) return;
-    const int t0 = (int)((int64_t)g * rows / G);
-    const int n = t0 / Ho, y0 = t0 - n * Ho;
-    if (y0 == 0) return;
-    const int co = i / pb.Wp, jj = i - co * pb.Wp;
-    float* o = pb.out + (((int64_t)n * Co + co) * pb.Hp + (y0 >> 1)) * pb.Wp + jj;
-    *o = fmaxf(*o, pb.side[((int64_t)(g - 1) * Co + co) * pb.Wp + jj]);
+    bool last_start, last_end;
+    finish_arrive_pair(pb.cnt + g, start_shared, pb.cnt + g + 1, end_shared, last_start, last_end);
+    if (co_a >= a.Co) return;
+    // every load of a finish before its stores (the next range's part is
+    // read from, and its max written to, the same addresses)
+    if (last_start) {  // this range's first pool row with the previous range's last maxima
+        const int n = t0 / a.Ho;
+        const int64_t oe = (((int64_t)n * a.Co + co_a) * pb.Hp + ((t0 % a.Ho) >> 1)) * pb.Wp + 2 * kq;
+        const uint32_t se = (uint32_t)(((int64_t)(g - 1) * a.Co + co_a) * pb.Wp + 2 * kq) * 4u;
+        float sv[BPR][2];
+#pragma unroll
+        for (int b = 0; b < BPR; ++b) {
+            sv[b][0] = load_partial(rside, se + 32u * b);
+            sv[b][1] = load_partial(rside, se + 32u * b + 4u);
+        }
+#pragma unroll
+        for (int b = 0; b < BPR; ++b)
+            *reinterpret_cast<float2*>(pb.out + oe + 8 * b) =
+                make_float2(fmaxf(first[b][0], sv[b][0]), fmaxf(first[b][1], sv[b][1]));
+    }
+    if (last_end) {  // the next range's first pool row with this range's last maxima
+        const int n = t1 / a.Ho;
+        const int64_t oe = (((int64_t)n * a.Co + co_a) * pb.Hp + ((t1 % a.Ho) >> 1)) * pb.Wp + 2 * kq;
+        float pv[BPR][2];
+#pragma unroll
+        for (int b = 0; b < BPR; ++b) {
+            pv[b][0] = load_partial(rout, (uint32_t)(oe + 8 * b) * 4u);
+            pv[b][1] = load_partial(rout, (uint32_t)(oe + 8 * b + 1) * 4u);
+        }
+#pragma unroll
+        for (int b = 0; b < BPR; ++b)
+            *reinterpret_cast<float2*>(pb.out + oe + 8 * b) =
+                make_float2(fmaxf(run[b][0], pv[b][0]), fmaxf(run[b][1], pv[b][1]));
+    }
 }
 
 template <class T>
@@ -1745,15 +1787,16 @@ static void launch_conv_stem_pool(const ConvArgs& c, float* out, int Hp, int Wp,
     const size_t side_bytes = (size_t)G * c.Co * Wp * sizeof(float);
     pb.side = workspace(side_bytes);
     if (!pb.side) return partials_fail(entry, side_bytes);
+    // boundary counters: the ranges finish the shared pool rows themselves
+    // (every thread state holds far more counters than G from its creation)
+    pb.cnt = tile_counters((size_t)G);
+    if (!pb.cnt) return fail(NNC_HIP_ENOMEM, entry, "no %d range-boundary counters", G);
+    if (ts().fixed)
+        launch("zero_tile_counters", zero_counters_k, dim3((unsigned)ceil_div(G, 256)), dim3(256), 0, pb.cnt, G);
     set_work(2.0 * c.Co * (double)rows * c.Wo * kStemK, 0.0);
     char name[64];
     snprintf(name, sizeof name, "conv_stem_pool_w%d", 16 * BPR);
     launch(name, kernel, dim3((unsigned)G), dim3(256), kStemLdsBytes, a, pb);
-    if (G > 1) {
-        set_work(0.0, 12.0 * (double)(G - 1) * c.Co * Wp);
-        launch("conv_stem_pool_fixup", conv_stem_pool_fixup_k, dim3((unsigned)ceil_div((int64_t)c.Co * Wp, 256), G - 1),
-               dim3(256), 0, pb, c.Co, c.Ho, rows, G);
-    }
 }
 
 static void conv_maxpool_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh, int kw, int sh, int sw, int ph,
@@ -1793,7 +1836,8 @@ static void conv_maxpool_run(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int 
     // where the unfused stem runs its row kernel, the pool folds into that
     // (the same convolution bits)
     if (sh == 2 && sw == 2 && ph == 3 && pw == 3 && a.H == 2 * Ho && a.W == 2 * Wr && (Wr == 112 || Wr == 32) &&
-        aligned16(a.in) && aligned16(out->data) && kp >= 4 * kStemSteps && (int64_t)a.N * Ho >= 2 * cu_count()) {
+        aligned16(a.in) && aligned16(out->data) && kp >= 4 * kStemSteps && (int64_t)a.N * Ho >= 2 * cu_count() &&
+        (int64_t)a.N * a.Co * Hp * Wp * 4 < ((int64_t)1 << 31)) {
         ConvArgs c = a;
         c.Ho = Ho;
         c.Wo = Wr;

@@ -544,8 +544,8 @@ void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh,
     if (sh == 2 && sw == 2 && ph == 3 && pw == 3 && in->shape[2] == 2 * Ho && in->shape[3] == 2 * Wo &&
         (Wo == 112 || Wo == 32) && N * Ho >= 2 * kCUs) {
         // conv.hip launch_conv_stem_pool: the stem's row kernel over
-        // contiguous ranges of rows (two workgroups per CU), then the fixup
-        // of each range's first pool row
+        // contiguous ranges of rows (two workgroups per CU); neighbouring
+        // ranges finish the pool row they share in-kernel, over counters
         const int64_t rows = N * Ho, G = rows / 2 < 2 * kCUs ? rows / 2 : 2 * kCUs;
         const double per_cu = (double)ceil_div(rows, G) * (G > kCUs ? 2 : 1);
         const double row_flops = 2.0 * 64 * Wo * 148;
@@ -553,7 +553,6 @@ void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh,
         snprintf(name, sizeof name, "conv_stem_pool_w%d", (int)Wo);
         record("nnc_hip_conv_maxpool", name, kLaunchUs + per_cu * row_flops / (kMfmaF32 / kCUs * kStemRowsEff) * 1e6,
                2.0 * Co * (double)rows * Wo * K, bytes);
-        if (G > 1) stream_kernel("nnc_hip_conv_maxpool", "conv_stem_pool_fixup", 12.0 * (double)(G - 1) * Co * Wp);
         return;
     }
     const int tiles = (int)(N * Ho);  // one conv row per tile: whole tiles, one band's rows per workgroup

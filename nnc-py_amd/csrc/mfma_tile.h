@@ -501,6 +501,11 @@ __device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t ws, uint32_
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), ws, (int)byte_off, 0, kDeviceScope);
 }
 
+// One float of a partial, loaded with device-scope coherence.
+__device__ __forceinline__ float load_partial(__amdgpu_buffer_rsrc_t ws, uint32_t byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ws, (int)byte_off, 0, kDeviceScope));
+}
+
 // Four floats of a partial, loaded with device-scope coherence.
 __device__ __forceinline__ f32x4 load_partial4(__amdgpu_buffer_rsrc_t ws, uint32_t byte_off) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ws, (int)byte_off, 0, kDeviceScope));
@@ -530,6 +535,34 @@ __device__ __forceinline__ bool finish_arrive(int* counter, int arrivals_before_
     }
     __syncthreads();
     return last;
+}
+
+// finish_arrive for a workgroup that shares two pieces of work, each with
+// one other workgroup (counter c0 when on0, c1 when on1; the flags uniform
+// over the workgroup): the same release and acquire, both atomics between
+// one pair of barriers. last0 / last1: this workgroup arrived second.
+__device__ __forceinline__ void finish_arrive_pair(int* c0, bool on0, int* c1, bool on1, bool& last0, bool& last1) {
+    __shared__ int last[2];
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int l0 = 0, l1 = 0;
+        if (on0) {
+            l0 = __hip_atomic_fetch_add(c0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+            if (l0) __hip_atomic_store(c0, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (on1) {
+            l1 = __hip_atomic_fetch_add(c1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+            if (l1) __hip_atomic_store(c1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        last[0] = l0;
+        last[1] = l1;
+    }
+    __syncthreads();
+    last0 = last[0];
+    last1 = last[1];
 }
 
 // Direct-to-LDS buffer loads: lane l's `size` bytes land at LDS[lds_dst +

@@ -33,7 +33,6 @@ FIXTURE = json.loads((ROOT / "tests" / "golden" / "costmodel_mi355x.json").read_
 FAMILY = [
     (r"conv_stem_rows_", "conv_stem_k"),
     (r"conv_stem_pool_w", "conv_stem_pool_k"),
-    (r"conv_stem_pool_fixup$", "conv_stem_pool_fixup_k"),
     (r"conv_igemm_.*_dma$", "conv_dma_k"),
     (r"conv_igemm_", "conv_streamk_k"),
     (r"conv_streamk_fixup$", "conv_fixup_k"),

@@ -34,8 +34,8 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 BUNDLE_MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 
-PARTIAL_STORE = re.compile(r"^\s*buffer_store_dword\s.*\bsc1\b")
-PARTIAL_LOAD = re.compile(r"^\s*buffer_load_dwordx4\s.*\bsc1\b")
+PARTIAL_STORE = re.compile(r"^\s*buffer_store_dword(x2)?\s.*\bsc1\b")
+PARTIAL_LOAD = re.compile(r"^\s*buffer_load_dword(x2|x4)?\s.*\bsc1\b")
 COUNTER_RMW = re.compile(r"^\s*(global|buffer|flat)_atomic_add\w*\s.*\bsc0\b")  # sc0: returns the old value
 WAIT_VM0 = re.compile(r"^\s*s_waitcnt\s.*\bvmcnt\(0\)")
 BARRIER = re.compile(r"^\s*s_barrier\b")
@@ -45,10 +45,13 @@ L2_MAINT = re.compile(r"^\s*buffer_(wbl2|inv)\b")
 def check_finish_order(lines: list[str]) -> None:
     """Assert the protocol's order on one kernel's instructions, in the
     order the assembler lays them out (the finish code is straight-line
-    between the last partial store and the first partial load)."""
+    between the last partial store and the first partial load). A kernel
+    that shares two pieces of work (finish_arrive_pair) has two counter
+    atomics, both between the same two barriers."""
     rmw = [i for i, l in enumerate(lines) if COUNTER_RMW.match(l)]
-    assert len(rmw) == 1, f"expected one counter atomic, found {len(rmw)}"
-    a = rmw[0]
+    assert 1 <= len(rmw) <= 2, f"expected one or two counter atomics, found {len(rmw)}"
+    a, a_last = rmw[0], rmw[-1]
+    assert not any(BARRIER.match(lines[i]) for i in range(a, a_last)), "the counter atomics straddle a barrier"
     stores = [i for i, l in enumerate(lines) if PARTIAL_STORE.match(l)]
     assert stores and stores[-1] < a, "no device-scope partial store before the counter atomic"
     # release: the stores' completion wait, then a barrier, before the atomic
@@ -57,10 +60,10 @@ def check_finish_order(lines: list[str]) -> None:
     assert b1 is not None, "no barrier between the partial stores and the counter atomic"
     assert any(WAIT_VM0.match(lines[i]) for i in range(stores[-1], b1)), \
         "the partial stores are not waited for (vmcnt(0)) before the barrier"
-    # acquire: the atomic has returned before the barrier that releases the readers
-    b2 = next((i for i in range(a, len(lines)) if BARRIER.match(lines[i])), None)
+    # acquire: the atomics have returned before the barrier that releases the readers
+    b2 = next((i for i in range(a_last, len(lines)) if BARRIER.match(lines[i])), None)
     assert b2 is not None, "no barrier after the counter atomic"
-    assert any(WAIT_VM0.match(lines[i]) for i in range(a, b2)), \
+    assert any(WAIT_VM0.match(lines[i]) for i in range(a_last, b2)), \
         "the counter atomic's return is not waited for before the barrier"
     loads = [i for i, l in enumerate(lines) if PARTIAL_LOAD.match(l)]
     assert loads, "no device-scope partial loads"
@@ -157,8 +160,9 @@ def test_finish_protocol_order_in_library(tmp_path, pkg):
     kernels = _library_kernels(runtime.LIB_PATH, tmp_path)
     finishing = {k: v for k, v in kernels.items() if any(COUNTER_RMW.match(l) for l in v)}
     families = {re.match(r"_ZN3nnc\d+(\w+?_k)", k).group(1) for k in finishing}
-    # the GEMM's and the convolution's direct-to-LDS kernels finish split tiles in-kernel
-    assert {"gemm_dma_k", "conv_dma_k"} <= families, families
+    # the GEMM's and the convolution's direct-to-LDS kernels finish split
+    # tiles in-kernel, the stem's pool its range boundaries
+    assert {"gemm_dma_k", "conv_dma_k", "conv_stem_pool_k"} <= families, families
     for name, lines in finishing.items():
         try:
             check_finish_order(lines)

@@ -363,8 +363,10 @@ def test_gemm_layouts_and_streamk(shape, hip, dmem, abi, oracle_lib):
 # the last of their 3-4 workgroups (stream-K plan with 256 or 512 resident
 # workgroups): 64 channels 3x3 over 8 x 56x56 (64x128 tiles, 196 tiles of 18
 # slices), GEMM 512x512x288 (64x64 tiles, 64 tiles of 9 slices) and
-# 2048x1024x256 (128x128 tiles, 128 tiles of 8 slices).
-IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "gemm_512x512x288", "gemm_2048x1024x256"]
+# 2048x1024x256 (128x128 tiles, 128 tiles of 8 slices); and the stem's fused
+# max pool at 10 x 224x224, whose 512 ranges of two or three conv rows
+# finish the pool rows they share with their neighbours in the kernel.
+IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "gemm_512x512x288", "gemm_2048x1024x256", "stem_pool_b10"]
 
 
 @pytest.mark.parametrize("which", IN_KERNEL_FINISH_CASES)
@@ -378,6 +380,8 @@ def test_in_kernel_finish_alternating_inputs(which, hip, dmem, abi, oracle_lib):
         rng = np.random.default_rng(seed)
         if which == "conv_b8_64c_56":
             return _packed_case(rng, 8, 64, 56, 64, 3, 1, 1)
+        if which == "stem_pool_b10":
+            return _conv_maxpool_case(rng, 10, 224, 224, 64, True)
         m, n, k = {"gemm_512x512x288": (512, 512, 288), "gemm_2048x1024x256": (2048, 1024, 256)}[which]
         return _gemm_case(rng, m, n, k, 0, 1, True)
     cases = [make(41), make(42)]
