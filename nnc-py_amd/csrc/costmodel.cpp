@@ -281,6 +281,16 @@ void gemm(const char* op, int M, int N, int K, int batches, bool a_kc, bool b_kc
         record(op, K % 4 == 0 ? "dot_rows_v4" : "dot_rows_s1", kLaunchUs + b / (kHbm * kStreamEff) * 1e6, flops, b);
         return;
     }
+    if (batches == 1 && a_kc && b_kc && M <= 32 && K <= 1024 && K % 4 == 0) {
+        // gemm.hip gemm_skinny_nt_k: 16 columns per workgroup, all rows, K
+        // over 8 waves; latency-bound: one round trip for every wave's loads
+        // (1 us), then its chunks' 16x16x4 MFMAs (32 cycles each at 2.1 GHz)
+        const double b = 4.0 * ((double)M * K + (double)N * K + (double)M * N);
+        const double chain_us = (double)ceil_div(ceil_div(K, 16), 8) * 4 * (M > 16 ? 2 : 1) * 32 / 2100.0;
+        record(op, M > 16 ? "gemm_skinny_nt_32" : "gemm_skinny_nt_16",
+               kLaunchUs + 1.0 + chain_us + b / (kHbm * kStreamEff) * 1e6, flops, b);
+        return;
+    }
     const bool a4 = a_kc ? K % 4 == 0 : M % 4 == 0;  // 16-byte loads along the contiguous axis
     const bool b4 = b_kc ? K % 4 == 0 : N % 4 == 0;
     const bool big = (int64_t)M * N * batches >= (int64_t)128 * 128 * 2 * kCUs / 4 && M >= 128 && N >= 128;

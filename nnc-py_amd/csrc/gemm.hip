@@ -14,6 +14,9 @@
 //              K split across workgroups, deterministic partial reduction)
 //   dot_k      out[i][j] = sum_k A[i][k] * B[j][k]  (both k-contiguous; one
 //              wave per output, shuffle reduction)
+// and products with at most 32 output rows, both operands k-contiguous, one
+// MFMA launch without partials (gemm_skinny_nt_k: 16 columns per workgroup,
+// K split over its waves, summed in LDS).
 //
 // The reference accumulates Gemm in fp64 and MatMul with a Kahan fp32 sum;
 // here every product accumulates in fp32 (two-level in the register-staged
@@ -621,6 +624,79 @@ __global__ void __launch_bounds__(256) dot_k(GemmArgs g) {
     if (lane == 0) g.out[(int64_t)i * g.N + j] = gemm_finish(g, i, j, acc);
 }
 
+// Few output rows, both operands k-contiguous (a classifier at small batch:
+// [M <= 32, K] x [N, K]^T). The tile kernels would give each 64x64 tile to
+// many workgroups and finish it in a second launch; here a workgroup owns 16
+// output columns for all rows and its 8 waves split K, so the whole product
+// is one launch with no partials in memory. Wave w takes K chunks of 16
+// [w*C/8, (w+1)*C/8); lane (i = lane % 16, q = lane / 16) loads A row i and B
+// row j0 + i at k = 16c + 4q .. +3 as one 16-byte load each, and the four
+// 16x16x4 MFMAs of a chunk take element e of those loads (k = 16c + 4q + e for
+// lane group q: every k exactly once). MB 16-row blocks (M <= 16 MB). The
+// waves' 16 x 16 sums meet in LDS and are added in wave order. Needs K <= 1024
+// (at most 8 chunks per wave, all loads issued before the first MFMA), K % 4
+// == 0, 16-byte aligned rows, and both operands under 2 GiB of byte offsets;
+// rows beyond M or N and k beyond K read 0.
+static constexpr int kSkinnyWaves = 8, kSkinnyMaxK = 1024, kSkinnyRows = 32;
+template <int MB>
+__global__ void __launch_bounds__(64 * kSkinnyWaves) gemm_skinny_nt_k(GemmArgs g) {
+    constexpr int CH = kSkinnyMaxK / 16 / kSkinnyWaves;  // chunks per wave at most
+    __shared__ float part[kSkinnyWaves][MB][4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 15, q = lane >> 4;
+    const int j0 = blockIdx.x * 16;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A), rb = make_rsrc(g.B);
+    const int chunks = (g.K + 15) >> 4;
+    const int c0 = wave * chunks / kSkinnyWaves, c1 = (wave + 1) * chunks / kSkinnyWaves;
+    uint32_t arow[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) arow[m] = 16 * m + li < g.M ? (uint32_t)((16 * m + li) * g.lda) * 4u : kOutOfRange;
+    const uint32_t brow = j0 + li < g.N ? (uint32_t)((j0 + li) * g.ldb) * 4u : kOutOfRange;
+    f32x4 xa[CH][MB], xb[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+        const int k = 16 * (c0 + u) + 4 * q;
+        const bool in = c0 + u < c1 && k < g.K;
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+            xa[u][m] = load_f32x4(ra, in && arow[m] != kOutOfRange ? arow[m] + 4u * k : kOutOfRange);
+        xb[u] = load_f32x4(rb, in && brow != kOutOfRange ? brow + 4u * k : kOutOfRange);
+    }
+    f32x4 acc[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+        if (c0 + u >= c1) break;  // wave-uniform
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // element copies first: bit_cast of an ext-vector element is miscompiled
+            const float b = xb[u][e];
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                const float a = xa[u][m][e];
+                acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[m], 0, 0, 0);
+            }
+        }
+    }
+    // lane's acc[m][r] is row 16 m + 4 q + r, column j0 + li
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float v = acc[m][r];
+            part[wave][m][r][lane] = v;
+        }
+    __syncthreads();
+    const int t = threadIdx.x, row = t >> 4, jj = t & 15;
+    if (row >= 16 * MB) return;
+    const int m = row >> 4, rr = row & 15, src = 16 * (rr >> 2) + jj;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSkinnyWaves; ++w) s += part[w][m][rr & 3][src];
+    if (row < g.M && j0 + jj < g.N) g.out[(int64_t)row * g.N + j0 + jj] = gemm_finish(g, row, j0 + jj, s);
+}
+
 typedef Tile<128, 128, 32, 2, 2> GemmT128;
 typedef Tile<64, 64, 32, 2, 2> GemmT64;
 
@@ -834,6 +910,15 @@ static void gemm_run(const GemmProblem& p, const char* name) {
         set_work(2.0 * p.M * (double)p.N * p.K, 4.0 * ((double)p.M * p.K + (double)p.N * p.K + (double)p.M * p.N));
         if (vec) launch("dot_rows_v4", dot_k<true>, grid, dim3(256), 0, g);
         else launch("dot_rows_s1", dot_k<false>, grid, dim3(256), 0, g);
+        return;
+    }
+    if (p.batches == 1 && p.a_kc && p.b_kc && p.M <= kSkinnyRows && p.K <= kSkinnyMaxK && p.K % 4 == 0 &&
+        aligned16(p.A) && aligned16(p.B) && p.lda % 4 == 0 && p.ldb % 4 == 0 &&
+        (int64_t)p.M * p.lda * 4 < ((int64_t)1 << 31) && (int64_t)p.N * p.ldb * 4 < ((int64_t)1 << 31)) {
+        const dim3 grid((unsigned)ceil_div(p.N, 16)), block(64 * kSkinnyWaves);
+        set_work(2.0 * p.M * (double)p.N * p.K, 0.0);
+        if (p.M <= 16) launch("gemm_skinny_nt_16", gemm_skinny_nt_k<1>, grid, block, 0, g);
+        else launch("gemm_skinny_nt_32", gemm_skinny_nt_k<2>, grid, block, 0, g);
         return;
     }
     // MFMA tiles address each operand tile with 32-bit byte offsets from the

@@ -347,6 +347,13 @@ GEMM_SHAPES = [
     (200, 128, 68, 0, 1, True),
     (64, 96, 40, 1, 1, False),
     (1536, 1536, 132, 0, 1, True),  # 128x128 direct-to-LDS tiles, K tail of 4
+    # at most 32 rows, both operands k-contiguous: one launch, 16 columns per
+    # workgroup, K over 8 waves - one row block, N not a multiple of 16, a K
+    # tail inside a 16-wide chunk, fewer chunks than waves, K = 1024
+    (8, 1000, 512, 0, 1, True),     # ResNet FC at batch 8
+    (17, 333, 1020, 0, 1, False),
+    (32, 50, 36, 0, 1, True),
+    (3, 40, 1024, 0, 1, True),
 ]
 
 
