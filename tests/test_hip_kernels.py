@@ -51,6 +51,9 @@ CONV_SHAPES = [
     (4, 256, 14, 512, 1, 2, 0),   # 1x1 stride 2
     (3, 5, 11, 7, 3, 1, 1),       # odd sizes everywhere
     (1, 33, 9, 130, 5, 2, 2),     # generic kernel size, K tail, Co tail
+    # register-staged 128x128 tiles (Ci % 32 != 0, K = 540): stream-K
+    # partials in register order, a Co tail and images straddling tiles
+    (2, 60, 24, 136, 3, 1, 1),
 ]
 
 
@@ -155,6 +158,7 @@ PACKED_SHAPES = [
     (2, 256, 14, 512, 3, 2, 1),   # stride 2, many M tiles
     (4, 512, 7, 512, 3, 1, 1),    # K = 4608: many partials per tile
     (3, 32, 13, 96, 3, 2, 1),     # odd image, Co and pixel tails
+    (3, 64, 19, 198, 3, 1, 1),    # 128x128 tiles: Co % 4 != 0, 1083 pixels of 361-pixel images
     (2, 32, 9, 40, 3, 1, 1),      # Co < tile
     (2, 64, 10, 64, 3, 1, 0),     # no padding
     (4, 64, 14, 128, 1, 1, 0),    # 1x1
