@@ -34,7 +34,7 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 BUNDLE_MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 
-PARTIAL_STORE = re.compile(r"^\s*buffer_store_dword(x2)?\s.*\bsc1\b")
+PARTIAL_STORE = re.compile(r"^\s*buffer_store_dword(x2|x4)?\s.*\bsc1\b")
 PARTIAL_LOAD = re.compile(r"^\s*buffer_load_dword(x2|x4)?\s.*\bsc1\b")
 COUNTER_RMW = re.compile(r"^\s*(global|buffer|flat)_atomic_add\w*\s.*\bsc0\b")  # sc0: returns the old value
 WAIT_VM0 = re.compile(r"^\s*s_waitcnt\s.*\bvmcnt\(0\)")
@@ -44,32 +44,44 @@ L2_MAINT = re.compile(r"^\s*buffer_(wbl2|inv)\b")
 
 def check_finish_order(lines: list[str]) -> None:
     """Assert the protocol's order on one kernel's instructions, in the
-    order the assembler lays them out (the finish code is straight-line
-    between the last partial store and the first partial load). A kernel
-    that shares two pieces of work (finish_arrive_pair) has two counter
-    atomics, both between the same two barriers."""
+    order the assembler lays them out. Every hand-off - a counter atomic, or
+    the two atomics of finish_arrive_pair between the same two barriers -
+    needs its own release and acquire: the device-scope stores before it
+    waited for (vmcnt(0)) before a barrier that precedes it, its return
+    waited for before the next barrier, and no partial load between it and
+    that barrier. A two-level finish chains two hand-offs (a group's sum is
+    stored, then handed on)."""
     rmw = [i for i, l in enumerate(lines) if COUNTER_RMW.match(l)]
-    assert 1 <= len(rmw) <= 2, f"expected one or two counter atomics, found {len(rmw)}"
-    a, a_last = rmw[0], rmw[-1]
-    assert not any(BARRIER.match(lines[i]) for i in range(a, a_last)), "the counter atomics straddle a barrier"
+    assert rmw, "no counter atomic"
+    barriers = [i for i, l in enumerate(lines) if BARRIER.match(l)]
+    handoffs: list[list[int]] = []
+    for i in rmw:
+        if handoffs and not any(handoffs[-1][-1] < b < i for b in barriers):
+            handoffs[-1].append(i)
+        else:
+            handoffs.append([i])
+    assert all(len(h) <= 2 for h in handoffs), "more than two counter atomics between the same barriers"
     stores = [i for i, l in enumerate(lines) if PARTIAL_STORE.match(l)]
-    assert stores and stores[-1] < a, "no device-scope partial store before the counter atomic"
-    # release: the stores' completion wait, then a barrier, before the atomic
-    b1 = max(i for i in range(stores[-1], a) if BARRIER.match(lines[i])) if any(
-        BARRIER.match(lines[i]) for i in range(stores[-1], a)) else None
-    assert b1 is not None, "no barrier between the partial stores and the counter atomic"
-    assert any(WAIT_VM0.match(lines[i]) for i in range(stores[-1], b1)), \
-        "the partial stores are not waited for (vmcnt(0)) before the barrier"
-    # acquire: the atomics have returned before the barrier that releases the readers
-    b2 = next((i for i in range(a_last, len(lines)) if BARRIER.match(lines[i])), None)
-    assert b2 is not None, "no barrier after the counter atomic"
-    assert any(WAIT_VM0.match(lines[i]) for i in range(a_last, b2)), \
-        "the counter atomic's return is not waited for before the barrier"
     loads = [i for i, l in enumerate(lines) if PARTIAL_LOAD.match(l)]
     assert loads, "no device-scope partial loads"
-    early = [lines[i].strip() for i in loads if a < i < b2]
-    assert not early, f"partial loads between the atomic and the barrier: {early[:2]}"
-    assert all(i > b2 or i < stores[0] for i in loads), "a partial load sits inside the hand-off"
+    for h in handoffs:
+        a, a_last = h[0], h[-1]
+        before = [i for i in stores if i < a]
+        assert before, "no device-scope partial store before the counter atomic"
+        # release: the stores' completion wait, then a barrier, before the atomic
+        b1 = max((b for b in barriers if before[-1] < b < a), default=None)
+        assert b1 is not None, "no barrier between the partial stores and the counter atomic"
+        assert any(WAIT_VM0.match(lines[i]) for i in range(before[-1], b1)), \
+            "the partial stores are not waited for (vmcnt(0)) before the barrier"
+        # acquire: the atomics have returned before the barrier that releases the readers
+        b2 = next((b for b in barriers if b > a_last), None)
+        assert b2 is not None, "no barrier after the counter atomic"
+        assert any(WAIT_VM0.match(lines[i]) for i in range(a_last, b2)), \
+            "the counter atomic's return is not waited for before the barrier"
+        # (the window between the two barriers: the code of another path of
+        # the kernel may be laid out between a store and this hand-off)
+        early = [lines[i].strip() for i in loads if b1 < i < b2]
+        assert not early, f"partial loads inside the hand-off: {early[:2]}"
     # the point of the protocol: no whole-L2 write-back or invalidate
     assert not any(L2_MAINT.match(l) for l in lines), "buffer_wbl2 / buffer_inv in the kernel"
 
@@ -118,6 +130,18 @@ def test_check_rejects_a_missing_wait():
         check_finish_order(hoisted)
     with pytest.raises(AssertionError):
         check_finish_order(good[:4] + ["buffer_inv sc1"] + good[4:])
+    # two chained hand-offs (a group's sum stored, then handed on): each needs
+    # its own release and acquire
+    second = ["buffer_store_dwordx4 v[0:3], v5, s[0:3], 0 offen sc1", "s_waitcnt vmcnt(0)", "s_barrier",
+              "global_atomic_add v1, v2, v3, s[4:5] sc0", "s_waitcnt vmcnt(0)", "s_barrier",
+              "buffer_load_dwordx4 v[0:3], v6, s[0:3], 0 offen sc1"]
+    check_finish_order(good + second)
+    with pytest.raises(AssertionError):
+        check_finish_order(good + second[:1] + second[2:])  # the group sum's store wait dropped
+    with pytest.raises(AssertionError):
+        check_finish_order(good + second[:4] + second[5:])  # the second atomic's wait dropped
+    with pytest.raises(AssertionError):
+        check_finish_order(good + second[:4] + [second[6]] + second[4:6])  # a load inside the second hand-off
 
 
 def _library_kernels(lib: Path, tmp_path: Path) -> dict[str, list[str]]:
