@@ -417,6 +417,31 @@ def run_suite() -> int:
              _op_roofline(runtime, lambda op=op: getattr(lib, op)(tr, tro, 2, 1)))
     keep.clear()
 
+    # the element-wise chain relu(x + y) * x, clip(-6, 6), sigmoid, + t as one
+    # nnc_hip_fused_eltwise pass (three inputs read, one output written)
+    tx, ty, tt = (dev(rng.standard_normal(shape).astype(np.float32)) for _ in range(3))
+    to = dev(np.zeros(shape, np.float32))
+    ins3 = (abi.TP * 3)(tx, ty, tt)
+    prog5 = (ctypes.c_int * 15)(4, 0, 1, 2, -1, 0, 9, -1, -1, 7, -1, -1, 0, -1, 2)
+    consts5 = (ctypes.c_float * 10)(0, 0, 0, 0, -6, 6, 0, 0, 0, 0)
+    emit("bandwidth", "nnc_hip_fused_eltwise: relu(x+y)*x, clip, sigmoid, +t [32,256,56,56]",
+         _op_roofline(runtime, lambda: lib.nnc_hip_fused_eltwise(ctypes.cast(ins3, abi.TPP), 3, prog5, 5, consts5, to)))
+    keep.clear()
+    # the whole chain program (config's element-wise chain, softmax, layernorm
+    # and reductions) at O3 on this target, and the reference's own O3 call
+    # sequence on this library, one hipGraph per step
+    for label, target in (("mi355x O3 (fused element-wise chains, no Concat -> Split)", True),
+                          ("reference O3 call sequence", False)):
+        prog = build_program(zoo.bandwidth_chain(seed=1), opt_level=3, target_passes=target)
+        ex = Executor(prog, device=True)
+        for k in ("x", "y", "s", "l", "r"):
+            ex.set_input(k, rng.standard_normal(prog.graph.tensors[k].shape).astype(np.float32))
+        steps = 20
+        dt = timed_steps(ex, steps, 5, True, runtime)
+        emit("bandwidth", f"bandwidth chain program, {label}, hipGraph", {"kernels": kernel_table(ex, runtime, 3)},
+             ms_per_step=round(dt / steps * 1e3, 4), calls=len(prog.calls))
+        ex.close()
+
     prog = build_program(zoo.transformer_encoder(seed=1), opt_level=3)
     ex = Executor(prog, device=True)
     ex.set_input("input", (rng.standard_normal((8, 128, 256)) * 0.02).astype(np.float32))

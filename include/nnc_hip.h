@@ -230,6 +230,26 @@ void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh,
  * counterpart in the reference ABI. */
 void nnc_hip_gap_gemm_nt(Tensor* in, Tensor* w, Tensor* c, Tensor* out, float alpha, float beta);
 
+/* nnc_hip_fused_eltwise: a chain of element-wise ops evaluated in registers
+ * in one pass over HBM, no intermediate tensor written. ins: n_in (1..4)
+ * tensors of numel(out) elements each (no broadcast). prog: n_steps (1..8)
+ * steps of three ints {op, x, y} computing acc = op(x, y), an operand being
+ * -1 (acc, the previous step's value; not in step 0) or an input index; y is
+ * ignored by the unary ops. consts: two floats per step, Clip's lo and hi
+ * (may be NULL without Clip steps). out = acc after the last step; out may be
+ * one of the inputs. Ops (NNC_EW_*): ADD 0, SUB 1, MUL 2, DIV 3, ADD_RELU 4
+ * (s > 0 ? s : 0, as nnc_add_relu), ADD_SIGMOID 5, RELU 6 (as nnc_relu),
+ * SIGMOID 7, TANH 8, CLIP 9. Every step is the corresponding nnc_* op's
+ * arithmetic, so the result equals the ops run one call after another
+ * through temporaries (bit for bit on this library). NNC_HIP_EINVAL for a
+ * malformed program or a short input. Emitted by the mi355x target's O3
+ * pass for element-wise nodes each feeding only the next. No counterpart in
+ * the reference ABI (which runs each op as its own call, runtime/x86/
+ * ops.c:82-258, 2253-2262, 3233-3346). */
+enum { NNC_EW_ADD = 0, NNC_EW_SUB, NNC_EW_MUL, NNC_EW_DIV, NNC_EW_ADD_RELU, NNC_EW_ADD_SIGMOID, NNC_EW_RELU,
+       NNC_EW_SIGMOID, NNC_EW_TANH, NNC_EW_CLIP, NNC_EW_OPS };
+void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out);
+
 /* nnc_hip_conv_packed_noalloc: nnc_hip_conv_packed for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference ABI.

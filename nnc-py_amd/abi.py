@@ -47,6 +47,8 @@ class Tensor(ctypes.Structure):
 TP = ctypes.POINTER(Tensor)
 TPP = ctypes.POINTER(TP)
 I64P = ctypes.POINTER(ctypes.c_int64)
+I32P = ctypes.POINTER(ctypes.c_int)
+F32P = ctypes.POINTER(ctypes.c_float)
 c_int = ctypes.c_int
 c_float = ctypes.c_float
 
@@ -123,7 +125,12 @@ TARGET_SIGNATURES = {
     "nnc_hip_conv_packed_noalloc": [TP, TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
     "nnc_hip_gap_gemm_nt": [TP, TP, TP, TP, c_float, c_float],
     "nnc_hip_conv_maxpool": [TP, TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int],
+    "nnc_hip_fused_eltwise": [TPP, c_int, I32P, c_int, F32P, TP],
 }
+
+# nnc_hip_fused_eltwise's op codes (include/nnc_hip.h NNC_EW_*)
+EW_OPS = {"ADD": 0, "SUB": 1, "MUL": 2, "DIV": 3, "ADD_RELU": 4, "ADD_SIGMOID": 5, "RELU": 6, "SIGMOID": 7,
+          "TANH": 8, "CLIP": 9}
 
 
 def bind(lib: ctypes.CDLL, names=None) -> ctypes.CDLL:

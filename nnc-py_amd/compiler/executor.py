@@ -24,7 +24,8 @@ from .ir import Graph, Node
 from .lower import Call, lower
 from .passes import (SPILL_OPS, Branch, MemoryPlan, branch_calls, check_plan, eliminate_dead_code,
                      eliminate_identity, find_branches, fit_memory, fuse_matmul_bias, fuse_patterns, fuse_projection,
-                     fuse_residual, pack_conv_weights, plan_memory, prepack_lowering, stream_tiles)
+                     fuse_residual, pack_conv_weights, plan_memory, prepack_lowering, stream_tiles,
+                     eliminate_concat_split, fuse_eltwise_chains)
 
 
 @dataclass
@@ -48,6 +49,9 @@ PROJECTION_FUSION = True
 # at O3 (mi355x target): GlobalAveragePool -> Flatten -> Gemm as
 # nnc_hip_gap_gemm_nt.
 STREAM_TILES = True
+# O3: element-wise chains in one pass (nnc_hip_fused_eltwise) and Concat ->
+# Split round trips removed
+ELTWISE_FUSION = True
 # independent side branches (ResNet's downsample convolutions) on the second
 # library stream at O3 (mi355x target), while the main branch's convolutions
 # total at most BRANCH_MAX_FLOPS: two kernels overlap only while neither fills
@@ -87,6 +91,9 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
         prepack_lowering(graph)
         if target_passes and STREAM_TILES:
             stream_tiles(graph)
+        if target_passes and ELTWISE_FUSION:
+            eliminate_concat_split(graph)
+            fuse_eltwise_chains(graph)
     order = graph.topological_sort()
     branches = find_branches(graph, order, BRANCH_MAX_FLOPS) if use_branches else []
     groups = [[b.side] + b.main for b in branches]
@@ -214,6 +221,14 @@ class Executor:
                 arr = (ctypes.c_int64 * max(1, len(spec[1])))(*[int(v) for v in spec[1]])
                 self._keep.append(arr)
                 out.append(ctypes.cast(arr, abi.I64P))
+            elif kind == "i32":
+                arr = (ctypes.c_int * max(1, len(spec[1])))(*[int(v) for v in spec[1]])
+                self._keep.append(arr)
+                out.append(ctypes.cast(arr, abi.I32P))
+            elif kind == "f32":
+                arr = (ctypes.c_float * max(1, len(spec[1])))(*[float(v) for v in spec[1]])
+                self._keep.append(arr)
+                out.append(ctypes.cast(arr, abi.F32P))
             else:
                 raise ValueError(f"unknown argument kind {kind!r}")
         return tuple(out)

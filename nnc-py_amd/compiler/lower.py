@@ -14,6 +14,8 @@ Argument specs:
   ("tl", [names])          Tensor** array
   ("i64", [values])        const int64_t* array
   ("i64null",)             NULL int64_t*
+  ("i32", [values])        const int* array
+  ("f32", [values])        const float* array
 
 DIVERGES from the reference for ReduceMean/ReduceSum over several axes: the
 reference passes axes[0] only (c_emitter.py:593-607) and then writes outside
@@ -92,6 +94,18 @@ def _scalar_const(g: Graph, name: str | None):
     return float(np.asarray(g.tensors[name].data).reshape(-1)[0])
 
 
+def clip_bounds(g: Graph, node: Node) -> tuple[float, float]:
+    """Clip's bounds as the reference code generator takes them
+    (c_emitter.py:657-698): attributes, else constant second / third inputs,
+    else +-3.402823e38."""
+    ins = node.inputs
+    lo = node.attrs.get("min", _scalar_const(g, ins[1] if len(ins) > 1 else None))
+    hi = node.attrs.get("max", _scalar_const(g, ins[2] if len(ins) > 2 else None))
+    lo = -F32_MAX if lo is None or lo == -np.inf else float(lo)
+    hi = F32_MAX if hi is None or hi == np.inf else float(hi)
+    return lo, hi
+
+
 def _reduce_call(g: Graph, node: Node, entry: str) -> Call:
     x, y = node.inputs[0], node.outputs[0]
     shape = list(g.tensors[x].shape)
@@ -168,6 +182,12 @@ def lower_node(g: Graph, node: Node) -> Call:
         return Call("nnc_hip_gap_gemm_nt", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0]),
                                             ("f", float(node.attrs.get("alpha", 1.0))),
                                             ("f", float(node.attrs.get("beta", 1.0)))], node.name)
+    if op == "FusedEltwise":  # an element-wise chain in one pass (include/nnc_hip.h)
+        steps = node.attrs["steps"]
+        prog = [v for st in steps for v in (st[0], st[1], st[2])]
+        consts = [v for st in steps for v in (st[3], st[4])]
+        return Call("nnc_hip_fused_eltwise", [("tl", list(ins)), ("i", len(ins)), ("i32", prog), ("i", len(steps)),
+                                              ("f32", consts), _t(outs[0])], node.name)
     if op == "FusedMatMulRelu":
         return Call("nnc_matmul_relu", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0])], node.name)
     if op == "MaxPool":
@@ -207,10 +227,7 @@ def lower_node(g: Graph, node: Node) -> Call:
         return Call("nnc_split", [_t(ins[0]), ("tl", list(outs)), ("i", len(outs)),
                                   ("i", int(node.attrs.get("axis", 0)))], node.name)
     if op == "Clip":
-        lo = node.attrs.get("min", _scalar_const(g, ins[1] if len(ins) > 1 else None))
-        hi = node.attrs.get("max", _scalar_const(g, ins[2] if len(ins) > 2 else None))
-        lo = -F32_MAX if lo is None or lo == -np.inf else float(lo)
-        hi = F32_MAX if hi is None or hi == np.inf else float(hi)
+        lo, hi = clip_bounds(g, node)
         return Call("nnc_clip", [_t(ins[0]), _t(outs[0]), ("f", lo), ("f", hi)], node.name)
     if op == "Pow":  # always x*x in the reference runtime (ops.c:2449-2461)
         return Call("nnc_pow", [_t(ins[0]), _t(outs[0])], node.name)

@@ -33,7 +33,7 @@ ALIGN = 256  # arena offsets; 16-byte vector loads need 16, 256 keeps rows cache
 # ops that may write over a same-sized input that dies at the node
 # (cost_aware_allocator.py:39-48)
 INPLACE_OPS = {"Relu", "Sigmoid", "Tanh", "Add", "Sub", "Mul", "Div", "Clip",
-               "FusedAddRelu", "FusedAddSigmoid", "FusedConvAddRelu"}
+               "FusedAddRelu", "FusedAddSigmoid", "FusedConvAddRelu", "FusedEltwise"}
 # inputs an in-place output may take over (default: any); the fused conv
 # reads its image input at neighbouring pixels, so only the residual
 INPLACE_INPUTS = {"FusedConvAddRelu": (3,)}
@@ -485,6 +485,120 @@ def stream_tiles(g: Graph, lds_budget: int = LDS_BUDGET) -> int:
         g.tensors.pop(flat_out, None)
         fused += 1
     return fused
+
+
+# ---------------------------------------------------------------------------
+# element-wise chains and Concat -> Split round trips (O3, mi355x target)
+# ---------------------------------------------------------------------------
+# Element-wise ops the chain kernel (nnc_hip_fused_eltwise) takes: step op
+# (include/nnc_hip.h NNC_EW_*) and number of data operands.
+EW_STEPS = {"Add": ("ADD", 2), "Sub": ("SUB", 2), "Mul": ("MUL", 2), "Div": ("DIV", 2),
+            "FusedAddRelu": ("ADD_RELU", 2), "FusedAddSigmoid": ("ADD_SIGMOID", 2),
+            "Relu": ("RELU", 1), "Sigmoid": ("SIGMOID", 1), "Tanh": ("TANH", 1), "Clip": ("CLIP", 1)}
+EW_MAX_INPUTS, EW_MAX_STEPS = 4, 8
+
+
+def _ew_node_ok(g: Graph, node: Node) -> bool:
+    """A float32 element-wise node whose data operands all have its output's
+    element count (the chain kernel does not broadcast)."""
+    if node.op_type not in EW_STEPS or len(node.outputs) != 1:
+        return False
+    arity = EW_STEPS[node.op_type][1]
+    out = g.tensors[node.outputs[0]]
+    if out.dtype != "float32" or len(node.inputs) < arity:
+        return False
+    return all(node.inputs[k] and g.tensors[node.inputs[k]].dtype == "float32"
+               and g.tensors[node.inputs[k]].numel == out.numel for k in range(arity))
+
+
+def fuse_eltwise_chains(g: Graph) -> int:
+    """Element-wise nodes each feeding only the next (an output with one
+    reader, not a graph output) become one FusedEltwise node, lowered to
+    nnc_hip_fused_eltwise: the chain runs in registers, its intermediates
+    never reach HBM. A chain takes at most EW_MAX_STEPS nodes and
+    EW_MAX_INPUTS distinct external inputs; its nodes keep their order and
+    arithmetic (steps: op, x, y, lo, hi with operand -1 the running value),
+    so the values are those of the op-by-op calls."""
+    from .lower import clip_bounds
+    from ..abi import EW_OPS
+    fused = 0
+    done: set[str] = set()
+    for head in g.topological_sort():
+        if head.name in done or not _ew_node_ok(g, head):
+            continue
+        chain, inputs, steps, prev = [], [], [], None
+        node = head
+        while True:
+            op, arity = EW_STEPS[node.op_type]
+            new_in = [t for t in node.inputs[:arity] if t != prev and t not in inputs]
+            if len(chain) == EW_MAX_STEPS or len(inputs) + len(set(new_in)) > EW_MAX_INPUTS:
+                break
+            for t in new_in:
+                if t not in inputs:
+                    inputs.append(t)
+            ops = [-1 if t == prev else inputs.index(t) for t in node.inputs[:arity]]
+            lo, hi = clip_bounds(g, node) if node.op_type == "Clip" else (0.0, 0.0)
+            steps.append((EW_OPS[op], ops[0], ops[1] if arity == 2 else ops[0], lo, hi))
+            chain.append(node)
+            prev = node.outputs[0]
+            users = g.consumers(prev)
+            if prev in g.outputs or len(users) != 1 or not _ew_node_ok(g, users[0]):
+                break
+            nxt = users[0]
+            if nxt.name in done or prev not in nxt.inputs[:EW_STEPS[nxt.op_type][1]]:
+                break
+            node = nxt
+        if len(chain) < 2:
+            continue
+        last = chain[-1]
+        fusedn = Node(name=head.name, op_type="FusedEltwise", inputs=list(inputs), outputs=list(last.outputs),
+                      attrs={"steps": [list(s) for s in steps]})
+        fusedn.metadata["fused_from"] = [n.name for n in chain]
+        inter = [n.outputs[0] for n in chain[:-1]]
+        fusedn.metadata["tile_stream"] = {"intermediates": inter,
+                                          "hbm_bytes_saved": 2 * sum(g.tensors[t].nbytes for t in inter)}
+        # (in place of the last node: every external input exists by then)
+        at = g.nodes.index(last)
+        g.nodes[at] = fusedn
+        for n in chain[:-1]:
+            g.nodes.remove(n)
+        done.update(n.name for n in chain)
+        for t in inter:
+            g.tensors.pop(t, None)
+        fused += 1
+    return fused
+
+
+def eliminate_concat_split(g: Graph) -> int:
+    """A Split whose input is a Concat along the same axis into the same
+    pieces (the Concat's output read by nothing else, neither result a graph
+    output) hands the Concat's inputs straight to the Split's readers: both
+    copies disappear and every value is unchanged."""
+    removed = 0
+    for split in list(g.nodes):
+        if split.op_type != "Split" or not split.inputs:
+            continue
+        cat = g.producer(split.inputs[0])
+        if cat is None or cat.op_type != "Concat" or cat.outputs[0] in g.outputs:
+            continue
+        if len(g.consumers(cat.outputs[0])) != 1 or any(o in g.outputs for o in split.outputs):
+            continue
+        nd = len(g.tensors[cat.outputs[0]].shape)
+        ax_c, ax_s = int(cat.attrs.get("axis", 0)) % nd, int(split.attrs.get("axis", 0)) % nd
+        if ax_c != ax_s or len(cat.inputs) != len(split.outputs):
+            continue
+        if any(list(g.tensors[a].shape) != list(g.tensors[b].shape) or g.tensors[a].dtype != g.tensors[b].dtype
+               for a, b in zip(cat.inputs, split.outputs)):
+            continue
+        rename = dict(zip(split.outputs, cat.inputs))
+        for c in g.nodes:
+            c.inputs = [rename.get(i, i) for i in c.inputs]
+        g.nodes.remove(split)
+        g.nodes.remove(cat)
+        for t in list(split.outputs) + [cat.outputs[0]]:
+            g.tensors.pop(t, None)
+        removed += 1
+    return removed
 
 
 # ---------------------------------------------------------------------------

@@ -668,6 +668,15 @@ void nnc_clip(Tensor* in, Tensor* out, float lo, float hi) {
     (void)lo, (void)hi;
     unary("nnc_clip", in, out);
 }
+// eltwise.hip nnc_hip_fused_eltwise: one streaming pass, each input read and
+// the output written once
+void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out) {
+    (void)prog, (void)n_steps, (void)consts;
+    if (!ins || !out || n_in < 1) return;
+    double bytes = nbytes(out);
+    for (int i = 0; i < n_in; ++i) bytes += nbytes(ins[i]);
+    stream_kernel("nnc_hip_fused_eltwise", "nnc_hip_fused_eltwise", bytes);
+}
 void nnc_sqrt(Tensor* in, Tensor* out) { unary("nnc_sqrt", in, out); }
 void nnc_pow(Tensor* in, Tensor* out) { unary("nnc_pow", in, out); }
 void nnc_exp(Tensor* in, Tensor* out) { unary("nnc_exp", in, out); }

@@ -236,6 +236,121 @@ static void unary_entry(const char* name, Tensor* in, Tensor* out, float lo = 0.
 }
 
 // ---------------------------------------------------------------------------
+// fused element-wise chains (nnc_hip_fused_eltwise): every step in registers,
+// the inputs read and the result written once. Each step calls the binop /
+// unop of the op's own kernel, so the values equal those of the op-by-op
+// calls. Operands are picked by selects over the loaded inputs (no indexing
+// of registers by a runtime value); the op of a step is uniform over the
+// grid, so its switch is a scalar branch.
+// ---------------------------------------------------------------------------
+static constexpr int kEwMaxIn = 4, kEwMaxSteps = 8;
+struct EwProg {
+    const float* in[kEwMaxIn];
+    float* out;
+    int n_in, n_steps;
+    int op[kEwMaxSteps], x[kEwMaxSteps], y[kEwMaxSteps];
+    float lo[kEwMaxSteps], hi[kEwMaxSteps];
+};
+
+__device__ __forceinline__ float ew_apply(int op, float x, float y, float lo, float hi) {
+    switch (op) {
+        case NNC_EW_ADD: return binop<kAdd>(x, y);
+        case NNC_EW_SUB: return binop<kSub>(x, y);
+        case NNC_EW_MUL: return binop<kMul>(x, y);
+        case NNC_EW_DIV: return binop<kDiv>(x, y);
+        case NNC_EW_ADD_RELU: return binop<kAddRelu>(x, y);
+        case NNC_EW_ADD_SIGMOID: return binop<kAddSigmoid>(x, y);
+        case NNC_EW_RELU: return unop<kRelu>(x, lo, hi);
+        case NNC_EW_SIGMOID: return unop<kSigmoid>(x, lo, hi);
+        case NNC_EW_TANH: return unop<kTanh>(x, lo, hi);
+        default: return unop<kClip>(x, lo, hi);
+    }
+}
+
+// operand slot s: an input 0..3, or kEwMaxIn the running value (selects
+// over scalars)
+__device__ __forceinline__ float ew_pick(int s, float acc, float a0, float a1, float a2, float a3) {
+    float r = a3;
+    r = s == 2 ? a2 : r;
+    r = s == 1 ? a1 : r;
+    r = s == 0 ? a0 : r;
+    return s >= kEwMaxIn ? acc : r;
+}
+
+// the chain on one element whose inputs are a0..a3
+__device__ __forceinline__ float ew_eval(const EwProg& p, float a0, float a1, float a2, float a3) {
+    float acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < kEwMaxSteps; ++s)
+        if (s < p.n_steps)
+            acc = ew_apply(p.op[s], ew_pick(p.x[s], acc, a0, a1, a2, a3), ew_pick(p.y[s], acc, a0, a1, a2, a3),
+                           p.lo[s], p.hi[s]);
+    return acc;
+}
+
+__device__ __forceinline__ float4 ew_load4(const EwProg& p, int i, uint32_t g) {
+    return i < p.n_in ? reinterpret_cast<const float4*>(p.in[i])[g] : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+template <int BOP>
+__device__ __forceinline__ float4 ew_bin4(float4 a, float4 b) {
+    return make_float4(binop<BOP>(a.x, b.x), binop<BOP>(a.y, b.y), binop<BOP>(a.z, b.z), binop<BOP>(a.w, b.w));
+}
+template <int UOP>
+__device__ __forceinline__ float4 ew_un4(float4 a, float lo, float hi) {
+    return make_float4(unop<UOP>(a.x, lo, hi), unop<UOP>(a.y, lo, hi), unop<UOP>(a.z, lo, hi), unop<UOP>(a.w, lo, hi));
+}
+
+// The program on one float4: inputs in slots 0..3 and the running value in
+// slot 4 of one register array, an operand read by its slot - a uniform
+// index, so one indexed register read per component (the slot of operand
+// -1 is 4, set on the host).
+__device__ __forceinline__ float4 ew_eval4(const EwProg& p, float4 v0, float4 v1, float4 v2, float4 v3) {
+    float r[20] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2.x, v2.y, v2.z, v2.w,
+                   v3.x, v3.y, v3.z, v3.w, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kEwMaxSteps; ++s) {
+        if (s >= p.n_steps) continue;
+        const int xs = 4 * p.x[s], ys = 4 * p.y[s];
+        const float4 a = make_float4(r[xs], r[xs + 1], r[xs + 2], r[xs + 3]);
+        const float4 b = make_float4(r[ys], r[ys + 1], r[ys + 2], r[ys + 3]);
+        float4 acc;
+        switch (p.op[s]) {  // one scalar branch per step, the op applied to all four
+            case NNC_EW_ADD: acc = ew_bin4<kAdd>(a, b); break;
+            case NNC_EW_SUB: acc = ew_bin4<kSub>(a, b); break;
+            case NNC_EW_MUL: acc = ew_bin4<kMul>(a, b); break;
+            case NNC_EW_DIV: acc = ew_bin4<kDiv>(a, b); break;
+            case NNC_EW_ADD_RELU: acc = ew_bin4<kAddRelu>(a, b); break;
+            case NNC_EW_ADD_SIGMOID: acc = ew_bin4<kAddSigmoid>(a, b); break;
+            case NNC_EW_RELU: acc = ew_un4<kRelu>(a, 0.f, 0.f); break;
+            case NNC_EW_SIGMOID: acc = ew_un4<kSigmoid>(a, 0.f, 0.f); break;
+            case NNC_EW_TANH: acc = ew_un4<kTanh>(a, 0.f, 0.f); break;
+            default: acc = ew_un4<kClip>(a, p.lo[s], p.hi[s]); break;
+        }
+        r[16] = acc.x, r[17] = acc.y, r[18] = acc.z, r[19] = acc.w;
+    }
+    return make_float4(r[16], r[17], r[18], r[19]);
+}
+
+template <bool NT>
+__global__ void __launch_bounds__(256) fused_eltwise_vec4_k(EwProg p, uint32_t n4) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t g = blockIdx.x * blockDim.x + threadIdx.x; g < n4; g += stride) {
+        const float4 v0 = ew_load4(p, 0, g), v1 = ew_load4(p, 1, g), v2 = ew_load4(p, 2, g), v3 = ew_load4(p, 3, g);
+        store_f4<NT>(p.out + 4 * (size_t)g, ew_eval4(p, v0, v1, v2, v3));
+    }
+}
+
+__global__ void __launch_bounds__(256) fused_eltwise_scalar_k(EwProg p, uint32_t begin, uint32_t n) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = begin + blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float a0 = p.in[0][i], a1 = p.n_in > 1 ? p.in[1][i] : 0.f;
+        const float a2 = p.n_in > 2 ? p.in[2][i] : 0.f, a3 = p.n_in > 3 ? p.in[3][i] : 0.f;
+        p.out[i] = ew_eval(p, a0, a1, a2, a3);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // uint8 logic, comparisons, casts, fills
 // ---------------------------------------------------------------------------
 __global__ void greater_k(const float* a, const float* b, uint8_t* out, uint32_t n, uint32_t an,
@@ -326,6 +441,58 @@ void nnc_log(Tensor* i, Tensor* o) { unary_entry<kLog>("nnc_log", i, o); }
 void nnc_abs(Tensor* i, Tensor* o) { unary_entry<kAbs>("nnc_abs", i, o); }
 void nnc_neg(Tensor* i, Tensor* o) { unary_entry<kNeg>("nnc_neg", i, o); }
 void nnc_clip(Tensor* i, Tensor* o, float lo, float hi) { unary_entry<kClip>("nnc_clip", i, o, lo, hi); }
+
+// No reference counterpart: a chain of element-wise ops in one pass (the
+// mi355x target's O3 fusion of element-wise nodes each feeding only the next).
+void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out) {
+    const char* name = "nnc_hip_fused_eltwise";
+    if (!ready(name)) return;
+    if (!ins || !prog || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL argument");
+    if (n_in < 1 || n_in > kEwMaxIn) return fail(NNC_HIP_EINVAL, name, "1 to %d inputs, got %d", kEwMaxIn, n_in);
+    if (n_steps < 1 || n_steps > kEwMaxSteps)
+        return fail(NNC_HIP_EINVAL, name, "1 to %d steps, got %d", kEwMaxSteps, n_steps);
+    const int64_t n = numel(out);
+    if (n <= 0) return;
+    if (n >= (int64_t)1 << 31) return fail(NNC_HIP_EUNSUPP, name, "more than 2^31 elements");
+    EwProg p{};
+    p.out = static_cast<float*>(out->data);
+    p.n_in = n_in;
+    p.n_steps = n_steps;
+    bool vec = aligned16(p.out);
+    for (int i = 0; i < n_in; ++i) {
+        if (!has_data(ins[i]) || numel(ins[i]) != n)
+            return fail(NNC_HIP_EINVAL, name, "input %d must have numel(out) = %lld elements", i, (long long)n);
+        p.in[i] = static_cast<const float*>(ins[i]->data);
+        vec = vec && aligned16(p.in[i]);
+    }
+    for (int s = 0; s < n_steps; ++s) {
+        const int op = prog[3 * s], x = prog[3 * s + 1], y = prog[3 * s + 2];
+        const bool binary = op <= NNC_EW_ADD_SIGMOID;
+        if (op < 0 || op >= NNC_EW_OPS) return fail(NNC_HIP_EINVAL, name, "step %d: unknown op %d", s, op);
+        if (x < -1 || x >= n_in || (binary && (y < -1 || y >= n_in)))
+            return fail(NNC_HIP_EINVAL, name, "step %d: operand out of range", s);
+        if (s == 0 && (x < 0 || (binary && y < 0)))
+            return fail(NNC_HIP_EINVAL, name, "step 0 reads the running value");
+        if (op == NNC_EW_CLIP && !consts) return fail(NNC_HIP_EINVAL, name, "step %d: Clip without bounds", s);
+        p.op[s] = op;
+        p.x[s] = x < 0 ? kEwMaxIn : x;  // (the running value's slot)
+        p.y[s] = binary ? (y < 0 ? kEwMaxIn : y) : p.x[s];
+        p.lo[s] = consts ? consts[2 * s] : 0.f;
+        p.hi[s] = consts ? consts[2 * s + 1] : 0.f;
+    }
+    set_work(0.0, 4.0 * (double)n * (n_in + 1));
+    uint32_t done = 0;
+    if (vec && n >= 4) {
+        const uint32_t n4 = (uint32_t)(n / 4);
+        if (4 * n >= kNtStoreBytes)
+            launch(name, fused_eltwise_vec4_k<true>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
+        else
+            launch(name, fused_eltwise_vec4_k<false>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
+        done = n4 * 4;
+    }
+    if (done < n)
+        launch(name, fused_eltwise_scalar_k, dim3(grid_for(n - done, 4)), dim3(256), 0, p, done, (uint32_t)n);
+}
 
 void nnc_greater(Tensor* a, Tensor* b, Tensor* out) {
     const char* name = "nnc_greater";

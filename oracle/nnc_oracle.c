@@ -163,6 +163,41 @@ void nnc_clip(Tensor* in, Tensor* out, float lo, float hi) {
 }
 
 /* ------------------------------------------------------------------------
+ * nnc_hip_fused_eltwise (include/nnc_hip.h): a chain of element-wise ops,
+ * target-only, no reference counterpart. Restated as the op-by-op calls it
+ * replaces: each step is this file's apply_binary / apply_unary / clip
+ * arithmetic (ops.c:82-258, 2253-2262, 3233-3346), applied element by
+ * element - with every tensor of numel(out) elements that equals running
+ * the steps one call after another through temporaries (every input of an
+ * element is read before its output is written, so out may alias an
+ * input). Pinned against that composition by tests/test_oracle.py.
+ * ---------------------------------------------------------------------- */
+void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out) {
+    static const int bin[] = {OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_ADD_RELU, OP_ADD_SIGMOID};
+    static const int un[] = {U_RELU, U_SIGMOID, U_TANH};
+    int64_t n = numel(out);
+    float* z = (float*)out->data;
+    for (int64_t i = 0; i < n; ++i) {
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < n_in && k < 4; ++k) v[k] = ((const float*)ins[k]->data)[i];
+        float acc = 0.0f;
+        for (int s = 0; s < n_steps; ++s) {
+            int op = prog[3 * s], xi = prog[3 * s + 1], yi = prog[3 * s + 2];
+            float x = xi < 0 ? acc : v[xi];
+            if (op <= NNC_EW_ADD_SIGMOID) {
+                float y = yi < 0 ? acc : v[yi];
+                acc = apply_binary(bin[op], x, y);
+            } else if (op <= NNC_EW_TANH) {
+                acc = apply_unary(un[op - NNC_EW_RELU], x);
+            } else {
+                acc = fminf(fmaxf(x, consts[2 * s]), consts[2 * s + 1]);
+            }
+        }
+        z[i] = acc;
+    }
+}
+
+/* ------------------------------------------------------------------------
  * Softmax (ops.c:260-310): per (outer, inner) column, max with strict '>'
  * from -inf, sequential float sum of expf(x - max), then a second expf.
  * ---------------------------------------------------------------------- */

@@ -11,6 +11,8 @@ A case is a dict:
                ("tl", [keys])      Tensor** array
                ("i64", [ints])     int64_t* array
                ("i64null",)        NULL int64_t*
+               ("i32", [ints])     int* array
+               ("f32", [floats])   float* array
     outputs  keys whose contents are compared after the call
     bar      "exact" (bit-for-bit, NaN == NaN) or "fp" (atol/rtol rule)
 
@@ -76,6 +78,14 @@ def build_call(case: dict, abi, mem):
             args.append(ctypes.cast(arr, abi.I64P))
         elif kind == "i64null":
             args.append(None)
+        elif kind == "i32":
+            arr = (ctypes.c_int * max(1, len(spec[1])))(*[int(v) for v in spec[1]])
+            keep.append(arr)
+            args.append(ctypes.cast(arr, abi.I32P))
+        elif kind == "f32":
+            arr = (ctypes.c_float * max(1, len(spec[1])))(*[float(v) for v in spec[1]])
+            keep.append(arr)
+            args.append(ctypes.cast(arr, abi.F32P))
         else:
             raise ValueError(f"unknown arg kind {kind!r}")
     return args, handles, (keep, tensors)

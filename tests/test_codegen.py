@@ -163,3 +163,29 @@ def test_generated_c_on_gpu_make_and_run(tmp_path, hip, oracle_lib, monkeypatch,
     want = ex.get("output").ravel()[:10]
     bad = caserun.fp_violations(got, want, 3e-3, 1.5e-2)
     assert bad.size == 0, f"generated model output {got} vs oracle {want}"
+
+
+def test_generated_c_with_fused_eltwise_runs_on_the_oracle(tmp_path, pkg, oracle_lib):
+    """An O3 program that is one element-wise chain: model.c hands the
+    chain's inputs, steps and Clip bounds to nnc_hip_fused_eltwise as static
+    arrays and computes what the executor computes."""
+    from nnc_py_amd.compiler import Executor, GraphBuilder, build_program
+
+    def chain():
+        b = GraphBuilder("chain")
+        x = b.input("input", (2, 3, 8, 8))
+        t = b.add(b.mul(b.tanh(x), x), x)
+        b.output(b.sigmoid(b.clip(t, -0.5, 0.75), out="output"))
+        return b.build()
+    prog = _compile(tmp_path, chain(), opt=3)
+    assert [c.op for c in prog.calls] == ["nnc_hip_fused_eltwise"]
+    src = (tmp_path / "model.c").read_text()
+    assert "static const int" in src and "static const float" in src and "nnc_hip_fused_eltwise(" in src
+    exe = _build_with_shim(tmp_path)
+    run = subprocess.run([str(exe), str(tmp_path / "constants.bin"), "1"], capture_output=True, text=True,
+                         timeout=60)
+    assert run.returncode == 0, run.stderr
+    ex = Executor(build_program(chain(), opt_level=3), device=False, lib=oracle_lib)
+    ex.set_input("input", (np.arange(2 * 3 * 8 * 8, dtype=np.float32) * np.float32(0.01)).reshape(2, 3, 8, 8))
+    ex.run()
+    np.testing.assert_allclose(_parse_outputs(run.stdout), ex.get("output").ravel()[:10], rtol=1e-5, atol=1e-5)

@@ -333,3 +333,86 @@ def test_conv_pool_tile_streaming_pass(pkg, oracle_lib):
         ex.run()
         outs.append(ex.get("output"))
     assert outs[0].tobytes() == outs[1].tobytes()
+
+
+_BW_SMALL = dict(batch=2, channels=8, hw=6, rows_softmax=4, len_softmax=16, rows_ln=4, len_ln=8, red_channels=4,
+                 red_hw=4)
+
+
+def test_eltwise_chains_of_the_bandwidth_chain(pkg, oracle_lib):
+    """O3 (mi355x target): the bandwidth chain's element-wise ops become two
+    FusedEltwise nodes - tanh(x - y), then relu(x + y) * x, clip(-6, 6),
+    sigmoid, plus that tanh - lowered to nnc_hip_fused_eltwise, and its
+    Concat -> Split round trip is gone. On the oracle every output has the
+    bits of the reference pipeline's O3 program."""
+    from nnc_py_amd.compiler import Executor, build_program, zoo
+    prog = build_program(zoo.bandwidth_chain(**_BW_SMALL), opt_level=3)
+    ops = [n.op_type for n in prog.order]
+    assert ops.count("FusedEltwise") == 2
+    assert not {"Concat", "Split", "Mul", "Clip", "Sigmoid", "Tanh", "Sub", "FusedAddRelu", "Add"} & set(ops)
+    tanh_node, main = [n for n in prog.order if n.op_type == "FusedEltwise"]
+    assert tanh_node.inputs == ["x", "y"] and tanh_node.attrs["steps"] == [[1, 0, 1, 0.0, 0.0], [8, -1, -1, 0.0, 0.0]]
+    assert main.inputs == ["x", "y", tanh_node.outputs[0]] and main.outputs == ["chain"]
+    assert [s[:3] for s in main.attrs["steps"]] == [[4, 0, 1], [2, -1, 0], [9, -1, -1], [7, -1, -1], [0, -1, 2]]
+    assert main.attrs["steps"][2][3:] == [-6.0, 6.0]
+    assert main.metadata["fused_from"] == ["/Add", "/Mul", "/Clip", "/Sigmoid", "/Add_1"]
+    calls = [c.op for c in prog.calls]
+    assert calls.count("nnc_hip_fused_eltwise") == 2 and "nnc_concat" not in calls and "nnc_split" not in calls
+    ref = build_program(zoo.bandwidth_chain(**_BW_SMALL), opt_level=3, target_passes=False)
+    assert "nnc_hip_fused_eltwise" not in [c.op for c in ref.calls] and "nnc_concat" in [c.op for c in ref.calls]
+    rng = np.random.default_rng(8)
+    feeds = {n: (rng.standard_normal(prog.graph.tensors[n].shape) * 4).astype(np.float32)
+             for n in ("x", "y", "s", "l", "r")}
+    outs = []
+    for p in (prog, ref):
+        ex = Executor(p, device=False, lib=oracle_lib)
+        for k, v in feeds.items():
+            ex.set_input(k, v)
+        ex.run()
+        outs.append({o: ex.get(o) for o in ("chain", "softmax", "layernorm", "mean", "sum")})
+    for o in outs[0]:
+        assert outs[0][o].tobytes() == outs[1][o].tobytes(), o
+
+
+def test_eltwise_chain_limits(pkg):
+    """A chain holds at most EW_MAX_STEPS nodes and EW_MAX_INPUTS distinct
+    inputs, and ends at an output read twice, at a graph output and before
+    a broadcast operand; a lone node stays as it is."""
+    from nnc_py_amd.compiler import GraphBuilder, build_program, passes
+
+    def fused(build):
+        b = GraphBuilder("chains")
+        build(b)
+        return [(n.op_type, len(n.attrs.get("steps", []))) for n in build_program(b.build(), opt_level=3).order]
+
+    def long_chain(b):
+        t = b.input("x", (4, 8))
+        for i in range(passes.EW_MAX_STEPS + 2):
+            t = b.sigmoid(t, name=f"/s{i}")
+        b.output(t)
+    assert fused(long_chain) == [("FusedEltwise", passes.EW_MAX_STEPS), ("FusedEltwise", 2)]
+
+    def five_inputs(b):
+        xs = [b.input(f"x{i}", (4, 8)) for i in range(5)]
+        t = b.add(xs[0], xs[1])
+        for x in xs[2:]:
+            t = b.add(t, x)
+        b.output(t)
+    assert fused(five_inputs) == [("FusedEltwise", 3), ("Add", 0)]
+
+    def fan_out(b):
+        u = b.relu(b.input("x", (4, 8)))
+        b.output(b.sigmoid(u))
+        b.output(b.tanh(u))
+    assert sorted(fused(fan_out)) == [("Relu", 0), ("Sigmoid", 0), ("Tanh", 0)]
+
+    def output_inside(b):
+        u = b.relu(b.input("x", (4, 8)))
+        b.output(u)
+        b.output(b.sigmoid(u))
+    assert sorted(fused(output_inside)) == [("Relu", 0), ("Sigmoid", 0)]
+
+    def broadcast(b):
+        bias = b.input("bias", (8,))
+        b.output(b.sigmoid(b.tanh(b.add(b.input("x", (4, 8)), bias))))
+    assert fused(broadcast) == [("Add", 0), ("FusedEltwise", 2)]

@@ -634,3 +634,62 @@ def test_conv_maxpool_rejections(hip, dmem, abi):
         out = caserun.run_case(hip, case, abi, dmem)["out"]
         assert runtime.last_error()[0] == 4 and not out.any(), (h, w)
     runtime.clear_error()
+
+
+@pytest.mark.parametrize("n", [4099, 1 << 20])
+@pytest.mark.parametrize("prog", range(4))
+def test_fused_eltwise_matches_op_by_op(prog, n, hip, dmem, abi, oracle_lib):
+    """nnc_hip_fused_eltwise against the same program run as single GPU
+    calls through temporaries (the same device arithmetic: bit for bit),
+    and against the oracle within the fp bar (sigmoid and tanh use the
+    device's expf / tanhf); 4099 elements take the scalar tail; the output
+    written over an input gives the same bits."""
+    from ew_cases import EW_PROGRAMS, ew_arrays, ew_case, ew_compose
+    from nnc_py_amd import runtime
+    n_in, steps = EW_PROGRAMS[prog]
+    print(f"case fused_eltwise program {prog} n {n}", flush=True)
+    xs = ew_arrays(n_in, n, 60 + prog)
+    got = caserun.run_case(hip, ew_case(n_in, steps, xs), abi, dmem)["out"]
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    assert caserun.same_bits(got, ew_compose(hip, abi, steps, xs, dmem))
+    _check(got, caserun.run_case(oracle_lib, ew_case(n_in, steps, xs), abi)["out"], f"fused_eltwise {prog}")
+    over = caserun.run_case(hip, ew_case(n_in, steps, xs, out_key="i0"), abi, dmem)["i0"]
+    assert caserun.same_bits(over, got)
+
+
+def test_fused_eltwise_rejects_malformed_programs(hip, dmem, abi):
+    """Input and step counts out of range, an unknown op, step 0 reading the
+    running value, an operand past the inputs, an input shorter than the
+    output and Clip without bounds are refused before any launch
+    (NNC_HIP_EINVAL); the output is untouched."""
+    from ew_cases import ew_case
+    from nnc_py_amd import runtime
+    xs = [np.ones(64, np.float32), np.ones(64, np.float32)]
+
+    def edit(case, **kw):
+        args = list(case["args"])
+        for i, v in kw.items():
+            args[int(i[1:])] = v
+        case["args"] = args
+        return case
+
+    bad = [
+        ("no inputs", edit(ew_case(2, [("ADD", 0, 1)], xs), a1=("i", 0))),
+        ("five inputs", edit(ew_case(2, [("ADD", 0, 1)], xs), a1=("i", 5))),
+        ("no steps", edit(ew_case(2, [("ADD", 0, 1)], xs), a3=("i", 0))),
+        ("nine steps", edit(ew_case(2, [("ADD", 0, 1)] * 9, xs), a3=("i", 9))),
+        ("unknown op", edit(ew_case(2, [("ADD", 0, 1)], xs), a2=("i32", [10, 0, 1]))),
+        ("step 0 reads acc", ew_case(2, [("ADD", -1, 1)], xs)),
+        ("operand past the inputs", ew_case(2, [("ADD", 0, 2)], xs)),
+        ("clip without bounds", edit(ew_case(1, [("CLIP", 0, 0, -1.0, 1.0)], xs[:1]), a4=("null",))),
+    ]
+    short = ew_case(2, [("ADD", 0, 1)], [xs[0], np.ones(63, np.float32)])
+    short["tensors"]["out"] = np.zeros(64, np.float32)
+    bad.append(("short input", short))
+    for why, case in bad:
+        case["tensors"]["out"] = np.full_like(case["tensors"]["out"], 7.0)
+        runtime.clear_error()
+        out = caserun.run_case(hip, case, abi, dmem)["out"]
+        assert runtime.last_error()[0] == 1, (why, runtime.last_error())
+        assert (out == 7.0).all(), why
+    runtime.clear_error()

@@ -414,3 +414,32 @@ def test_oracle_gap_gemm_nt_composition(n, c, h, w, o, bias, oracle_lib, abi):
     if bias:
         ref = ref + -1.5 * tensors["c"].astype(np.float64)
     np.testing.assert_allclose(got, ref.astype(F32), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("prog", range(4))
+def test_oracle_fused_eltwise_composition(prog, oracle_lib, abi):
+    """nnc_hip_fused_eltwise: each program equals its steps run as single
+    nnc_* calls through temporaries (the oracle's own binary / unary / clip
+    entry points, pinned against the reference above), bit for bit, also
+    with the output written over an input."""
+    from ew_cases import EW_PROGRAMS, ew_arrays, ew_case, ew_compose
+    n_in, steps = EW_PROGRAMS[prog]
+    xs = ew_arrays(n_in, 1031, 50 + prog)
+    got = caserun.run_case(oracle_lib, ew_case(n_in, steps, xs), abi)["out"]
+    assert caserun.same_bits(got, ew_compose(oracle_lib, abi, steps, xs))
+    over = caserun.run_case(oracle_lib, ew_case(n_in, steps, xs, out_key="i0"), abi)["i0"]
+    assert caserun.same_bits(over, got)
+
+
+def test_oracle_fused_eltwise_closed_form(oracle_lib, abi):
+    """The bandwidth chain's longer chain against numpy: add, relu, multiply
+    and clip are exact in float32, sigmoid within a float32 ulp of float64."""
+    from ew_cases import EW_PROGRAMS, ew_arrays, ew_case
+    n_in, steps = EW_PROGRAMS[1]
+    x, y, t = ew_arrays(n_in, 4096, 7)
+    got = caserun.run_case(oracle_lib, ew_case(n_in, steps, [x, y, t]), abi)["out"]
+    s = x + y
+    r = np.where(s > 0, s, F32(0)) * x
+    c = np.minimum(np.maximum(r, F32(-6)), F32(6)).astype(np.float64)
+    ref = 1.0 / (1.0 + np.exp(-c)) + t.astype(np.float64)
+    np.testing.assert_allclose(got, ref.astype(F32), rtol=2e-7, atol=2e-7)

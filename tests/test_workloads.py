@@ -252,15 +252,16 @@ def _run_uncapped(host):
 @pytest.mark.gpu
 def test_bandwidth_chain_program_o3(hip, oracle_lib):
     """The whole chain (zoo.bandwidth_chain) at the workload's sizes,
-    compiled at O3 with fusion and run as one program on the GPU, against
-    the oracle running the same program on the host (its concat without the
-    reference's 64 MiB cap): every output within 1e-4 abs / 1e-3 rel; a captured hipGraph replayed twice gives the eager
-    result bit for bit."""
+    compiled at O3 with fusion (the element-wise ops as two
+    nnc_hip_fused_eltwise passes, the Concat -> Split round trip gone) and
+    run as one program on the GPU, against the oracle running the same
+    program on the host: every output within 1e-4 abs / 1e-3 rel; a
+    captured hipGraph replayed twice gives the eager result bit for bit."""
     from nnc_py_amd import runtime
     from nnc_py_amd.compiler import Executor, build_program, zoo
     prog = build_program(zoo.bandwidth_chain(), opt_level=3)
     ops = [c.op for c in prog.calls]
-    assert "nnc_add_relu" in ops and "nnc_relu" not in ops  # the Add+Relu pattern fused
+    assert ops.count("nnc_hip_fused_eltwise") == 2 and "nnc_concat" not in ops and "nnc_relu" not in ops
     feeds = _chain_inputs(prog.graph)
     print(f"chain O3: {len(ops)} calls, arena {prog.plan.total_bytes / 1e6:.0f} MB", flush=True)
     dev = Executor(prog, device=True)
