@@ -250,6 +250,17 @@ enum { NNC_EW_ADD = 0, NNC_EW_SUB, NNC_EW_MUL, NNC_EW_DIV, NNC_EW_ADD_RELU, NNC_
        NNC_EW_SIGMOID, NNC_EW_TANH, NNC_EW_CLIP, NNC_EW_OPS };
 void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out);
 
+/* nnc_hip_add_layernorm: out = layernorm(a + b) over dims [axis:] with
+ * scale and bias indexed by the axis dimension - a transformer's residual
+ * add and the normalisation after it in one pass, the sum never written.
+ * a and b have the same element count (no broadcast). The same bits as
+ * nnc_add(a, b, t) then nnc_layernorm(t, scale, bias, out, axis, eps) on this
+ * library (the sum is that of nnc_add, the normalisation that of
+ * nnc_layernorm). Emitted by the mi355x target's O3 pass for an Add whose
+ * only reader is a LayerNormalization. No counterpart in the reference ABI
+ * (runtime/x86/ops.c:82-119 then 2095-2171). */
+void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps);
+
 /* nnc_hip_conv_packed_noalloc: nnc_hip_conv_packed for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference ABI.

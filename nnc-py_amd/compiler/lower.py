@@ -182,6 +182,10 @@ def lower_node(g: Graph, node: Node) -> Call:
         return Call("nnc_hip_gap_gemm_nt", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _t(outs[0]),
                                             ("f", float(node.attrs.get("alpha", 1.0))),
                                             ("f", float(node.attrs.get("beta", 1.0)))], node.name)
+    if op == "FusedAddLayerNorm":  # residual add + layernorm in one pass (include/nnc_hip.h)
+        return Call("nnc_hip_add_layernorm", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _opt(node, 3), _t(outs[0]),
+                                              ("i", int(node.attrs.get("axis", -1))),
+                                              ("f", float(node.attrs.get("epsilon", 1e-5)))], node.name)
     if op == "FusedEltwise":  # an element-wise chain in one pass (include/nnc_hip.h)
         steps = node.attrs["steps"]
         prog = [v for st in steps for v in (st[0], st[1], st[2])]

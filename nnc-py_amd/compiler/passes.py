@@ -569,6 +569,64 @@ def fuse_eltwise_chains(g: Graph) -> int:
     return fused
 
 
+def fuse_add_layernorm(g: Graph) -> int:
+    """An Add of two same-size float32 tensors whose output only a
+    LayerNormalization reads (as its input, no graph output) becomes one
+    FusedAddLayerNorm node (inputs: a, b, scale, bias; the LayerNorm's
+    attrs), lowered to nnc_hip_add_layernorm: the sum stays in registers.
+    The same bits as the Add and the LayerNorm run one after the other."""
+    fused = 0
+    for add in list(g.nodes):
+        if add.op_type != "Add" or len(add.inputs) != 2 or add.outputs[0] in g.outputs:
+            continue
+        s = add.outputs[0]
+        t = g.tensors[s]
+        if t.dtype != "float32" or any(g.tensors[i].dtype != "float32" or g.tensors[i].numel != t.numel
+                                       for i in add.inputs):
+            continue
+        users = g.consumers(s)
+        if len(users) != 1 or users[0].op_type != "LayerNormalization" or users[0].inputs[0] != s:
+            continue
+        ln = users[0]
+        ln.op_type = "FusedAddLayerNorm"
+        ln.inputs = list(add.inputs) + list(ln.inputs[1:3]) + [""] * (3 - len(ln.inputs))
+        ln.metadata["fused_from"] = [add.name, ln.name]
+        ln.metadata["tile_stream"] = {"intermediate": s, "hbm_bytes_saved": 2 * t.nbytes}
+        g.nodes.remove(add)
+        g.tensors.pop(s, None)
+        fused += 1
+    return fused
+
+
+def compose_transposes(g: Graph) -> int:
+    """A Transpose whose input is another Transpose's output read by nothing
+    else (and no graph output) becomes one Transpose of the first's input
+    with the composed permutation: out.shape[i] = x.shape[p1[p2[i]]], the
+    same element moves, one copy instead of two."""
+    merged = 0
+    for t2 in list(g.nodes):
+        if t2.op_type != "Transpose" or not t2.inputs:
+            continue
+        t1 = g.producer(t2.inputs[0])
+        if t1 is None or t1.op_type != "Transpose" or t1.outputs[0] in g.outputs:
+            continue
+        if len(g.consumers(t1.outputs[0])) != 1:
+            continue
+        nd = len(g.tensors[t1.inputs[0]].shape)
+        p1 = list(t1.attrs.get("perm") or range(nd - 1, -1, -1))
+        p2 = list(t2.attrs.get("perm") or range(nd - 1, -1, -1))
+        if len(p1) != nd or len(p2) != nd:
+            continue
+        mid = t1.outputs[0]
+        t2.inputs = [t1.inputs[0]] + list(t2.inputs[1:])
+        t2.attrs = {**t2.attrs, "perm": [int(p1[p2[i]]) for i in range(nd)]}
+        t2.metadata["fused_from"] = [t1.name, t2.name]
+        g.nodes.remove(t1)
+        g.tensors.pop(mid, None)
+        merged += 1
+    return merged
+
+
 def eliminate_concat_split(g: Graph) -> int:
     """A Split whose input is a Concat along the same axis into the same
     pieces (the Concat's output read by nothing else, neither result a graph

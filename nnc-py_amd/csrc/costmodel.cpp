@@ -668,6 +668,14 @@ void nnc_clip(Tensor* in, Tensor* out, float lo, float hi) {
     (void)lo, (void)hi;
     unary("nnc_clip", in, out);
 }
+// norm.hip nnc_hip_add_layernorm: nnc_layernorm's row kernel reading a
+// second addend
+void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps) {
+    (void)axis, (void)eps;
+    if (!a || !b || !out) return;
+    stream_kernel("nnc_hip_add_layernorm", "nnc_hip_add_layernorm",
+                  nbytes(a) + nbytes(b) + nbytes(out) + nbytes(scale) + nbytes(bias));
+}
 // eltwise.hip nnc_hip_fused_eltwise: one streaming pass, each input read and
 // the output written once
 void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out) {

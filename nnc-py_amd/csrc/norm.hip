@@ -177,8 +177,22 @@ __global__ void __launch_bounds__(256) softmax_cols_k(const float* in, float* ou
 // ---------------------------------------------------------------------------
 // layernorm over a contiguous span of D*inner floats per outer row
 // ---------------------------------------------------------------------------
-template <int PER, bool INNER1>
-__global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, const float* g,
+// ADD: the row is in + in2 (same size, nnc_add's element-wise sum) - the
+// residual add of nnc_hip_add_layernorm, summed in registers
+template <int PER, bool ADD>
+__device__ __forceinline__ void load_ln_row(float4 (&v)[PER], const float* in, const float* in2, int64_t off, int s4,
+                                            int lane) {
+    load_row4<PER>(v, in + off, s4, lane, 0.f);
+    if (ADD) {
+        float4 w[PER];
+        load_row4<PER>(w, in2 + off, s4, lane, 0.f);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) v[q] = make_float4(v[q].x + w[q].x, v[q].y + w[q].y, v[q].z + w[q].z, v[q].w + w[q].w);
+    }
+}
+
+template <int PER, bool INNER1, bool ADD>
+__global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, const float* in2, const float* g,
                                                            const float* b, float* out, int64_t rows,
                                                            int span, int inner, float eps) {
     const int lane = threadIdx.x & 63;
@@ -187,12 +201,12 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
     int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     float4 v[PER];
-    load_row4<PER>(v, in + row * span, s4, lane, 0.f);
+    load_ln_row<PER, ADD>(v, in, in2, row * span, s4, lane);
     while (true) {
         const int64_t nrow = row + wstride;
         const bool more = nrow < rows;
         float4 nx[PER];
-        if (kPrefetch<PER> && more) load_row4<PER>(nx, in + nrow * span, s4, lane, 0.f);
+        if (kPrefetch<PER> && more) load_ln_row<PER, ADD>(nx, in, in2, nrow * span, s4, lane);
         float acc = 0.f;
 #pragma unroll
         for (int q = 0; q < PER; ++q) acc += (v[q].x + v[q].y) + (v[q].z + v[q].w);
@@ -241,7 +255,7 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
             }
         }
         if (!more) break;
-        if (!kPrefetch<PER>) load_row4<PER>(nx, in + nrow * span, s4, lane, 0.f);
+        if (!kPrefetch<PER>) load_ln_row<PER, ADD>(nx, in, in2, nrow * span, s4, lane);
 #pragma unroll
         for (int q = 0; q < PER; ++q) v[q] = nx[q];
         row = nrow;
@@ -389,15 +403,15 @@ static void softmax_v4(const float* x, float* y, int64_t rows, int dim, const ch
 }
 
 template <int PER>
-static void layernorm_v4(const float* x, const float* g, const float* b, float* y, int64_t rows,
+static void layernorm_v4(const float* x, const float* x2, const float* g, const float* b, float* y, int64_t rows,
                          int span, int inner, float eps, const char* name) {
     // inner == 1 with 16-byte aligned scale/bias: vector loads of those too
-    if (inner == 1 && (!g || aligned16(g)) && (!b || aligned16(b)))
-        launch(name, layernorm_rows_v4_k<PER, true>, dim3(row_grid(rows)), dim3(256), 0, x, g, b, y,
-               rows, span, inner, eps);
-    else
-        launch(name, layernorm_rows_v4_k<PER, false>, dim3(row_grid(rows)), dim3(256), 0, x, g, b, y,
-               rows, span, inner, eps);
+    const bool in1 = inner == 1 && (!g || aligned16(g)) && (!b || aligned16(b));
+    const dim3 grid(row_grid(rows)), block(256);
+    if (x2 && in1) launch(name, layernorm_rows_v4_k<PER, true, true>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
+    else if (x2) launch(name, layernorm_rows_v4_k<PER, false, true>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
+    else if (in1) launch(name, layernorm_rows_v4_k<PER, true, false>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
+    else launch(name, layernorm_rows_v4_k<PER, false, false>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
 }
 
 }  // namespace nnc
@@ -433,31 +447,52 @@ void nnc_softmax(Tensor* in, Tensor* out, int axis) {
            inner);
 }
 
-void nnc_layernorm(Tensor* in, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps) {
-    const char* name = "nnc_layernorm";
+// layernorm of in (+ in2, same size: the residual add of
+// nnc_hip_add_layernorm) over [axis:]
+static void layernorm_run(Tensor* in, Tensor* in2, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps,
+                          const char* name) {
     if (!ready(name)) return;
-    if (!has_data(in) || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
+    if (!has_data(in) || !has_data(out) || (in2 && !has_data(in2))) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
     int64_t outer, len, inner;
     if (!split_axis(name, in, axis, outer, len, inner)) return;
     const int64_t span = len * inner;
     if (numel(out) < numel(in)) return fail(NNC_HIP_EINVAL, name, "output smaller than input");
+    if (in2 && numel(in2) != numel(in)) return fail(NNC_HIP_EINVAL, name, "the two addends differ in size");
     if (outer * span == 0) return;
     const float* x = (const float*)in->data;
+    const float* x2 = in2 ? (const float*)in2->data : nullptr;
     const float* g = (scale && scale->data) ? (const float*)scale->data : nullptr;
     const float* b = (bias && bias->data) ? (const float*)bias->data : nullptr;
     if ((g && numel(scale) < len) || (b && numel(bias) < len))
         return fail(NNC_HIP_EINVAL, name, "scale/bias shorter than the axis");
     float* y = (float*)out->data;
-    set_work(0.0, 8.0 * (double)(outer * span) + (g ? 4.0 * len : 0.0) + (b ? 4.0 * len : 0.0));
-    const bool v4 = span % 4 == 0 && span < (1 << 30) && aligned16(x) && aligned16(y);
+    set_work(0.0, (x2 ? 12.0 : 8.0) * (double)(outer * span) + (g ? 4.0 * len : 0.0) + (b ? 4.0 * len : 0.0));
+    const bool v4 = span % 4 == 0 && span < (1 << 30) && aligned16(x) && aligned16(y) && (!x2 || aligned16(x2));
     const int sp = (int)span, inn = (int)inner;
-    if (v4 && span <= 256) return layernorm_v4<1>(x, g, b, y, outer, sp, inn, eps, name);
-    if (v4 && span <= 512) return layernorm_v4<2>(x, g, b, y, outer, sp, inn, eps, name);
-    if (v4 && span <= 1024) return layernorm_v4<4>(x, g, b, y, outer, sp, inn, eps, name);
-    if (v4 && span <= 2048) return layernorm_v4<8>(x, g, b, y, outer, sp, inn, eps, name);
-    if (v4 && span <= 4096) return layernorm_v4<16>(x, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 256) return layernorm_v4<1>(x, x2, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 512) return layernorm_v4<2>(x, x2, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 1024) return layernorm_v4<4>(x, x2, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 2048) return layernorm_v4<8>(x, x2, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span <= 4096) return layernorm_v4<16>(x, x2, g, b, y, outer, sp, inn, eps, name);
+    if (x2) {
+        // other spans: the sum into out, then the layernorm over it in place
+        // (each pass reads an element before writing it)
+        nnc_add(in, in2, out);
+        x = y;
+    }
     unsigned grid = (unsigned)(outer < 65536 ? outer : 65536);
     launch(name, layernorm_rows_k, dim3(grid), dim3(256), 0, x, g, b, y, outer, span, inner, eps);
+}
+
+void nnc_layernorm(Tensor* in, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps) {
+    layernorm_run(in, nullptr, scale, bias, out, axis, eps, "nnc_layernorm");
+}
+
+// No reference counterpart: the residual add and the layernorm after it in
+// one pass (the mi355x target's O3 fusion of Add -> LayerNormalization).
+void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps) {
+    if (!b) return fail(NNC_HIP_EINVAL, "nnc_hip_add_layernorm", "NULL addend");
+    layernorm_run(a, b, scale, bias, out, axis, eps, "nnc_hip_add_layernorm");
 }
 
 static void reduce_entry(const char* name, Tensor* in, Tensor* out, int axis, bool mean) {

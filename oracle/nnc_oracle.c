@@ -172,6 +172,21 @@ void nnc_clip(Tensor* in, Tensor* out, float lo, float hi) {
  * element is read before its output is written, so out may alias an
  * input). Pinned against that composition by tests/test_oracle.py.
  * ---------------------------------------------------------------------- */
+/* ------------------------------------------------------------------------
+ * nnc_hip_add_layernorm (include/nnc_hip.h): target-only, no reference
+ * counterpart. Restated as the two calls it replaces: nnc_add into a
+ * temporary (ops.c:82-119), then nnc_layernorm of it (ops.c:2095-2171).
+ * ---------------------------------------------------------------------- */
+void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps) {
+    int64_t n = numel(a);
+    float* tmp = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    Tensor t = *a;
+    t.data = tmp;
+    nnc_add(a, b, &t);
+    nnc_layernorm(&t, scale, bias, out, axis, eps);
+    free(tmp);
+}
+
 void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out) {
     static const int bin[] = {OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_ADD_RELU, OP_ADD_SIGMOID};
     static const int un[] = {U_RELU, U_SIGMOID, U_TANH};

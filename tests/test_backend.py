@@ -124,9 +124,13 @@ def test_generate_equals_compile(model, opt, pkg, tmp_path):
     assert result.metadata["target"] == "mi355x" and result.metadata["calls"] > 0
 
 
-def test_generate_reads_entry_point_budget_and_strategy(pkg, tmp_path):
-    from nnc_py_amd.compiler import zoo
+def test_generate_reads_entry_point_budget_and_strategy(pkg, tmp_path, monkeypatch):
+    from nnc_py_amd.compiler import executor, zoo
     from nnc_py_amd.compiler.backend import Mi355xBackend
+    # (with the residual Add fused into its LayerNorm this encoder's plan
+    # peaks at the FFN MatMul's own working set, which no spill can lower:
+    # the budget test runs on the unfused program, whose peak can)
+    monkeypatch.setattr(executor, "ELTWISE_FUSION", False)
     g = zoo.transformer_encoder(batch=2, seq=16, seed=0)
     from nnc_py_amd.compiler import build_program
     peak = build_program(zoo.transformer_encoder(batch=2, seq=16, seed=0), 3).plan.activation_bytes

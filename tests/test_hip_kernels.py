@@ -693,3 +693,36 @@ def test_fused_eltwise_rejects_malformed_programs(hip, dmem, abi):
         assert runtime.last_error()[0] == 1, (why, runtime.last_error())
         assert (out == 7.0).all(), why
     runtime.clear_error()
+
+
+@pytest.mark.parametrize("shape,axis", [((3, 5, 256), -1), ((64, 3072), -1), ((2, 6, 4, 3), 1), ((3, 1001), -1)])
+def test_add_layernorm_matches_add_then_layernorm(shape, axis, hip, dmem, abi):
+    """nnc_hip_add_layernorm against nnc_add then nnc_layernorm on the GPU,
+    bit for bit: the row kernel with contiguous scale / bias (spans 256 and
+    3072), a strided axis (inner 12), and a span that is no multiple of 4
+    (the sum written, then the layernorm over it in place); a second addend
+    of another size is refused."""
+    from nnc_py_amd import runtime
+    rng = np.random.default_rng(9)
+    a, b = (rng.standard_normal(shape).astype(np.float32) for _ in range(2))
+    n = shape[axis % len(shape)]
+    g, bb = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32), (0.1 * rng.standard_normal(n)).astype(np.float32)
+    tail = [("t", "g"), ("t", "bb"), ("t", "out"), ("i", axis), ("f", 1e-5)]
+    print(f"case add_layernorm {shape} axis {axis}", flush=True)
+    got = caserun.run_case(hip, {"name": "addln", "op": "nnc_hip_add_layernorm",
+                                 "tensors": {"a": a, "b": b, "g": g, "bb": bb, "out": np.zeros_like(a)},
+                                 "args": [("t", "a"), ("t", "b")] + tail, "outputs": ["out"]}, abi, dmem)["out"]
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    s = caserun.run_case(hip, {"name": "add", "op": "nnc_add", "tensors": {"a": a, "b": b, "s": np.zeros_like(a)},
+                               "args": [("t", "a"), ("t", "b"), ("t", "s")], "outputs": ["s"]}, abi, dmem)["s"]
+    want = caserun.run_case(hip, {"name": "ln", "op": "nnc_layernorm",
+                                  "tensors": {"s": s, "g": g, "bb": bb, "out": np.zeros_like(a)},
+                                  "args": [("t", "s")] + tail, "outputs": ["out"]}, abi, dmem)["out"]
+    assert caserun.same_bits(got, want)
+    short = {"name": "short", "op": "nnc_hip_add_layernorm",
+             "tensors": {"a": a, "b": b.ravel()[:-4].copy(), "g": g, "bb": bb, "out": np.full_like(a, 7.0)},
+             "args": [("t", "a"), ("t", "b")] + tail, "outputs": ["out"]}
+    runtime.clear_error()
+    out = caserun.run_case(hip, short, abi, dmem)["out"]
+    assert runtime.last_error()[0] == 1 and (out == 7.0).all()
+    runtime.clear_error()

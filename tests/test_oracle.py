@@ -443,3 +443,31 @@ def test_oracle_fused_eltwise_closed_form(oracle_lib, abi):
     c = np.minimum(np.maximum(r, F32(-6)), F32(6)).astype(np.float64)
     ref = 1.0 / (1.0 + np.exp(-c)) + t.astype(np.float64)
     np.testing.assert_allclose(got, ref.astype(F32), rtol=2e-7, atol=2e-7)
+
+
+@pytest.mark.parametrize("shape,axis", [((3, 5, 256), -1), ((2, 6, 4, 3), 1)])
+def test_oracle_add_layernorm_composition(shape, axis, oracle_lib, abi):
+    """nnc_hip_add_layernorm: the oracle's nnc_add into a temporary, then its
+    nnc_layernorm (both pinned above), bit for bit; and within float32
+    rounding of float64 numpy (two-pass mean and variance over [axis:])."""
+    rng = np.random.default_rng(3)
+    a, b = (rng.standard_normal(shape).astype(F32) for _ in range(2))
+    ax = axis % len(shape)
+    n = shape[ax]
+    g, bb = (1 + 0.1 * rng.standard_normal(n)).astype(F32), (0.1 * rng.standard_normal(n)).astype(F32)
+    args = [("t", "g"), ("t", "bb"), ("t", "out"), ("i", axis), ("f", 1e-5)]
+    got = caserun.run_case(oracle_lib, {"name": "addln", "op": "nnc_hip_add_layernorm",
+                                        "tensors": {"a": a, "b": b, "g": g, "bb": bb, "out": np.zeros_like(a)},
+                                        "args": [("t", "a"), ("t", "b")] + args, "outputs": ["out"]}, abi)["out"]
+    s = caserun.run_case(oracle_lib, {"name": "add", "op": "nnc_add", "tensors": {"a": a, "b": b, "s": np.zeros_like(a)},
+                                      "args": [("t", "a"), ("t", "b"), ("t", "s")], "outputs": ["s"]}, abi)["s"]
+    want = caserun.run_case(oracle_lib, {"name": "ln", "op": "nnc_layernorm",
+                                         "tensors": {"s": s, "g": g, "bb": bb, "out": np.zeros_like(a)},
+                                         "args": [("t", "s")] + args, "outputs": ["out"]}, abi)["out"]
+    assert caserun.same_bits(got, want)
+    x = (a + b).astype(np.float64).reshape(int(np.prod(shape[:ax])), -1)
+    mean = x.mean(axis=1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=1, keepdims=True)
+    inner = int(np.prod(shape[ax + 1:]))
+    ref = (x - mean) / np.sqrt(var + 1e-5) * np.repeat(g, inner) + np.repeat(bb, inner)
+    np.testing.assert_allclose(got.reshape(ref.shape), ref, rtol=1e-4, atol=1e-5)
