@@ -261,6 +261,15 @@ void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps,
  * (runtime/x86/ops.c:82-119 then 2095-2171). */
 void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Tensor* out, int axis, float eps);
 
+/* nnc_hip_scaled_softmax: out = softmax(in / div[0]) over axis - attention's
+ * score scaling and the softmax after it in one pass, the quotient never
+ * written. div has one element; out is the size of in. The same bits as
+ * nnc_div(in, div, t) then nnc_softmax(t, out, axis) on this library.
+ * Emitted by the mi355x target's O3 pass for a Div by a one-element tensor
+ * whose only reader is a Softmax. No counterpart in the reference ABI
+ * (runtime/x86/ops.c:82-224 then 260-310). */
+void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis);
+
 /* nnc_hip_conv_packed_noalloc: nnc_hip_conv_packed for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference ABI.

@@ -25,7 +25,8 @@ from .lower import Call, lower
 from .passes import (SPILL_OPS, Branch, MemoryPlan, branch_calls, check_plan, eliminate_dead_code,
                      eliminate_identity, find_branches, fit_memory, fuse_matmul_bias, fuse_patterns, fuse_projection,
                      fuse_residual, pack_conv_weights, plan_memory, prepack_lowering, stream_tiles,
-                     eliminate_concat_split, fuse_eltwise_chains, compose_transposes, fuse_add_layernorm)
+                     eliminate_concat_split, fuse_eltwise_chains, compose_transposes, fuse_add_layernorm,
+                     fuse_scaled_softmax)
 
 
 @dataclass
@@ -50,8 +51,9 @@ PROJECTION_FUSION = True
 # nnc_hip_gap_gemm_nt.
 STREAM_TILES = True
 # O3: element-wise chains in one pass (nnc_hip_fused_eltwise), Add ->
-# LayerNormalization in one pass (nnc_hip_add_layernorm), Concat -> Split
-# round trips removed, Transpose -> Transpose composed into one copy
+# LayerNormalization in one pass (nnc_hip_add_layernorm), Div by one element
+# -> Softmax in one pass (nnc_hip_scaled_softmax), Concat -> Split round
+# trips removed, Transpose -> Transpose composed into one copy
 ELTWISE_FUSION = True
 # independent side branches (ResNet's downsample convolutions) on the second
 # library stream at O3 (mi355x target), while the main branch's convolutions
@@ -96,6 +98,7 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
             eliminate_concat_split(graph)
             compose_transposes(graph)
             fuse_add_layernorm(graph)
+            fuse_scaled_softmax(graph)
             fuse_eltwise_chains(graph)
     order = graph.topological_sort()
     branches = find_branches(graph, order, BRANCH_MAX_FLOPS) if use_branches else []

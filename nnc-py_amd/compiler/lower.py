@@ -186,6 +186,9 @@ def lower_node(g: Graph, node: Node) -> Call:
         return Call("nnc_hip_add_layernorm", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _opt(node, 3), _t(outs[0]),
                                               ("i", int(node.attrs.get("axis", -1))),
                                               ("f", float(node.attrs.get("epsilon", 1e-5)))], node.name)
+    if op == "ScaledSoftmax":  # Div by one element + softmax in one pass (include/nnc_hip.h)
+        return Call("nnc_hip_scaled_softmax", [_t(ins[0]), _t(ins[1]), _t(outs[0]),
+                                               ("i", int(node.attrs.get("axis", -1)))], node.name)
     if op == "FusedEltwise":  # an element-wise chain in one pass (include/nnc_hip.h)
         steps = node.attrs["steps"]
         prog = [v for st in steps for v in (st[0], st[1], st[2])]

@@ -598,6 +598,36 @@ def fuse_add_layernorm(g: Graph) -> int:
     return fused
 
 
+def fuse_scaled_softmax(g: Graph) -> int:
+    """A Div of a float32 tensor by a one-element float32 tensor whose
+    output only a Softmax reads (no graph output) becomes one ScaledSoftmax
+    node (inputs: x, divisor; the Softmax's attrs), lowered to
+    nnc_hip_scaled_softmax: attention's score scaling applied as the rows
+    are loaded. The same bits as the Div and the Softmax one after the
+    other."""
+    fused = 0
+    for div in list(g.nodes):
+        if div.op_type != "Div" or len(div.inputs) != 2 or div.outputs[0] in g.outputs:
+            continue
+        q = div.outputs[0]
+        x, d = (g.tensors[i] for i in div.inputs)
+        t = g.tensors[q]
+        if any(v.dtype != "float32" for v in (x, d, t)) or d.numel != 1 or x.numel != t.numel:
+            continue
+        users = g.consumers(q)
+        if len(users) != 1 or users[0].op_type != "Softmax" or users[0].inputs[0] != q:
+            continue
+        sm = users[0]
+        sm.op_type = "ScaledSoftmax"
+        sm.inputs = list(div.inputs)
+        sm.metadata["fused_from"] = [div.name, sm.name]
+        sm.metadata["tile_stream"] = {"intermediate": q, "hbm_bytes_saved": 2 * t.nbytes}
+        g.nodes.remove(div)
+        g.tensors.pop(q, None)
+        fused += 1
+    return fused
+
+
 def compose_transposes(g: Graph) -> int:
     """A Transpose whose input is another Transpose's output read by nothing
     else (and no graph output) becomes one Transpose of the first's input

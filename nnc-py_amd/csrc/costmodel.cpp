@@ -283,12 +283,14 @@ void gemm(const char* op, int M, int N, int K, int batches, bool a_kc, bool b_kc
     }
     if (batches == 1 && a_kc && b_kc && M <= 32 && K <= 1024 && K % 4 == 0) {
         // gemm.hip gemm_skinny_nt_k: 16 columns per workgroup, all rows, K
-        // over 8 waves; latency-bound: one round trip for every wave's loads
-        // (1 us), then its chunks' 16x16x4 MFMAs (32 cycles each at 2.1 GHz)
+        // over 8 waves; latency-bound: the first round trip of every wave's
+        // loads (0.5 us past the launch ramp; traced 4.1 us at M = 8, 5.1 us
+        // at M = 32, K = 512, N = 1000), then its chunks' 16x16x4 MFMAs
+        // (32 cycles each at 2.1 GHz)
         const double b = 4.0 * ((double)M * K + (double)N * K + (double)M * N);
         const double chain_us = (double)ceil_div(ceil_div(K, 16), 8) * 4 * (M > 16 ? 2 : 1) * 32 / 2100.0;
         record(op, M > 16 ? "gemm_skinny_nt_32" : "gemm_skinny_nt_16",
-               kLaunchUs + 1.0 + chain_us + b / (kHbm * kStreamEff) * 1e6, flops, b);
+               kLaunchUs + 0.5 + chain_us + b / (kHbm * kStreamEff) * 1e6, flops, b);
         return;
     }
     const bool a4 = a_kc ? K % 4 == 0 : M % 4 == 0;  // 16-byte loads along the contiguous axis
@@ -675,6 +677,12 @@ void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Te
     if (!a || !b || !out) return;
     stream_kernel("nnc_hip_add_layernorm", "nnc_hip_add_layernorm",
                   nbytes(a) + nbytes(b) + nbytes(out) + nbytes(scale) + nbytes(bias));
+}
+// norm.hip nnc_hip_scaled_softmax: nnc_softmax's row kernel dividing on load
+void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis) {
+    (void)axis;
+    if (in && div && out && numel(out) > 0)
+        stream_kernel("nnc_hip_scaled_softmax", "nnc_hip_scaled_softmax", nbytes(in) + nbytes(out), 0.40);
 }
 // eltwise.hip nnc_hip_fused_eltwise: one streaming pass, each input read and
 // the output written once

@@ -84,21 +84,35 @@ __device__ __forceinline__ void load_row4(float4 (&v)[PER], const float* base, i
     }
 }
 
-template <int PER>
-__global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, float* out, int64_t rows,
-                                                         int dim) {
+// DIV: the row's elements divided by the scalar *dv first (nnc_div's x / y)
+// - the attention score scaling of nnc_hip_scaled_softmax; the -inf fill of
+// lanes past the row stays as it is
+template <int PER, bool DIV>
+__device__ __forceinline__ void load_sm_row(float4 (&v)[PER], const float* base, int d4, int lane, float dv) {
+    load_row4<PER>(v, base, d4, lane, -INFINITY);
+    if (DIV) {
+#pragma unroll
+        for (int q = 0; q < PER; ++q)
+            if (lane + 64 * q < d4) v[q] = make_float4(v[q].x / dv, v[q].y / dv, v[q].z / dv, v[q].w / dv);
+    }
+}
+
+template <int PER, bool DIV>
+__global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, const float* div, float* out,
+                                                         int64_t rows, int dim) {
     const int lane = threadIdx.x & 63;
     const int64_t wstride = (int64_t)gridDim.x * 4;
     const int d4 = dim / 4;
     int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
+    const float dv = DIV ? div[0] : 1.0f;
     float4 v[PER];
-    load_row4<PER>(v, in + row * dim, d4, lane, -INFINITY);
+    load_sm_row<PER, DIV>(v, in + row * dim, d4, lane, dv);
     while (true) {
         const int64_t nrow = row + wstride;
         const bool more = nrow < rows;
         float4 nx[PER];
-        if (kPrefetch<PER> && more) load_row4<PER>(nx, in + nrow * dim, d4, lane, -INFINITY);
+        if (kPrefetch<PER> && more) load_sm_row<PER, DIV>(nx, in + nrow * dim, d4, lane, dv);
         float m = -INFINITY;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
@@ -130,7 +144,7 @@ __global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, float*
             if (idx < d4) y[idx] = make_float4(v[q].x * rs, v[q].y * rs, v[q].z * rs, v[q].w * rs);
         }
         if (!more) break;
-        if (!kPrefetch<PER>) load_row4<PER>(nx, in + nrow * dim, d4, lane, -INFINITY);
+        if (!kPrefetch<PER>) load_sm_row<PER, DIV>(nx, in + nrow * dim, d4, lane, dv);
 #pragma unroll
         for (int q = 0; q < PER; ++q) v[q] = nx[q];
         row = nrow;
@@ -398,8 +412,9 @@ static bool split_axis(const char* name, Tensor* in, int& axis, int64_t& outer, 
 static unsigned row_grid(int64_t rows) { return grid_for(rows, 4, 1); }
 
 template <int PER>
-static void softmax_v4(const float* x, float* y, int64_t rows, int dim, const char* name) {
-    launch(name, softmax_rows_v4_k<PER>, dim3(row_grid(rows)), dim3(256), 0, x, y, rows, dim);
+static void softmax_v4(const float* x, const float* dv, float* y, int64_t rows, int dim, const char* name) {
+    if (dv) launch(name, softmax_rows_v4_k<PER, true>, dim3(row_grid(rows)), dim3(256), 0, x, dv, y, rows, dim);
+    else launch(name, softmax_rows_v4_k<PER, false>, dim3(row_grid(rows)), dim3(256), 0, x, dv, y, rows, dim);
 }
 
 template <int PER>
@@ -420,31 +435,53 @@ using namespace nnc;
 
 extern "C" {
 
-void nnc_softmax(Tensor* in, Tensor* out, int axis) {
-    const char* name = "nnc_softmax";
+// softmax over axis of in (divided first by the one-element div: the
+// attention scaling of nnc_hip_scaled_softmax, out the size of in)
+static void softmax_run(Tensor* in, Tensor* div, Tensor* out, int axis, const char* name) {
     if (!ready(name)) return;
-    if (!has_data(in) || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
+    if (!has_data(in) || !has_data(out) || (div && !has_data(div))) return fail(NNC_HIP_EINVAL, name, "NULL tensor or data");
     int64_t outer, len, inner;
     if (!split_axis(name, in, axis, outer, len, inner)) return;
     if (numel(out) < numel(in)) return fail(NNC_HIP_EINVAL, name, "output smaller than input");
+    if (div && numel(div) != 1) return fail(NNC_HIP_EINVAL, name, "the divisor is not one element");
+    if (div && numel(out) != numel(in)) return fail(NNC_HIP_EINVAL, name, "output and input differ in size");
     if (outer * len * inner == 0) return;
     const float* x = (const float*)in->data;
+    const float* dv = div ? (const float*)div->data : nullptr;
     float* y = (float*)out->data;
     if (len >= (1 << 30)) return fail(NNC_HIP_EUNSUPP, name, "axis too long");
-    set_work(0.0, 8.0 * (double)(outer * len * inner));
+    set_work(0.0, 8.0 * (double)(outer * len * inner) + (div ? 4.0 : 0.0));
     if (inner == 1) {
         const int dim = (int)len;
         const bool v4 = dim % 4 == 0 && aligned16(x) && aligned16(y);
-        if (v4 && dim <= 256) return softmax_v4<1>(x, y, outer, dim, name);
-        if (v4 && dim <= 512) return softmax_v4<2>(x, y, outer, dim, name);
-        if (v4 && dim <= 1024) return softmax_v4<4>(x, y, outer, dim, name);
-        if (v4 && dim <= 2048) return softmax_v4<8>(x, y, outer, dim, name);
-        if (v4 && dim <= 4096) return softmax_v4<16>(x, y, outer, dim, name);
-        launch(name, softmax_rows_k, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, dim);
+        if (v4 && dim <= 256) return softmax_v4<1>(x, dv, y, outer, dim, name);
+        if (v4 && dim <= 512) return softmax_v4<2>(x, dv, y, outer, dim, name);
+        if (v4 && dim <= 1024) return softmax_v4<4>(x, dv, y, outer, dim, name);
+        if (v4 && dim <= 2048) return softmax_v4<8>(x, dv, y, outer, dim, name);
+        if (v4 && dim <= 4096) return softmax_v4<16>(x, dv, y, outer, dim, name);
+    }
+    if (div) {
+        // other rows: the quotient into out, then the softmax over it in
+        // place (each lane reads an element before it writes it)
+        nnc_div(in, div, out);
+        x = y;
+    }
+    if (inner == 1) {
+        launch(name, softmax_rows_k, dim3(grid_for(outer, 4, 1)), dim3(256), 0, x, y, outer, (int)len);
         return;
     }
     launch(name, softmax_cols_k, dim3(grid_for(outer * inner, 1)), dim3(256), 0, x, y, outer, (int)len,
            inner);
+}
+
+void nnc_softmax(Tensor* in, Tensor* out, int axis) { softmax_run(in, nullptr, out, axis, "nnc_softmax"); }
+
+// No reference counterpart: the attention scaling (a Div by a one-element
+// tensor) and the softmax after it in one pass (the mi355x target's O3
+// fusion of Div -> Softmax).
+void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis) {
+    if (!div) return fail(NNC_HIP_EINVAL, "nnc_hip_scaled_softmax", "NULL divisor");
+    softmax_run(in, div, out, axis, "nnc_hip_scaled_softmax");
 }
 
 // layernorm of in (+ in2, same size: the residual add of

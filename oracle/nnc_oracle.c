@@ -187,6 +187,22 @@ void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Te
     free(tmp);
 }
 
+/* ------------------------------------------------------------------------
+ * nnc_hip_scaled_softmax (include/nnc_hip.h): target-only, no reference
+ * counterpart. Restated as the two calls it replaces: nnc_div by the
+ * one-element div into a temporary (ops.c:82-224), then nnc_softmax of it
+ * (ops.c:260-310).
+ * ---------------------------------------------------------------------- */
+void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis) {
+    int64_t n = numel(in);
+    float* tmp = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    Tensor t = *in;
+    t.data = tmp;
+    nnc_div(in, div, &t);
+    nnc_softmax(&t, out, axis);
+    free(tmp);
+}
+
 void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out) {
     static const int bin[] = {OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_ADD_RELU, OP_ADD_SIGMOID};
     static const int un[] = {U_RELU, U_SIGMOID, U_TANH};

@@ -695,6 +695,38 @@ def test_fused_eltwise_rejects_malformed_programs(hip, dmem, abi):
     runtime.clear_error()
 
 
+@pytest.mark.parametrize("shape,axis,d", [((8, 4, 128, 128), -1, 4.0), ((32, 2048), -1, -1.5),
+                                         ((4, 4000), -1, 0.125), ((3, 6, 5), 1, 2.5), ((5, 1001), -1, 3.0)])
+def test_scaled_softmax_matches_div_then_softmax(shape, axis, d, hip, dmem, abi):
+    """nnc_hip_scaled_softmax against nnc_div then nnc_softmax on the GPU,
+    bit for bit: the row kernel dividing on load (rows of 128, 2048 with a
+    negative divisor, 4000), a strided axis and a row that is no multiple of
+    4 (the quotient written, then the softmax over it in place); a divisor of
+    two elements is refused."""
+    from nnc_py_amd import runtime
+    rng = np.random.default_rng(6)
+    x = (3 * rng.standard_normal(shape)).astype(np.float32)
+    dv = np.array([d], np.float32)
+    print(f"case scaled_softmax {shape} axis {axis} d {d}", flush=True)
+    args = [("t", "x"), ("t", "d"), ("t", "out"), ("i", axis)]
+    got = caserun.run_case(hip, {"name": "ssm", "op": "nnc_hip_scaled_softmax",
+                                 "tensors": {"x": x, "d": dv, "out": np.zeros_like(x)},
+                                 "args": args, "outputs": ["out"]}, abi, dmem)["out"]
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    q = caserun.run_case(hip, {"name": "div", "op": "nnc_div", "tensors": {"x": x, "d": dv, "q": np.zeros_like(x)},
+                               "args": [("t", "x"), ("t", "d"), ("t", "q")], "outputs": ["q"]}, abi, dmem)["q"]
+    want = caserun.run_case(hip, {"name": "sm", "op": "nnc_softmax", "tensors": {"q": q, "out": np.zeros_like(x)},
+                                  "args": [("t", "q"), ("t", "out"), ("i", axis)], "outputs": ["out"]}, abi, dmem)["out"]
+    assert caserun.same_bits(got, want)
+    two = {"name": "two", "op": "nnc_hip_scaled_softmax",
+           "tensors": {"x": x, "d": np.array([d, d], np.float32), "out": np.full_like(x, 7.0)},
+           "args": args, "outputs": ["out"]}
+    runtime.clear_error()
+    out = caserun.run_case(hip, two, abi, dmem)["out"]
+    assert runtime.last_error()[0] == 1 and (out == 7.0).all()
+    runtime.clear_error()
+
+
 @pytest.mark.parametrize("shape,axis", [((3, 5, 256), -1), ((64, 3072), -1), ((2, 6, 4, 3), 1), ((3, 1001), -1)])
 def test_add_layernorm_matches_add_then_layernorm(shape, axis, hip, dmem, abi):
     """nnc_hip_add_layernorm against nnc_add then nnc_layernorm on the GPU,

@@ -445,6 +445,29 @@ def test_oracle_fused_eltwise_closed_form(oracle_lib, abi):
     np.testing.assert_allclose(got, ref.astype(F32), rtol=2e-7, atol=2e-7)
 
 
+@pytest.mark.parametrize("shape,axis,d", [((2, 4, 16, 16), -1, 2.0), ((3, 7), -1, -0.7), ((2, 5, 3), 1, 0.35)])
+def test_oracle_scaled_softmax_composition(shape, axis, d, oracle_lib, abi):
+    """nnc_hip_scaled_softmax: the oracle's nnc_div by the one-element
+    divisor into a temporary, then its nnc_softmax (both pinned above), bit
+    for bit; and within float32 rounding of float64 numpy softmax(x / d)
+    (a negative divisor flips which element is the row maximum)."""
+    rng = np.random.default_rng(4)
+    x = (3 * rng.standard_normal(shape)).astype(F32)
+    dv = np.array([d], F32)
+    got = caserun.run_case(oracle_lib, {"name": "ssm", "op": "nnc_hip_scaled_softmax",
+                                        "tensors": {"x": x, "d": dv, "out": np.zeros_like(x)},
+                                        "args": [("t", "x"), ("t", "d"), ("t", "out"), ("i", axis)],
+                                        "outputs": ["out"]}, abi)["out"]
+    q = caserun.run_case(oracle_lib, {"name": "div", "op": "nnc_div", "tensors": {"x": x, "d": dv, "q": np.zeros_like(x)},
+                                      "args": [("t", "x"), ("t", "d"), ("t", "q")], "outputs": ["q"]}, abi)["q"]
+    want = caserun.run_case(oracle_lib, {"name": "sm", "op": "nnc_softmax", "tensors": {"q": q, "out": np.zeros_like(x)},
+                                         "args": [("t", "q"), ("t", "out"), ("i", axis)], "outputs": ["out"]}, abi)["out"]
+    assert caserun.same_bits(got, want)
+    z = x.astype(np.float64) / float(dv[0])
+    e = np.exp(z - z.max(axis=axis, keepdims=True))
+    np.testing.assert_allclose(got, e / e.sum(axis=axis, keepdims=True), rtol=2e-6, atol=1e-7)
+
+
 @pytest.mark.parametrize("shape,axis", [((3, 5, 256), -1), ((2, 6, 4, 3), 1)])
 def test_oracle_add_layernorm_composition(shape, axis, oracle_lib, abi):
     """nnc_hip_add_layernorm: the oracle's nnc_add into a temporary, then its
