@@ -270,6 +270,17 @@ void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Te
  * (runtime/x86/ops.c:82-224 then 260-310). */
 void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis);
 
+/* nnc_hip_transpose_slice: out = transpose(view, perm), where view is the
+ * block of columns [col0, col0 + width) of in (in read as rows of its last
+ * extent W), taken row-major and shaped as out and perm imply (view.shape
+ * [perm[d]] = out.shape[d]) - a Split piece along the last axis, reshaped
+ * and transposed, read straight from the unsplit tensor. 4-byte elements.
+ * The same bits as nnc_split, then nnc_transpose of the reshaped piece.
+ * Emitted by the mi355x target's O3 pass for attention's head split. No
+ * counterpart in the reference ABI (runtime/x86/ops.c:2183-2251 nnc_split,
+ * then 1531-1581 nnc_transpose). */
+void nnc_hip_transpose_slice(Tensor* in, Tensor* out, int64_t* perm, int ndim, int col0, int width);
+
 /* nnc_hip_conv_packed_noalloc: nnc_hip_conv_packed for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference ABI.

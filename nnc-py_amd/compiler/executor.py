@@ -26,7 +26,7 @@ from .passes import (SPILL_OPS, Branch, MemoryPlan, branch_calls, check_plan, el
                      eliminate_identity, find_branches, fit_memory, fuse_matmul_bias, fuse_patterns, fuse_projection,
                      fuse_residual, pack_conv_weights, plan_memory, prepack_lowering, stream_tiles,
                      eliminate_concat_split, fuse_eltwise_chains, compose_transposes, fuse_add_layernorm,
-                     fuse_scaled_softmax)
+                     fuse_scaled_softmax, fuse_split_transposes)
 
 
 @dataclass
@@ -53,7 +53,8 @@ STREAM_TILES = True
 # O3: element-wise chains in one pass (nnc_hip_fused_eltwise), Add ->
 # LayerNormalization in one pass (nnc_hip_add_layernorm), Div by one element
 # -> Softmax in one pass (nnc_hip_scaled_softmax), Concat -> Split round
-# trips removed, Transpose -> Transpose composed into one copy
+# trips removed, Transpose -> Transpose composed into one copy, a Split's
+# pieces reshaped and transposed straight from the unsplit tensor
 ELTWISE_FUSION = True
 # independent side branches (ResNet's downsample convolutions) on the second
 # library stream at O3 (mi355x target), while the main branch's convolutions
@@ -97,6 +98,7 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
         if target_passes and ELTWISE_FUSION:
             eliminate_concat_split(graph)
             compose_transposes(graph)
+            fuse_split_transposes(graph)
             fuse_add_layernorm(graph)
             fuse_scaled_softmax(graph)
             fuse_eltwise_chains(graph)

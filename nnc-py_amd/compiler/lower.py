@@ -186,6 +186,11 @@ def lower_node(g: Graph, node: Node) -> Call:
         return Call("nnc_hip_add_layernorm", [_t(ins[0]), _t(ins[1]), _opt(node, 2), _opt(node, 3), _t(outs[0]),
                                               ("i", int(node.attrs.get("axis", -1))),
                                               ("f", float(node.attrs.get("epsilon", 1e-5)))], node.name)
+    if op == "SliceTranspose":  # a Split piece's reshape + transpose in one copy (include/nnc_hip.h)
+        perm = [int(v) for v in node.attrs["perm"]]
+        return Call("nnc_hip_transpose_slice", [_t(ins[0]), _t(outs[0]), ("i64", perm), ("i", len(perm)),
+                                                ("i", int(node.attrs["col0"])), ("i", int(node.attrs["width"]))],
+                    node.name)
     if op == "ScaledSoftmax":  # Div by one element + softmax in one pass (include/nnc_hip.h)
         return Call("nnc_hip_scaled_softmax", [_t(ins[0]), _t(ins[1]), _t(outs[0]),
                                                ("i", int(node.attrs.get("axis", -1)))], node.name)

@@ -628,6 +628,56 @@ def fuse_scaled_softmax(g: Graph) -> int:
     return fused
 
 
+def fuse_split_transposes(g: Graph) -> int:
+    """A float32 Split along the last axis whose every piece is read only by
+    a Reshape, itself read only by a Transpose (attention's head split of
+    the fused QKV projection), loses the Split and the Reshapes: each
+    Transpose becomes a SliceTranspose of the unsplit tensor (attrs perm,
+    col0, width), lowered to nnc_hip_transpose_slice. A copy of the same
+    elements: the bits of the Split, the Reshape and the Transpose."""
+    fused = 0
+    for split in list(g.nodes):
+        if split.op_type != "Split" or not split.inputs or not split.outputs:
+            continue
+        x = g.tensors[split.inputs[0]]
+        nd = len(x.shape)
+        if nd < 1 or x.dtype != "float32" or int(split.attrs.get("axis", 0)) % nd != nd - 1:
+            continue
+        chains = []
+        for piece in split.outputs:
+            users = g.consumers(piece)
+            if piece in g.outputs or len(users) != 1 or users[0].op_type != "Reshape" or users[0].inputs[0] != piece:
+                break
+            rs = users[0]
+            tr = g.consumers(rs.outputs[0])
+            if rs.outputs[0] in g.outputs or len(tr) != 1 or tr[0].op_type != "Transpose" or tr[0].inputs[0] != rs.outputs[0]:
+                break
+            chains.append((piece, rs, tr[0]))
+        if len(chains) != len(split.outputs):
+            continue
+        widths = [int(g.tensors[p].shape[-1]) for p, _, _ in chains]
+        if sum(widths) != int(x.shape[-1]) or x.shape[-1] >= 1 << 31:
+            continue
+        col0 = 0
+        for (piece, rs, tr), w in zip(chains, widths):
+            vnd = len(g.tensors[rs.outputs[0]].shape)
+            tr.attrs["perm"] = [int(v) for v in (tr.attrs.get("perm") or range(vnd - 1, -1, -1))]
+            tr.op_type = "SliceTranspose"
+            tr.inputs = [split.inputs[0]]
+            tr.attrs["col0"], tr.attrs["width"] = col0, w
+            tr.metadata["fused_from"] = [split.name, rs.name, tr.name]
+            col0 += w
+            g.nodes.remove(rs)
+            for t in rs.outputs + [piece]:
+                g.tensors.pop(t, None)
+            for c in rs.inputs[1:]:
+                if c in g.tensors and not g.consumers(c) and c not in g.outputs:
+                    g.tensors.pop(c, None)
+        g.nodes.remove(split)
+        fused += 1
+    return fused
+
+
 def compose_transposes(g: Graph) -> int:
     """A Transpose whose input is another Transpose's output read by nothing
     else (and no graph output) becomes one Transpose of the first's input

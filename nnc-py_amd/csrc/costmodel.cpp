@@ -678,6 +678,13 @@ void nnc_hip_add_layernorm(Tensor* a, Tensor* b, Tensor* scale, Tensor* bias, Te
     stream_kernel("nnc_hip_add_layernorm", "nnc_hip_add_layernorm",
                   nbytes(a) + nbytes(b) + nbytes(out) + nbytes(scale) + nbytes(bias));
 }
+// movement.hip nnc_hip_transpose_slice: nnc_transpose's gather reading a
+// column block of the unsplit tensor
+void nnc_hip_transpose_slice(Tensor* in, Tensor* out, int64_t* perm, int ndim, int col0, int width) {
+    (void)in, (void)perm, (void)ndim, (void)col0, (void)width;
+    if (out && numel(out) > 0)
+        stream_kernel("nnc_hip_transpose_slice", "nnc_hip_transpose_slice", 2.0 * nbytes(out), 0.6);
+}
 // norm.hip nnc_hip_scaled_softmax: nnc_softmax's row kernel dividing on load
 void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis) {
     (void)axis;

@@ -70,6 +70,26 @@ __global__ void __launch_bounds__(256) permute_k(const E* in, E* out, int64_t to
     }
 }
 
+// permute_k over a column slice: the permuted tensor is the [rows][width]
+// block at column col0 of a [rows][W] buffer, read row-major (a Split's
+// piece, reshaped); p's strides are the slice's own, each source index f
+// lands at row f / width, column col0 + f % width of the buffer
+__global__ void __launch_bounds__(256) permute_slice_k(const float* in, float* out, int64_t total, PermArgs p,
+                                                       int64_t width, int64_t W, int64_t col0) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += stride) {
+        int64_t rem = o, src = 0;
+        for (int d = p.ndim - 1; d >= 0; --d) {
+            const int64_t ext = p.out_ext[d];
+            const int64_t idx = rem % ext;
+            rem /= ext;
+            src += idx * p.in_stride_of_out_axis[d];
+        }
+        const int64_t r = src / width;
+        out[o] = in[r * W + col0 + (src - r * width)];
+    }
+}
+
 // 2-D tile transpose through LDS for batched [B][R][C] -> [B][C][R]
 // (the innermost axis moves): coalesced reads along C and writes along R.
 __global__ void __launch_bounds__(256) transpose2d_k(const float* in, float* out, int64_t R, int64_t C) {
@@ -354,6 +374,46 @@ void nnc_transpose(Tensor* in, Tensor* out, int64_t* perm, int ndim) {
     }
     launch(name, permute_k<float>, dim3(grid_for(total, 1)), dim3(256), 0, (const float*)in->data,
            (float*)out->data, total, p);
+}
+
+// No reference counterpart: a Split piece's reshape and transpose read
+// straight from the unsplit tensor (the mi355x target's O3 fusion of Split
+// -> Reshape -> Transpose).
+void nnc_hip_transpose_slice(Tensor* in, Tensor* out, int64_t* perm, int ndim, int col0, int width) {
+    const char* name = "nnc_hip_transpose_slice";
+    if (!two(name, in, out)) return;
+    if (ndim < 1 || ndim > 8 || out->ndim != ndim || in->ndim < 1)
+        return fail(NNC_HIP_EINVAL, name, "rank %d (output %d, at most 8)", ndim, out->ndim);
+    if (in->dtype == NNC_DTYPE_INT64 || out->dtype == NNC_DTYPE_INT64)
+        return fail(NNC_HIP_EUNSUPP, name, "4-byte elements only");
+    const int64_t W = in->shape[in->ndim - 1];
+    if (col0 < 0 || width < 1 || col0 + width > W)
+        return fail(NNC_HIP_EINVAL, name, "columns [%lld, %lld) outside rows of %lld", (long long)col0,
+                    (long long)(col0 + width), (long long)W);
+    const int64_t rows = numel(in) / W, total = numel(out);
+    if (total != rows * width)
+        return fail(NNC_HIP_EINVAL, name, "output of %lld elements, the slice holds %lld", (long long)total,
+                    (long long)(rows * width));
+    int64_t pm[8], vs[8], vst[8];
+    unsigned seen = 0;
+    for (int d = 0; d < ndim; ++d) {
+        pm[d] = perm ? perm[d] : ndim - 1 - d;
+        if (pm[d] < 0 || pm[d] >= ndim || (seen >> pm[d] & 1u)) return fail(NNC_HIP_EINVAL, name, "not a permutation");
+        seen |= 1u << pm[d];
+        vs[pm[d]] = out->shape[d];
+    }
+    vst[ndim - 1] = 1;
+    for (int d = ndim - 2; d >= 0; --d) vst[d] = vst[d + 1] * vs[d + 1];
+    if (total == 0) return;
+    PermArgs p{};
+    p.ndim = ndim;
+    for (int d = 0; d < ndim; ++d) {
+        p.out_ext[d] = out->shape[d];
+        p.in_stride_of_out_axis[d] = vst[pm[d]];
+    }
+    set_work(0.0, 8.0 * (double)total);
+    launch(name, permute_slice_k, dim3(grid_for(total, 1)), dim3(256), 0, (const float*)in->data,
+           (float*)out->data, total, p, width, W, col0);
 }
 
 void nnc_tile(Tensor* in, Tensor* out, int64_t* repeats, int ndim) {

@@ -74,6 +74,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_fused_eltwise": (abi.TARGET_SIGNATURES["nnc_hip_fused_eltwise"], None),
     "nnc_hip_add_layernorm": (abi.TARGET_SIGNATURES["nnc_hip_add_layernorm"], None),
     "nnc_hip_scaled_softmax": (abi.TARGET_SIGNATURES["nnc_hip_scaled_softmax"], None),
+    "nnc_hip_transpose_slice": (abi.TARGET_SIGNATURES["nnc_hip_transpose_slice"], None),
 }
 
 

@@ -1178,3 +1178,30 @@ void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh,
     nnc_maxpool2d(&t, out, 3, 3, 2, 2, 1, 1);
     free(tmp);
 }
+
+/* ------------------------------------------------------------------------
+ * nnc_hip_transpose_slice (include/nnc_hip.h): target-only, no reference
+ * counterpart. Restated as the calls it replaces: the Split piece (columns
+ * [col0, col0 + width) of every row of in) copied out row-major into a
+ * temporary shaped as the transpose's input, then nnc_transpose of it.
+ * ---------------------------------------------------------------------- */
+void nnc_hip_transpose_slice(Tensor* in, Tensor* out, int64_t* perm, int ndim, int col0, int width) {
+    int64_t w_full = in->shape[in->ndim - 1];
+    int64_t rows = numel(in) / w_full, n = rows * width;
+    int64_t vs[8], pm[8];
+    for (int d = 0; d < ndim; ++d) {
+        pm[d] = perm ? perm[d] : ndim - 1 - d;
+        vs[pm[d]] = out->shape[d];
+    }
+    float* tmp = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    const float* x = (const float*)in->data;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < width; ++c) tmp[r * width + c] = x[r * w_full + col0 + c];
+    Tensor t = *in;
+    t.data = tmp;
+    t.shape = vs;
+    t.ndim = ndim;
+    t.nbytes = n * (int64_t)sizeof(float);
+    nnc_transpose(&t, out, perm, ndim);
+    free(tmp);
+}

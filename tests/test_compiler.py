@@ -422,9 +422,11 @@ def test_transformer_add_layernorm_and_transposes(pkg, oracle_lib, monkeypatch):
     """O3 (mi355x target) on the transformer encoder: each residual Add and
     the LayerNormalization reading it become one FusedAddLayerNorm
     (nnc_hip_add_layernorm), each score scaling Div and its Softmax become
-    one ScaledSoftmax (nnc_hip_scaled_softmax), and K's head transpose
+    one ScaledSoftmax (nnc_hip_scaled_softmax), K's head transpose
     followed by its transpose for Q K^T becomes one Transpose ([0,2,1,3]
-    then [0,1,3,2] = [0,2,3,1]): 36 -> 28 calls. On the oracle the output has the bits of the
+    then [0,1,3,2] = [0,2,3,1]), and the QKV Split's pieces are transposed
+    straight from the projection's output (nnc_hip_transpose_slice): 36 ->
+    26 calls. On the oracle the output has the bits of the
     same O3 program without these rewrites."""
     from nnc_py_amd.compiler import Executor, build_program, executor, zoo
     kw = dict(batch=2, seq=8, d_model=16, heads=2, ffn=32, seed=3)
@@ -432,12 +434,13 @@ def test_transformer_add_layernorm_and_transposes(pkg, oracle_lib, monkeypatch):
     ops = [c.op for c in prog.calls]
     assert ops.count("nnc_hip_add_layernorm") == 4 and "nnc_layernorm" not in ops and "nnc_add" not in ops
     assert ops.count("nnc_hip_scaled_softmax") == 2 and "nnc_softmax" not in ops and "nnc_div" not in ops
-    perms = [c.args[2][1] for c in prog.calls if c.op == "nnc_transpose"]
+    assert ops.count("nnc_hip_transpose_slice") == 6 and "nnc_split" not in ops
+    perms = [c.args[2][1] for c in prog.calls if c.op in ("nnc_transpose", "nnc_hip_transpose_slice")]
     assert perms.count([0, 2, 3, 1]) == 2 and [0, 1, 3, 2] not in perms
-    assert len(build_program(zoo.transformer_encoder(seed=1), opt_level=3).calls) == 28
+    assert len(build_program(zoo.transformer_encoder(seed=1), opt_level=3).calls) == 26
     monkeypatch.setattr(executor, "ELTWISE_FUSION", False)
     ref = build_program(zoo.transformer_encoder(**kw), opt_level=3)
-    assert [c.op for c in ref.calls].count("nnc_layernorm") == 4 and len(ref.calls) == len(prog.calls) + 8
+    assert [c.op for c in ref.calls].count("nnc_layernorm") == 4 and len(ref.calls) == len(prog.calls) + 10
     x = (np.random.default_rng(5).standard_normal((2, 8, 16)) * 0.5).astype(np.float32)
     outs = []
     for p in (prog, ref):

@@ -43,6 +43,7 @@ FAMILY = [
     (r"gemm_skinny_nt_", "gemm_skinny_nt_k"),
     (r"nnc_hip_add_layernorm$", "layernorm_rows_v4_k"),
     (r"nnc_hip_scaled_softmax$", "softmax_rows_v4_k"),
+    (r"nnc_hip_transpose_slice$", "permute_slice_k"),
     (r"nnc_hip_fused_eltwise$", "fused_eltwise_vec4_k"),
     (r"nnc_maxpool2d$", "maxpool3s2_v4_k"),
     (r"nnc_avgpool2d_global$", "global_avgpool_k"),

@@ -695,6 +695,35 @@ def test_fused_eltwise_rejects_malformed_programs(hip, dmem, abi):
     runtime.clear_error()
 
 
+@pytest.mark.parametrize("rows,W,col0,view,perm", [(1024, 768, 0, (8, 128, 4, 64), (0, 2, 1, 3)),
+                                                   (1024, 768, 256, (8, 128, 4, 64), (0, 2, 3, 1)),
+                                                   (1024, 768, 512, (8, 128, 4, 64), (0, 2, 1, 3)),
+                                                   (33, 10, 3, (33, 7), (1, 0))])
+def test_transpose_slice_matches_numpy(rows, W, col0, view, perm, hip, dmem, abi):
+    """nnc_hip_transpose_slice on the GPU: the QKV head split of the
+    encoder at batch 8, sequence 128 (each of the three pieces) and a ragged
+    2-D slice, equal to numpy's slice, reshape and transpose; columns past
+    the row and an output of the wrong size are refused."""
+    from nnc_py_amd import runtime
+    width = int(np.prod(view)) // rows
+    x = np.random.default_rng(8).standard_normal((rows, W)).astype(np.float32)
+    want = np.ascontiguousarray(x[:, col0:col0 + width].reshape(view).transpose(perm))
+    print(f"case transpose_slice rows {rows} W {W} col0 {col0} perm {perm}", flush=True)
+
+    def case(c0, out):
+        return {"name": "ts", "op": "nnc_hip_transpose_slice", "tensors": {"x": x, "out": out},
+                "args": [("t", "x"), ("t", "out"), ("i64", list(perm)), ("i", len(perm)), ("i", c0), ("i", width)],
+                "outputs": ["out"]}
+    got = caserun.run_case(hip, case(col0, np.zeros_like(want)), abi, dmem)["out"]
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    assert got.tobytes() == want.tobytes()
+    for c0, out in ((W - width + 1, np.full_like(want, 7.0)), (col0, np.full(want.size - 1, 7.0, np.float32))):
+        runtime.clear_error()
+        bad = caserun.run_case(hip, case(c0, out), abi, dmem)["out"]
+        assert runtime.last_error()[0] == 1 and (bad == 7.0).all()
+    runtime.clear_error()
+
+
 @pytest.mark.parametrize("shape,axis,d", [((8, 4, 128, 128), -1, 4.0), ((32, 2048), -1, -1.5),
                                          ((4, 4000), -1, 0.125), ((3, 6, 5), 1, 2.5), ((5, 1001), -1, 3.0)])
 def test_scaled_softmax_matches_div_then_softmax(shape, axis, d, hip, dmem, abi):

@@ -468,6 +468,23 @@ def test_oracle_scaled_softmax_composition(shape, axis, d, oracle_lib, abi):
     np.testing.assert_allclose(got, e / e.sum(axis=axis, keepdims=True), rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("rows,W,col0,view,perm", [(12, 24, 8, (3, 4, 2, 4), (0, 2, 1, 3)),
+                                                   (12, 24, 16, (3, 4, 2, 4), (0, 2, 3, 1)),
+                                                   (5, 7, 0, (5, 3), (1, 0))])
+def test_oracle_transpose_slice(rows, W, col0, view, perm, oracle_lib, abi):
+    """nnc_hip_transpose_slice: columns [col0, col0 + width) of every row,
+    reshaped to the view and permuted - numpy's slice, reshape and
+    transpose, exactly."""
+    width = int(np.prod(view)) // rows
+    x = np.arange(rows * W, dtype=F32).reshape(rows, W) * F32(0.5) - F32(3)
+    want = np.ascontiguousarray(x[:, col0:col0 + width].reshape(view).transpose(perm))
+    got = caserun.run_case(oracle_lib, {"name": "ts", "op": "nnc_hip_transpose_slice",
+                                        "tensors": {"x": x, "out": np.zeros_like(want)},
+                                        "args": [("t", "x"), ("t", "out"), ("i64", list(perm)), ("i", len(perm)),
+                                                 ("i", col0), ("i", width)], "outputs": ["out"]}, abi)["out"]
+    assert got.tobytes() == want.tobytes()
+
+
 @pytest.mark.parametrize("shape,axis", [((3, 5, 256), -1), ((2, 6, 4, 3), 1)])
 def test_oracle_add_layernorm_composition(shape, axis, oracle_lib, abi):
     """nnc_hip_add_layernorm: the oracle's nnc_add into a temporary, then its
