@@ -81,6 +81,93 @@ def timed_steps(ex, steps: int, warmup: int, graph: bool, runtime) -> float:
     return time.perf_counter() - t0
 
 
+def latency_samples(ex, iters: int, warmup: int, graph: bool, runtime) -> dict:
+    """The reference harness's measurement shape (benchmarks/cases.py:23-31:
+    5 warmup + 20 measured runs; benchmarks/harness.py:139-161: mean, p50
+    and p95 by nearest rank): each step timed on its own, from its launch
+    to the end of a synchronisation, in milliseconds."""
+    for _ in range(warmup):
+        ex.replay() if graph else ex.run()
+    runtime.sync()
+    samples = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        ex.replay() if graph else ex.run()
+        runtime.sync()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    srt = sorted(samples)
+
+    def rank(p):  # nearest rank, k = ceil(p * n), 1-indexed
+        return srt[max(0, min(len(srt) - 1, int(np.ceil(p * len(srt))) - 1))]
+    return {"latency_ms_mean": round(float(np.mean(samples)), 4), "latency_ms_p50": round(rank(0.50), 4),
+            "latency_ms_p95": round(rank(0.95), 4), "iters": iters, "warmup": warmup}
+
+
+class ClockSampler:
+    """The GPU's shader (GFX) clock sampled every `period` seconds on a
+    thread while the caller keeps the GPU busy, through amdsmi; of several
+    visible GPUs, the one whose GFX activity was highest. None where amdsmi
+    cannot read it (the reason is kept in `error`)."""
+
+    def __init__(self, period: float = 0.01):
+        self.period = period
+        self.error = None
+        self.handles = []
+        self.samples = {}
+        self._stop = None
+        self._thread = None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self.smi = amdsmi
+            self.handles = list(amdsmi.amdsmi_get_processor_handles())
+        except Exception as e:  # no driver access, no library
+            self.error = f"amdsmi: {e}".splitlines()[0][:160]
+
+    def _read(self, h):
+        info = self.smi.amdsmi_get_clock_info(h, self.smi.AmdSmiClkType.GFX)
+        act = self.smi.amdsmi_get_gpu_activity(h)
+        return float(info["clk"]), float(act.get("gfx_activity", 0) if isinstance(act, dict) else 0)
+
+    def _run(self):
+        while not self._stop.is_set():
+            for i, h in enumerate(self.handles):
+                try:
+                    self.samples.setdefault(i, []).append(self._read(h))
+                except Exception as e:
+                    self.error = f"amdsmi read: {e}".splitlines()[0][:160]
+            self._stop.wait(self.period)
+
+    def __enter__(self):
+        import threading
+        if self.handles:
+            self._stop = threading.Event()
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        if self._thread:
+            self._stop.set()
+            self._thread.join(timeout=5)
+        return False
+
+    def result(self) -> dict | None:
+        best = None
+        for i, rows in self.samples.items():
+            if not rows:
+                continue
+            clk = [r[0] for r in rows]
+            act = float(np.mean([r[1] for r in rows]))
+            if best is None or act > best["gfx_activity_pct"]:
+                best = {"mean_mhz": round(float(np.mean(clk)), 1), "min_mhz": round(min(clk), 1),
+                        "max_mhz": round(max(clk), 1), "samples": len(clk), "gfx_activity_pct": round(act, 1)}
+        if best is None:
+            return {"error": self.error or "no amdsmi samples"}
+        best["source"] = "amdsmi GFX clock, sampled every 10 ms during hipGraph replays of the batch program"
+        return best
+
+
 def kernel_table(ex, runtime, steps: int) -> list[dict]:
     """Per-kernel averages over `steps` directly launched nnc_run() calls."""
     runtime.profile_reset()
@@ -144,10 +231,18 @@ def cpu_baseline(pkg, iters_b1: int, iters_b32: int, batch: int) -> dict | None:
         path, kind = port, "port"
     else:
         return None
-    lib = abi.bind(ctypes.CDLL(str(path)))
     # the oracle's convolution uses OpenMP threads: pin it to one for a
-    # one-thread figure (the reference's ops.c is single-threaded)
+    # one-thread figure (the reference's ops.c is single-threaded). libgomp
+    # reads OMP_NUM_THREADS when it is loaded, so set it before the library
+    # is, and also through omp_set_num_threads in case libgomp was loaded
+    # earlier in this process
     os.environ["OMP_NUM_THREADS"] = "1"
+    raw = ctypes.CDLL(str(path))
+    try:
+        raw.omp_set_num_threads(ctypes.c_int(1))
+    except AttributeError:
+        pass  # not an OpenMP build (the reference runtime)
+    lib = abi.bind(raw)
     dt1 = _cpu_rate(lib, 1, 1, iters_b1)
     dtb = _cpu_rate(lib, batch, 1, iters_b32) if iters_b32 > 0 else None
     cpu = "unknown"
@@ -464,6 +559,10 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-graph", action="store_true", help="launch each nnc_* call instead of a hipGraph")
     ap.add_argument("--profile-steps", type=int, default=5)
+    ap.add_argument("--latency-batches", default="1,8,16,32",
+                    help="batches timed per step as the reference harness does (mean/p50/p95; '' skips)")
+    ap.add_argument("--clock-seconds", type=float, default=1.0,
+                    help="seconds of graph replays at the benchmark batch while the shader clock is sampled (0 skips)")
     ap.add_argument("--cpu-iters", type=int, default=10, help="timed batch-1 runs of the CPU baseline")
     ap.add_argument("--cpu-iters-batch", type=int, default=3,
                     help="timed runs of the CPU baseline at the benchmark batch (0: batch 1 only)")
@@ -498,7 +597,10 @@ def main() -> int:
     graph = not args.no_graph
     results = {}
     tables = {}
+    clock = None
+    lat_batches = [int(b) for b in args.latency_batches.split(",") if b.strip()]
     runs = [(args.batch, args.steps)] + ([] if args.no_b1 else [(1, max(args.steps, 50))])
+    runs += [(b, 20) for b in lat_batches if b not in dict(runs)]
     for batch, steps in runs:
         log(f"building ResNet-18 batch {batch}")
         prog = build_program(zoo.resnet18(batch=batch, seed=1), opt_level=3)
@@ -514,6 +616,20 @@ def main() -> int:
         results[batch] = {"images_per_s": batch * steps / dt, "ms_per_step": dt / steps * 1e3, "steps": steps}
         log(f"batch {batch}: {results[batch]['ms_per_step']:.3f} ms/step, "
             f"{results[batch]['images_per_s']:.1f} images/s")
+        if batch in lat_batches:
+            results[batch]["latency"] = latency_samples(ex, 20, 5, graph, runtime)
+            log(f"batch {batch}: per-step latency p50 {results[batch]['latency']['latency_ms_p50']:.3f} ms, "
+                f"p95 {results[batch]['latency']['latency_ms_p95']:.3f} ms")
+        if batch == args.batch and args.clock_seconds > 0 and graph:
+            sampler = ClockSampler()
+            with sampler:
+                t_end = time.perf_counter() + args.clock_seconds
+                while time.perf_counter() < t_end:
+                    for _ in range(10):
+                        ex.replay()
+                    runtime.sync()
+            clock = sampler.result()
+            log(f"shader clock during replays: {clock}")
         if batch == args.batch:
             tables[batch] = kernel_table(ex, runtime, args.profile_steps)
         ex.close()
@@ -547,6 +663,11 @@ def main() -> int:
                 "peak": peak, "unit": dom["unit"], "frac": round(dom["achieved"] / peak, 4),
                 "traffic": traffic, "avg_launch_us": dom["avg_us"],
                 "work_per_launch": dom["work_per_launch"]}
+    if clock and "mean_mhz" in clock:
+        # the published peak assumes the 2.4 GHz peak engine clock; the
+        # kernel ran at the sampled clock
+        roofline["shader_clock_mhz"] = clock["mean_mhz"]
+        roofline["frac_at_clock"] = round(dom["achieved"] / (peak * clock["mean_mhz"] / 2400.0), 4)
     if traffic_detail:
         roofline["traffic_detail"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in traffic_detail.items()}
     gpu_ms = sum(r["ms_per_step"] for r in table)
@@ -585,6 +706,9 @@ def main() -> int:
         "per_kernel_timing": ("hipEvent pair on the library stream around each launch of directly launched nnc_run() "
                               "calls: a launch of a few microseconds reads about 2.5 us long (event overhead), so "
                               "small kernels' frac is understated; rocprofv3 kernel durations are in profiles/"),
+        "batches": {str(bt): {"images_per_s": round(r["images_per_s"], 2), "ms_per_step": round(r["ms_per_step"], 4),
+                              **r.get("latency", {})} for bt, r in sorted(results.items())},
+        "shader_clock": clock,
         "cpu_baseline": cpu,
         "dropin": dropin,
         "host": platform.node(),

@@ -1141,10 +1141,6 @@ static constexpr bool kInKernelFixup = true;
 // reference-layout 3x3 convolutions from this much work on are repacked
 static constexpr double kRepackMinFlops = 1e9;
 static constexpr int kMaxInKernelParts = 4;
-// 128x128 direct-to-LDS tiles finish shared tiles in-kernel too (off: on
-// ResNet-18's batch-32 layers it measured 62.0 -> 69.0 us per launch, the
-// finishing workgroups' partial reads sit on the kernel's critical path)
-static constexpr bool kFinish128 = false;
 
 typedef Tile<128, 128, 32, 2, 2> ConvT128;  // Co >= 128: 2x2 blocks per wave
 typedef Tile<64, 128, 32, 1, 4> ConvT64;    // Co == 64, many pixels: 2x1 blocks per wave
@@ -1193,9 +1189,10 @@ template <class T, class L>
 static void launch_conv_dma_t(ConvArgs& a, const char* entry, const char* name) {
     // the in-kernel finish only where it measured faster than the fixup
     // kernel (64x128 tiles: ResNet's 64-channel layers and the stem);
-    // elsewhere its code costs the main loop registers
-    constexpr bool FIN = kInKernelFixup && L::kFinishInKernel && T::NW == 4 &&
-                         ((T::BM == 64 && T::BN == 128) || (kFinish128 && T::BM == 128 && T::BN == 128));
+    // elsewhere its code costs the main loop registers (128x128 tiles on
+    // ResNet-18's batch-32 layers: 62.0 -> 69.0 us per launch, the
+    // finishing workgroups' partial reads on the kernel's critical path)
+    constexpr bool FIN = kInKernelFixup && L::kFinishInKernel && T::NW == 4 && T::BM == 64 && T::BN == 128;
     auto kernel = conv_dma_k<T, L, FIN>;
     const size_t lds = (size_t)(DmaStage<T>::LDS_FLOATS + L::EXTRA_LDS_FLOATS) * sizeof(float);
     // once per kernel, thread-safe (C++ static initialisation): the LDS limit
@@ -1962,7 +1959,14 @@ static constexpr size_t kStaticCounters = 16384;
 static __device__ __align__(256) unsigned char scratch[kStaticPartialBytes + kStaticCounters * sizeof(int)];
 static constexpr int kMaxDevices = 64;
 static unsigned char* g_scratch_addr[kMaxDevices] = {};
+// per device: recorded after each call's last launch; the next call's
+// stream waits on it first, so calls on one device run one after another
+// whatever thread or stream issued them
+static hipEvent_t g_scratch_done[kMaxDevices] = {};
 static std::mutex g_scratch_mutex;
+// held while a call enqueues its wait, launches and record: the calls'
+// order on the device is the order in which they take it
+static std::mutex g_scratch_order;
 
 int conv_static_scratch_setup(int device) {
     if (device < 0 || device >= kMaxDevices) {
@@ -1974,6 +1978,10 @@ int conv_static_scratch_setup(int device) {
     void* p = nullptr;
     if (!hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "nnc_hip_init", "hipGetSymbolAddress(scratch)"))
         return NNC_HIP_EDEVICE;
+    hipEvent_t ev = nullptr;
+    if (!hip_ok(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "nnc_hip_init", "hipEventCreate(scratch order)"))
+        return NNC_HIP_EDEVICE;
+    g_scratch_done[device] = ev;
     g_scratch_addr[device] = static_cast<unsigned char*>(p);
     return NNC_HIP_OK;
 }
@@ -2080,10 +2088,15 @@ void nnc_hip_conv_maxpool(Tensor* in, Tensor* w, Tensor* b, Tensor* out, int kh,
 // counters in the device's static scratch (64 MiB + 16384 counters) instead
 // of the grow-only workspace; shapes needing more fail with NNC_HIP_EUNSUPP
 // before anything is launched. The counters a launch uses are cleared by a
-// fill kernel just before it; calls are not timed in the profiling table. Calls that overlap on one device - from several threads or streams -
-// share the one array and race. The calling thread must already have its
-// library state (nnc_hip_init or any earlier call on that thread), which
-// this entry point never creates (NNC_HIP_ESTATE otherwise).
+// fill kernel just before it; calls are not timed in the profiling table.
+// Calls on one device share the one array, so they are ordered on the
+// device: each call's stream first waits for the previous call's work (an
+// event recorded after every call, whichever thread or stream made it).
+// Inside a graph capture the captured calls are ordered by the graph
+// instead; a replay is not ordered against calls made outside it. The
+// calling thread must already have its library state (nnc_hip_init or any
+// earlier call on that thread), which this entry point never creates
+// (NNC_HIP_ESTATE otherwise).
 void nnc_hip_conv_packed_noalloc(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw, int sh,
                                  int sw, int ph, int pw, int act) {
     const char* name = "nnc_hip_conv_packed_noalloc";
@@ -2100,9 +2113,15 @@ void nnc_hip_conv_packed_noalloc(Tensor* in, Tensor* w, Tensor* b, Tensor* res, 
     fs.cnt = reinterpret_cast<int*>(base + kStaticPartialBytes);
     fs.cnt_n = kStaticCounters;
     ThreadState& t = ts();
+    std::lock_guard<std::mutex> order(g_scratch_order);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (!hip_ok(hipStreamIsCapturing(t.stream(), &cap), name, "hipStreamIsCapturing")) return;
+    const bool ordered = cap == hipStreamCaptureStatusNone;
+    if (ordered && !hip_ok(hipStreamWaitEvent(t.stream(), g_scratch_done[d], 0), name, "hipStreamWaitEvent")) return;
     t.fixed = &fs;
     conv_run(in, w, b, out, kh, kw, sh, sw, ph, pw, act, name, res, true);
     t.fixed = nullptr;
+    if (ordered) hip_ok(hipEventRecord(g_scratch_done[d], t.stream()), name, "hipEventRecord");
 }
 
 }  // extern "C"

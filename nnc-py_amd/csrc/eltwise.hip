@@ -448,6 +448,7 @@ void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps,
     const char* name = "nnc_hip_fused_eltwise";
     if (!ready(name)) return;
     if (!ins || !prog || !has_data(out)) return fail(NNC_HIP_EINVAL, name, "NULL argument");
+    if (out->dtype != NNC_DTYPE_FLOAT32) return fail(NNC_HIP_EUNSUPP, name, "float32 output only");
     if (n_in < 1 || n_in > kEwMaxIn) return fail(NNC_HIP_EINVAL, name, "1 to %d inputs, got %d", kEwMaxIn, n_in);
     if (n_steps < 1 || n_steps > kEwMaxSteps)
         return fail(NNC_HIP_EINVAL, name, "1 to %d steps, got %d", kEwMaxSteps, n_steps);
@@ -462,6 +463,7 @@ void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps,
     for (int i = 0; i < n_in; ++i) {
         if (!has_data(ins[i]) || numel(ins[i]) != n)
             return fail(NNC_HIP_EINVAL, name, "input %d must have numel(out) = %lld elements", i, (long long)n);
+        if (ins[i]->dtype != NNC_DTYPE_FLOAT32) return fail(NNC_HIP_EUNSUPP, name, "input %d: float32 only", i);
         p.in[i] = static_cast<const float*>(ins[i]->data);
         vec = vec && aligned16(p.in[i]);
     }

@@ -384,8 +384,12 @@ void nnc_hip_transpose_slice(Tensor* in, Tensor* out, int64_t* perm, int ndim, i
     if (!two(name, in, out)) return;
     if (ndim < 1 || ndim > 8 || out->ndim != ndim || in->ndim < 1)
         return fail(NNC_HIP_EINVAL, name, "rank %d (output %d, at most 8)", ndim, out->ndim);
-    if (in->dtype == NNC_DTYPE_INT64 || out->dtype == NNC_DTYPE_INT64)
-        return fail(NNC_HIP_EUNSUPP, name, "4-byte elements only");
+    // the gather moves 4-byte words: float32 or int32 on both sides
+    const bool four_in = in->dtype == NNC_DTYPE_FLOAT32 || in->dtype == NNC_DTYPE_INT32;
+    const bool four_out = out->dtype == NNC_DTYPE_FLOAT32 || out->dtype == NNC_DTYPE_INT32;
+    if (!four_in || !four_out || in->dtype != out->dtype)
+        return fail(NNC_HIP_EUNSUPP, name, "float32 or int32 elements of one type only (dtypes %d, %d)",
+                    (int)in->dtype, (int)out->dtype);
     const int64_t W = in->shape[in->ndim - 1];
     if (col0 < 0 || width < 1 || col0 + width > W)
         return fail(NNC_HIP_EINVAL, name, "columns [%lld, %lld) outside rows of %lld", (long long)col0,

@@ -661,7 +661,8 @@ def test_fused_eltwise_rejects_malformed_programs(hip, dmem, abi):
     """Input and step counts out of range, an unknown op, step 0 reading the
     running value, an operand past the inputs, an input shorter than the
     output and Clip without bounds are refused before any launch
-    (NNC_HIP_EINVAL); the output is untouched."""
+    (NNC_HIP_EINVAL), an int32 input too (NNC_HIP_EUNSUPP); the output is
+    untouched."""
     from ew_cases import ew_case
     from nnc_py_amd import runtime
     xs = [np.ones(64, np.float32), np.ones(64, np.float32)]
@@ -686,11 +687,13 @@ def test_fused_eltwise_rejects_malformed_programs(hip, dmem, abi):
     short = ew_case(2, [("ADD", 0, 1)], [xs[0], np.ones(63, np.float32)])
     short["tensors"]["out"] = np.zeros(64, np.float32)
     bad.append(("short input", short))
+    bad.append(("int32 input", ew_case(2, [("ADD", 0, 1)], [xs[0], np.ones(64, np.int32)])))
     for why, case in bad:
         case["tensors"]["out"] = np.full_like(case["tensors"]["out"], 7.0)
         runtime.clear_error()
         out = caserun.run_case(hip, case, abi, dmem)["out"]
-        assert runtime.last_error()[0] == 1, (why, runtime.last_error())
+        # a malformed call is NNC_HIP_EINVAL (1), a non-float32 tensor NNC_HIP_EUNSUPP (4)
+        assert runtime.last_error()[0] == (4 if why == "int32 input" else 1), (why, runtime.last_error())
         assert (out == 7.0).all(), why
     runtime.clear_error()
 
@@ -717,11 +720,55 @@ def test_transpose_slice_matches_numpy(rows, W, col0, view, perm, hip, dmem, abi
     got = caserun.run_case(hip, case(col0, np.zeros_like(want)), abi, dmem)["out"]
     assert runtime.last_error()[0] == 0, runtime.last_error()[1]
     assert got.tobytes() == want.tobytes()
-    for c0, out in ((W - width + 1, np.full_like(want, 7.0)), (col0, np.full(want.size - 1, 7.0, np.float32))):
+    for c0, out, code in ((W - width + 1, np.full_like(want, 7.0), 1), (col0, np.full(want.size - 1, 7.0, np.float32), 1),
+                          (col0, np.full(want.shape, 7, np.int8), 4), (col0, np.full(want.shape, 7, np.int32), 4)):
+        # past the row, one element short (NNC_HIP_EINVAL); 1-byte elements,
+        # float32 -> int32 (NNC_HIP_EUNSUPP)
         runtime.clear_error()
         bad = caserun.run_case(hip, case(c0, out), abi, dmem)["out"]
-        assert runtime.last_error()[0] == 1 and (bad == 7.0).all()
+        assert runtime.last_error()[0] == code and (bad == 7).all(), runtime.last_error()
     runtime.clear_error()
+
+
+def test_transformer_fusions_match_oracle_at_encoder_shapes(hip, dmem, abi, oracle_lib):
+    """The three O3 transformer entry points at the encoder's own shapes
+    (batch 8, sequence 128, d_model 256, 4 heads) on the GPU against the
+    oracle's compositions of pinned entry points: nnc_hip_scaled_softmax on
+    the [8,4,128,128] scores divided by sqrt(64) (nnc_div then nnc_softmax,
+    ops.c:82-224, 260-310), nnc_hip_add_layernorm on the [1024,256]
+    residual stream (nnc_add then nnc_layernorm, ops.c:2095-2171) within
+    the fp bar, and nnc_hip_transpose_slice for each of Q, K, V of the
+    [1024,768] projection (the slice copied out, then nnc_transpose,
+    ops.c:1531-1581) bit for bit."""
+    rng = np.random.default_rng(12)
+    scores = (rng.standard_normal((8, 4, 128, 128)) * 4).astype(np.float32)
+    case = {"name": "ssm", "op": "nnc_hip_scaled_softmax",
+            "tensors": {"x": scores, "d": np.array([8.0], np.float32), "out": np.zeros_like(scores)},
+            "args": [("t", "x"), ("t", "d"), ("t", "out"), ("i", -1)], "outputs": ["out"]}
+    print("case scaled_softmax [8,4,128,128] vs oracle", flush=True)
+    _check(caserun.run_case(hip, case, abi, dmem)["out"], caserun.run_case(oracle_lib, case, abi)["out"],
+           "scaled_softmax [8,4,128,128]")
+    a, b = (rng.standard_normal((1024, 256)).astype(np.float32) for _ in range(2))
+    g = (1 + 0.1 * rng.standard_normal(256)).astype(np.float32)
+    bb = (0.1 * rng.standard_normal(256)).astype(np.float32)
+    case = {"name": "addln", "op": "nnc_hip_add_layernorm",
+            "tensors": {"a": a, "b": b, "g": g, "bb": bb, "out": np.zeros_like(a)},
+            "args": [("t", "a"), ("t", "b"), ("t", "g"), ("t", "bb"), ("t", "out"), ("i", -1), ("f", 1e-5)],
+            "outputs": ["out"]}
+    print("case add_layernorm [1024,256] vs oracle", flush=True)
+    _check(caserun.run_case(hip, case, abi, dmem)["out"], caserun.run_case(oracle_lib, case, abi)["out"],
+           "add_layernorm [1024,256]")
+    qkv = rng.standard_normal((1024, 768)).astype(np.float32)
+    for col0, perm in ((0, (0, 2, 1, 3)), (256, (0, 2, 3, 1)), (512, (0, 2, 1, 3))):
+        out = np.zeros((8, 4, 128, 64) if perm[-1] == 3 else (8, 4, 64, 128), np.float32)
+        case = {"name": "ts", "op": "nnc_hip_transpose_slice", "tensors": {"x": qkv, "out": out},
+                "args": [("t", "x"), ("t", "out"), ("i64", list(perm)), ("i", 4), ("i", col0), ("i", 256)],
+                "outputs": ["out"]}
+        print(f"case transpose_slice [1024,768] col0 {col0} vs oracle", flush=True)
+        got = caserun.run_case(hip, case, abi, dmem)["out"]
+        want = caserun.run_case(oracle_lib, case, abi)["out"]
+        assert caserun.same_bits(got, want), f"transpose_slice col0 {col0}"
+    dmem.release()
 
 
 @pytest.mark.parametrize("shape,axis,d", [((8, 4, 128, 128), -1, 4.0), ((32, 2048), -1, -1.5),

@@ -131,6 +131,46 @@ def test_lenet5_end_to_end(hip, oracle_lib):
     assert caserun.fp_violations(got, want, 1e-4, 1e-3).size == 0
 
 
+def test_resnet18_benchmark_program_b32_end_to_end(hip, oracle_lib):
+    """The program bench.py times - ResNet-18 at batch 32, O3 with this
+    target's passes and the default cost_aware plan (residual convolutions
+    written in place over their skip tensors, the stem's max pool inside
+    its row kernel, folded projections, 128x128 stream-K tiles with fixups)
+    - against the oracle running ResNet-18 at O1 on the same input: every
+    logit of all 32 images within the reference's end-to-end ResNet bar
+    (rtol 1.5e-2, atol 3e-3), the same top-1 class per image; then captured
+    and replayed as a hipGraph three times, each replay bit-identical to
+    the eager run."""
+    from nnc_py_amd import runtime
+    from nnc_py_amd.compiler import Executor, build_program, zoo
+    x = np.random.default_rng(0).standard_normal((32, 3, 224, 224)).astype(np.float32)
+    prog = build_program(zoo.resnet18(batch=32, seed=1), opt_level=3)
+    ops = {c.op for c in prog.calls}
+    assert {"nnc_hip_conv_packed", "nnc_hip_conv_proj", "nnc_hip_conv_maxpool"} <= ops, ops
+    print("resnet18 b32 O3 benchmark program: eager run", flush=True)
+    dev = Executor(prog, device=True)
+    dev.set_input("input", x)
+    dev.run()
+    got = dev.get("output")
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    dev.capture()
+    for rep in range(3):
+        print(f"resnet18 b32 O3 benchmark program: graph replay {rep}", flush=True)
+        dev.replay()
+        runtime.sync()
+        assert caserun.same_bits(dev.get("output"), got), f"replay {rep} differs from the eager run"
+    dev.close()
+    print("resnet18 b32: oracle program (O1)", flush=True)
+    host = Executor(build_program(zoo.resnet18(batch=32, seed=1), opt_level=1), device=False, lib=oracle_lib)
+    host.set_input("input", x)
+    host.run()
+    want = host.get("output")
+    bad = caserun.fp_violations(got, want, 3e-3, 1.5e-2)
+    print(f"resnet18 b32 logits: max |diff| {np.abs(got - want).max():.3g}", flush=True)
+    assert bad.size == 0, f"{bad.size} of {want.size} logits outside rtol 1.5e-2 / atol 3e-3"
+    assert (np.argmax(got, axis=1) == np.argmax(want, axis=1)).all()
+
+
 def test_resnet18_batch32_matches_batch1_per_image(hip):
     from nnc_py_amd.compiler import Executor, build_program, zoo
     x = np.random.default_rng(0).standard_normal((32, 3, 224, 224)).astype(np.float32)

@@ -81,28 +81,56 @@ def _dev(arr):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("entry", ["nnc_gemm", "nnc_gemm_nt"])
 @pytest.mark.parametrize("n", [1024, 2048, 4096])
-def test_gemm_sweep_full_size(n, hip):
-    """Gemm M=N=K with bias [N], U(-1,1). Size-independent checks at full
-    size: rows against float64 on a sample of rows, and linearity
-    (A (B1 + B2) = A B1 + A B2 within the fp32 bar)."""
+def test_gemm_sweep_full_size(n, entry, hip):
+    """Gemm M=N=K with bias [N], U(-1,1), at full size: as emitted
+    (nnc_gemm, transB=0; ops.c:1732-1841) and as O3 emits it for a constant
+    B (nnc_gemm_nt on B stored [N][K]; ops.c:1843-1886,
+    prepack_lowering.py:89-118). Checks that need no full float64 product:
+    16 sampled rows and 16 sampled columns element by element against
+    float64 (1e-4 abs / 1e-3 rel), and every row sum and column sum of the
+    output against float64's A (B 1) + sum(c) and (1' A) B + n c, within
+    1e-5 of the row's (column's) absolute sum - far below what one wrong
+    element or tile moves it by (about |out| ~ sqrt(n)/3), far above fp32
+    accumulation noise."""
     from nnc_py_amd import runtime
     rng = np.random.default_rng(n)
     a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
     b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
     c = rng.uniform(-1, 1, n).astype(np.float32)
+    print(f"case {entry} {n}^3", flush=True)
     ba, ta = _dev(a)
-    bb, tb = _dev(b)
+    bb, tb = _dev(b if entry == "nnc_gemm" else np.ascontiguousarray(b.T))
     bc, tc = _dev(c)
     bo, to = _dev(np.zeros((n, n), np.float32))
-    hip.nnc_gemm(ctypes.byref(ta[0]), ctypes.byref(tb[0]), ctypes.byref(tc[0]), ctypes.byref(to[0]), 1.0, 1.0, 0, 0)
+    if entry == "nnc_gemm":
+        hip.nnc_gemm(ctypes.byref(ta[0]), ctypes.byref(tb[0]), ctypes.byref(tc[0]), ctypes.byref(to[0]),
+                     1.0, 1.0, 0, 0)
+    else:
+        hip.nnc_gemm_nt(ctypes.byref(ta[0]), ctypes.byref(tb[0]), ctypes.byref(tc[0]), ctypes.byref(to[0]), 1.0, 1.0)
     runtime.sync()
-    assert runtime.last_error()[0] == 0
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
     out = bo.to_array()
+    for b_ in (ba, bb, bc, bo):
+        b_.free()
+    a64, b64, c64 = a.astype(np.float64), b.astype(np.float64), c.astype(np.float64)
     rows = rng.choice(n, 16, replace=False)
-    ref = a[rows].astype(np.float64) @ b.astype(np.float64) + c
-    bad = caserun.fp_violations(out[rows], ref, 1e-4, 1e-3)
-    assert bad.size == 0, f"{bad.size} of {ref.size} sampled outputs outside the bar"
+    cols = rng.choice(n, 16, replace=False)
+    ref_r = a64[rows] @ b64 + c64
+    ref_c = a64 @ b64[:, cols] + c64[cols]
+    bad = caserun.fp_violations(out[rows], ref_r, 1e-4, 1e-3)
+    assert bad.size == 0, f"{bad.size} of {ref_r.size} sampled-row outputs outside the bar"
+    bad = caserun.fp_violations(out[:, cols], ref_c, 1e-4, 1e-3)
+    assert bad.size == 0, f"{bad.size} of {ref_c.size} sampled-column outputs outside the bar"
+    o64 = out.astype(np.float64)
+    row_sum, row_ref = o64.sum(axis=1), a64 @ b64.sum(axis=1) + c64.sum()
+    col_sum, col_ref = o64.sum(axis=0), a64.sum(axis=0) @ b64 + n * c64
+    row_err = np.abs(row_sum - row_ref) / np.abs(o64).sum(axis=1)
+    col_err = np.abs(col_sum - col_ref) / np.abs(o64).sum(axis=0)
+    print(f"{entry} {n}: worst row-sum error {row_err.max():.3g}, column-sum error {col_err.max():.3g} "
+          f"(relative to the absolute sums)", flush=True)
+    assert row_err.max() < 1e-5 and col_err.max() < 1e-5
 
 
 @pytest.mark.gpu

@@ -8,7 +8,9 @@ Two calls in a row through the C-ABI - a ResNet-18 batch-32 layer-2 shape
 through the static tile counters) - each equal bit for bit to
 nnc_hip_conv_packed on the same inputs (same kernels, same stream-K plan)
 and within 1e-4 abs / 1e-3 rel of the oracle. A thread without library state
-gets NNC_HIP_ESTATE and no launch: the entry point never creates it.
+gets NNC_HIP_ESTATE and no launch: the entry point never creates it. Calls
+from two host threads on their own streams are ordered on the device, so
+they do not race on the shared array.
 """
 
 from __future__ import annotations
@@ -45,6 +47,53 @@ def test_noalloc_matches_conv_packed_twice(hip, dmem, abi, oracle_lib):
         bad = caserun.fp_violations(got, exp, 1e-4, 1e-3)
         assert bad.size == 0, f"{case['name']}: {bad.size} outputs outside the bar"
         dmem.release()
+
+
+def test_noalloc_calls_from_two_threads_are_ordered(hip, abi, oracle_lib):
+    """Two host threads, each on its own library stream, start together and
+    alternate no-alloc calls on the batch-32 shape (its stream-K partials
+    and fixup in the shared static array) with their own inputs and
+    outputs, four calls each without synchronising in between: every call
+    waits on the device for the previous one, so each thread's output
+    equals its nnc_hip_conv_packed result bit for bit."""
+    from nnc_py_amd import runtime
+    cases = [_packed_case(np.random.default_rng(40 + i), *SHAPES[0], act=1, bias=True, res=False) for i in range(2)]
+    results, errors = {}, []
+    start = threading.Barrier(2)
+
+    def worker(i):
+        try:
+            case = cases[i]
+            bufs = {k: runtime.DeviceBuffer.from_array(np.ascontiguousarray(v)) for k, v in case["tensors"].items()}
+            ts = {k: b.tensor() for k, b in bufs.items()}
+            args = [ctypes.byref(ts[a[1]][0]) if a[0] == "t" else (None if a[0] == "null" else a[1])
+                    for a in case["args"]]
+            hip.nnc_hip_conv_packed(*args)  # creates this thread's library state
+            runtime.sync()
+            want = bufs["out"].to_array()
+            start.wait(timeout=60)
+            for _ in range(4):
+                hip.nnc_hip_conv_packed_noalloc(*args)
+            runtime.sync()
+            results[i] = (bufs["out"].to_array(), want)
+            for b in bufs.values():
+                b.free()
+        except Exception as e:  # reported by the main thread
+            errors.append(f"thread {i}: {e!r}")
+
+    print("no-alloc: two threads, four calls each", flush=True)
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    for i in range(2):
+        got, want = results[i]
+        assert caserun.same_bits(got, want), f"thread {i}: no-alloc output differs from nnc_hip_conv_packed"
+        exp = caserun.run_case(oracle_lib, cases[i], abi)["out"]
+        assert caserun.fp_violations(got, exp, 1e-4, 1e-3).size == 0
 
 
 def test_noalloc_needs_the_threads_library_state(hip, abi):
