@@ -818,6 +818,148 @@ __global__ void __launch_bounds__(T::THREADS, DmaStage<T>::MIN_WAVES) conv_dma_k
 }
 
 // ---------------------------------------------------------------------------
+// Short convolutions (ResNet-18 at batch 1 and 2: few output tiles, K up to
+// 4608): `conv_ws_k`. A workgroup owns one 32 x 32 output tile (32 channels
+// x 32 pixels) over a contiguous range of K slices, and its four waves split
+// that range among themselves - wave w takes the range's slices w, w + 4,
+// ... - each computing the whole tile into its own v_mfma_f32_32x32x2_f32
+// accumulator; the four sums are added through LDS in wave order. Operands
+// go straight from global memory into the MFMA operand registers, with no
+// LDS staging and no barrier in the main loop: per slice (one tap and 32
+// channels of the tap-major weights, or 32 channels of the folded 1x1
+// projection) lane half h of a wave takes the slice's k = 16h .. 16h + 15,
+// so lane (row i, half h) loads A[i][16h ..] as four 16-byte loads and lane
+// (pixel j, half h) gathers B[16h + c][j] for c < 16 (one input channel
+// each, 0 outside the image), and MFMA step c multiplies those pairs. All
+// of a wave's slices (at most NS) are loaded before its first MFMA.
+//
+// A tile with more K than one workgroup should take is split over S <= 16
+// workgroups (contiguous slice ranges): each stores its 4 KB partial with
+// device-scope stores and the last to arrive adds the S partials in range
+// order and writes the tile (the stream-K finish protocol of mfma_tile.h:
+// store_partial4, finish_arrive, load_partial4). The sums are the same
+// whichever workgroup finishes: deterministic. Every shared tile is finished
+// in the launch: no fixup kernel.
+// ---------------------------------------------------------------------------
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// One 16-byte partial, stored with device-scope coherence.
+__device__ __forceinline__ void store_partial4(__amdgpu_buffer_rsrc_t ws, uint32_t byte_off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ws, (int)byte_off, 0, kDeviceScope);
+}
+
+template <int NS, bool PROJ>
+__global__ void __launch_bounds__(256, 2) conv_ws_k(ConvArgs a, int S, int iters) {
+    __shared__ __align__(16) float red[4][32 * 32];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = blockIdx.x / S, part = blockIdx.x - t * S;
+    const int mt = t % a.tiles_m, nt = t / a.tiles_m;
+    const int i0 = mt * 32, j0 = nt * 32;
+    const int kb = (int)((int64_t)part * iters / S), ke = (int)((int64_t)(part + 1) * iters / S);
+    const int h = lane >> 5, l32 = lane & 31;
+
+    // A: this lane's weight row, from k = 16h of a slice
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w), rin = make_rsrc(a.in);
+    const int co = i0 + l32;
+    const uint32_t arow = keep_or_oob((uint32_t)(co * a.ldw + 16 * h) * 4u, co < a.Co);
+    // B: this lane's pixel; taps inside the image as a bit mask
+    const int px = j0 + l32;
+    const bool valid = px < a.Npix;
+    const int hw = a.Ho * a.Wo, HW = a.H * a.W;
+    const int pq = valid ? px : 0;
+    const int n = pq / hw, rem = pq - n * hw;
+    const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
+    const int h0 = oh * a.sh - a.ph, w0 = ow * a.sw - a.pw;
+    uint32_t mask = 0;
+    for (int r = 0; r < a.kh; ++r)
+        for (int c = 0; c < a.kw; ++c) {
+            const bool in = valid && (unsigned)(h0 + r) < (unsigned)a.H && (unsigned)(w0 + c) < (unsigned)a.W;
+            mask |= (uint32_t)in << (r * a.kw + c);
+        }
+    const int bpo = n * a.Ci * HW + h0 * a.W + w0 + 16 * h * HW;  // tap (0, 0), channel 16h
+    const int CB = a.Ci >> 5, taps = a.kh * a.kw;
+    __amdgpu_buffer_rsrc_t rx = rin;
+    int xvo = 0, pHW = 0;
+    if constexpr (PROJ) {
+        rx = make_rsrc(a.pin);
+        pHW = a.pH * a.pW;
+        xvo = n * a.pci * pHW + oh * a.psh * a.pW + ow * a.psw + 16 * h * pHW;
+    }
+
+    f32x4 av[NS][4];
+    float bv[NS][16];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const int sl = kb + wave + 4 * q;  // wave-uniform
+        const bool on = sl < ke;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            av[q][u] = load_f32x4(rw, on ? arow + (uint32_t)sl * 128u + 16u * u : kOutOfRange);
+        const int tap = sl / CB, cb = sl - tap * CB;
+        const int r = tap / a.kw, cc = tap - r * a.kw;
+        bool in = on && ((mask >> (tap & 31)) & 1u);
+        uint32_t base = (uint32_t)(bpo + r * a.W + cc + cb * 32 * HW) * 4u;
+        uint32_t step = (uint32_t)HW * 4u;
+        __amdgpu_buffer_rsrc_t rb = rin;
+        if constexpr (PROJ) {
+            // the folded projection's slices: selects, not a branch (the
+            // loads stay one straight run)
+            const bool proj = tap >= taps;
+            const int pcb = sl - taps * CB;
+            in = proj ? on && valid : in;
+            base = proj ? (uint32_t)(xvo + pcb * 32 * pHW) * 4u : base;
+            step = proj ? (uint32_t)pHW * 4u : step;
+            rb = proj ? rx : rin;
+        }
+#pragma unroll
+        for (int c = 0; c < 16; ++c) bv[q][c] = load_f32(rb, in ? base + step * (uint32_t)c : kOutOfRange);
+    }
+    // every load above is issued before the first MFMA below
+    __builtin_amdgcn_sched_barrier(0);
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    // a wave with fewer slices multiplies zeros in its last one (straight-line
+    // code: a branch around it made the compiler sink that slice's loads
+    // into it, one round trip per load); its workgroup waits for the waves
+    // with NS slices anyway
+#pragma unroll
+    for (int q = 0; q < NS; ++q)
+#pragma unroll
+        for (int c = 0; c < 16; ++c) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][c >> 2][c & 3], bv[q][c], acc, 0, 0, 0);
+    // the four waves' sums in wave order; thread t then holds 4 consecutive
+    // pixels (columns 4 (t % 8) ..) of tile row t / 8
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float x = acc[r];  // (element copied first: see store_tile)
+        red[wave][(8 * (r >> 2) + 4 * h + (r & 3)) * 32 + l32] = x;
+    }
+    __syncthreads();
+    const int row = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
+    f32x4 v = *reinterpret_cast<const f32x4*>(&red[0][row * 32 + c4]);
+#pragma unroll
+    for (int w = 1; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(&red[w][row * 32 + c4]);
+    const int oco = i0 + row, op0 = j0 + c4;
+    if (S > 1) {
+        const __amdgpu_buffer_rsrc_t rws = make_rsrc(a.ws);
+        const uint32_t slot = (uint32_t)t * (uint32_t)S * 4096u + threadIdx.x * 16u;
+        store_partial4(rws, slot + (uint32_t)part * 4096u, v);
+        if (!finish_arrive(a.cnt + t, S - 1)) return;  // uniform
+        f32x4 p[kWsMaxSplit];
+#pragma unroll
+        for (int q = 0; q < kWsMaxSplit; ++q)
+            p[q] = load_partial4(rws, q < S && q != part ? slot + (uint32_t)q * 4096u : kOutOfRange);
+        f32x4 sum = part == 0 ? v : p[0];
+#pragma unroll
+        for (int q = 1; q < kWsMaxSplit; ++q)
+            if (q < S) sum += q == part ? v : p[q];
+        v = sum;
+    }
+    if (oco < a.Co && op0 < a.Npix) fixup_store(a, oco, op0, make_float4(v.x, v.y, v.z, v.w));
+}
+
+// ---------------------------------------------------------------------------
 // Convolution + relu streamed into a 3x3 / stride 2 / pad 1 max pool
 // (nnc_hip_conv_maxpool): ResNet's stem without its 103 MB (batch 32)
 // activation in HBM.
@@ -1235,6 +1377,51 @@ static void launch_conv_dma(ConvArgs& a, const char* entry) {
     launch_conv_dma_t<T, DmaPacked<T, KH, KW>>(a, entry, name);
 }
 
+template <int NS, bool PROJ>
+static void launch_ws_ns(const ConvArgs& a, int S, int iters, unsigned grid, const char* name) {
+    launch(name, conv_ws_k<NS, PROJ>, dim3(grid), dim3(256), 0, a, S, iters);
+}
+
+// conv_ws_k where plan_ws (plan.h) takes the convolution. Needs tap-major
+// packed weights (k = tap * Ci + ci, then the projection's channels), Ci
+// (and the projection's channels) multiples of 32, 16-byte aligned weights,
+// at most 32 taps: checked by the callers. Returns false (nothing launched)
+// where plan_ws declines or the split's scratch cannot be had (capture
+// before growth); the caller then takes its usual path.
+template <bool PROJ>
+static bool launch_conv_ws(ConvArgs& a, const char* entry) {
+    WsPlan wp;
+    if (!plan_ws(a.Co, a.Npix, a.K, wp)) return false;
+    const int64_t tiles = wp.tiles;
+    const int iters = wp.iters, S = wp.S, NS = wp.NS;
+    a.tiles_m = (int)ceil_div(a.Co, 32);
+    a.tiles_n = (int)ceil_div(a.Npix, 32);
+    a.ws = nullptr;
+    a.cnt = nullptr;
+    if (S > 1) {
+        a.ws = workspace((size_t)tiles * S * 4096);
+        a.cnt = a.ws ? tile_counters((size_t)tiles) : nullptr;
+        if (!a.cnt) return false;
+        if (ts().fixed)
+            launch("zero_tile_counters", zero_counters_k, dim3((unsigned)ceil_div(tiles, 256)), dim3(256), 0, a.cnt,
+                   (int)tiles);
+    }
+    char name[64];
+    snprintf(name, sizeof name, "conv_ws_32x32_k%dx%d%s", a.kh, a.kw, PROJ ? "p" : "");
+    set_work(2.0 * a.Co * (double)a.Npix * a.K, 0.0);
+    const unsigned grid = (unsigned)(tiles * S);
+    switch (NS) {
+        case 1: launch_ws_ns<1, PROJ>(a, S, iters, grid, name); break;
+        case 2: launch_ws_ns<2, PROJ>(a, S, iters, grid, name); break;
+        case 3: launch_ws_ns<3, PROJ>(a, S, iters, grid, name); break;
+        case 4: launch_ws_ns<4, PROJ>(a, S, iters, grid, name); break;
+        case 5: launch_ws_ns<5, PROJ>(a, S, iters, grid, name); break;
+        default: launch_ws_ns<6, PROJ>(a, S, iters, grid, name); break;
+    }
+    (void)entry;
+    return true;
+}
+
 // ---------------------------------------------------------------------------
 // The RGB stem (3 channels, 7x7, stride 2, pad 3, H == 2 Ho, W == 2 Wo,
 // Wo = 16 * BPR, Co <= 64) as a persistent kernel over output rows. A tile
@@ -1612,6 +1799,7 @@ static void launch_conv_stem(ConvArgs& a, const char* entry) {
 // 1x1 or 3x3, weights 16-byte aligned; checked by the caller.
 template <class T>
 static void launch_conv(ConvArgs& a, bool avec, bool dma, const char* entry) {
+    if (dma && launch_conv_ws<false>(a, entry)) return;
     a.tiles_m = (int)ceil_div(a.Co, T::BM);
     a.tiles_n = (int)ceil_div(a.Npix, T::BN);
     if (dma) {
@@ -1937,6 +2125,7 @@ static void conv_proj_run(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* o
     a.vec_out = aligned16(a.out);
     a.out32 = (int64_t)a.N * a.Co * a.Ho * a.Wo * 4 < ((int64_t)1 << 31);
     if (a.N == 0 || a.Co == 0 || a.Ho <= 0 || a.Wo <= 0) return;
+    if (launch_conv_ws<true>(a, name)) return;
     // the tile choice of conv_run
     if (a.K >= 512 && a.Co >= 128 && a.Npix >= 1024) return launch_conv_proj<ConvT128>(a, name);
     if (a.K >= 512 && a.Co <= 64 && a.Npix >= 4096) return launch_conv_proj<ConvT64>(a, name);

@@ -81,6 +81,11 @@ constexpr double kStemRowsEff = 0.55;
 constexpr double kColdUsPerMB = 0.061;  // weights (B operand) arriving from HBM, per MB
 constexpr double kFixupUsPerMB = 0.073; // fixup kernel: partial tiles read + finished tiles written, per MB
 constexpr double kFixupUsPerPart = 0.069; // fixup kernel: each partial summed into a tile (sequential)
+// conv_ws_k (short convolutions, plan_ws): one wave slice (32 x 32 x 32 MACs
+// and its operands' arrival) and the in-kernel finish of a split tile
+// (partial stores, counter, partial loads), fitted to ResNet-18 at batch 1
+constexpr double kWsSliceUs = 0.88;
+constexpr double kWsFinishUs = 1.9, kWsFinishUsPerPart = 0.2;
 
 // ---------------------------------------------------------------------------
 // the timeline and the per-kernel table
@@ -195,6 +200,22 @@ double fixup_us(const MfmaKind& k, const nnc::StreamK& sk) {
     return kLaunchUs + kFixupUsPerMB * bytes * 1e-6 + kFixupUsPerPart * parts;
 }
 
+// conv.hip conv_ws_k: each workgroup's waves run NS slices side by side;
+// a split tile adds the finish
+bool ws_kernel(const char* op, int kh, int kw, bool proj, int64_t Co, int64_t npix, int64_t K, double flops,
+               double bytes, double weight_bytes) {
+    nnc::WsPlan p;
+    if (!nnc::plan_ws(Co, npix, K, p)) return false;
+    char name[64];
+    snprintf(name, sizeof name, "conv_ws_32x32_k%dx%d%s", kh, kw, proj ? "p" : "");
+    const int r = (int)ceil_div(p.tiles * p.S, kCUs);  // workgroups sharing a CU
+    double us = kLaunchUs + r * p.NS * kWsSliceUs + kColdUsPerMB * weight_bytes * 1e-6;
+    if (p.S > 1) us += kWsFinishUs + kWsFinishUsPerPart * p.S;
+    us = fmax(us, kLaunchUs + bytes / (kHbm * kStreamEff) * 1e6);
+    record(op, name, us, flops, bytes);
+    return true;
+}
+
 // ---------------------------------------------------------------------------
 // convolution: conv.hip conv_run's choices
 // ---------------------------------------------------------------------------
@@ -233,6 +254,7 @@ void conv(const char* op, Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor*
         k = (Co <= 64 && npix >= 65536) ? &kStem64x128 : &kStem64;
         snprintf(name, sizeof name, "conv_igemm_%dx%d_k7x7c3_dma", k->bm, k->bn);
     } else {
+        if (dma && ws_kernel(op, kh, kw, false, Co, npix, K, flops, bytes, nbytes(w))) return;
         const int tile = (K >= 512 && Co >= 128 && npix >= 1024) ? 2 : (K >= 512 && Co <= 64 && npix >= 4096) ? 1 : 0;
         if (dma) {
             k = tile == 2 ? &kConv128 : tile == 1 ? &kConv64x128 : &kConv64;
@@ -523,6 +545,7 @@ void nnc_hip_conv_proj(Tensor* in, Tensor* w, Tensor* b, Tensor* x, Tensor* out,
     if (N == 0 || Co == 0 || npix == 0) return;
     const double flops = 2.0 * Co * (double)npix * K;
     const double bytes = nbytes(in) + nbytes(x) + nbytes(w) + nbytes(b) + nbytes(out);
+    if (ws_kernel(op, 3, 3, true, Co, npix, K, flops, bytes, nbytes(w))) return;
     const MfmaKind* k = (K >= 512 && Co >= 128 && npix >= 1024) ? &kConv128
                         : (K >= 512 && Co <= 64 && npix >= 4096) ? &kConv64x128 : &kConv64;
     char name[64];

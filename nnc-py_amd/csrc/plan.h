@@ -82,6 +82,59 @@ inline StreamK plan_streamk(int tiles, int iters, int slots, int fixup_slices) {
     return sk;
 }
 
+// ---------------------------------------------------------------------------
+// Short convolutions (conv.hip conv_ws_k): 32 x 32 output tiles, the four
+// waves of a workgroup splitting each tile's K range, S workgroups sharing a
+// tile (the last to arrive finishes it in the kernel), at most kWsMaxSlices
+// slices of 32 k per wave held in registers (NS).
+// Taken for convolutions with fewer 64 x 64 tiles than kWsMaxTiles64 and
+// at most kWsMaxFlops of work (ResNet-18 at batch 1 and 2, and the stride-2
+// convolutions at batch 4), where the 64 x 64 stream-K plan splits nearly
+// every tile and needs a fixup launch. Bigger ones keep the LDS-shared
+// tiles, whose waves share their operands: measured on ResNet-18, this
+// kernel up to 0.5 GFLOP per convolution gives batch 1 0.262 -> 0.198 ms,
+// batch 2 0.346 -> 0.286 ms, batch 4 0.436 -> 0.435 ms; up to 1 GFLOP batch
+// 4 0.435 -> 0.466 ms and batch 8 0.570 -> 0.597 ms (its stride-2
+// convolutions); and ResNet-18's layer 4 at batch 32 (7.4 GFLOP on 200
+// tiles of 64 x 64) 25.8k -> 19.2k images/s.
+// S: the smallest power of two that leaves a wave at most kWsMaxSlices
+// slices; a split tile costs the finish's round trips (partial stores, the
+// counter, partial loads: several slice times), so a tile that fits one
+// workgroup stays whole, and a split one is split further while the grid
+// stays within kWsGroups workgroups (one per CU) and each keeps at least 8
+// slices.
+// ---------------------------------------------------------------------------
+constexpr int kWsMaxSlices = 6;
+constexpr int kWsMaxSplit = 16;
+constexpr int kWsMaxTiles64 = 256;
+constexpr double kWsMaxFlops = 5e8;
+constexpr int kWsGroups = 256;
+
+struct WsPlan {
+    int64_t tiles;  // 32 x 32 tiles
+    int iters;      // slices of 32 k
+    int S, NS;
+};
+
+// false: conv_ws_k does not take this convolution (K a multiple of 32 and
+// the tap-major layout are the caller's to check)
+inline bool plan_ws(int64_t Co, int64_t Npix, int64_t K, WsPlan& p) {
+    if (K <= 0 || K % 32 != 0 || Co <= 0 || Npix <= 0) return false;
+    if (((Co + 63) / 64) * ((Npix + 63) / 64) >= kWsMaxTiles64 || 2.0 * Co * (double)Npix * K > kWsMaxFlops)
+        return false;
+    p.tiles = ((Co + 31) / 32) * ((Npix + 31) / 32);
+    p.iters = (int)(K / 32);
+    int S = 1;
+    while (S < kWsMaxSplit && (p.iters + S - 1) / S > 4 * kWsMaxSlices) S *= 2;
+    if (S > 1)
+        while (S < kWsMaxSplit && p.tiles * 2 * S <= kWsGroups && p.iters / (2 * S) >= 8) S *= 2;
+    const int per = (p.iters + S - 1) / S;
+    if (per > 4 * kWsMaxSlices) return false;
+    p.S = S;
+    p.NS = (per + 3) / 4;
+    return true;
+}
+
 // Fixup cost in slice times of a BM x BN tile: about one slice for 128x128
 // tiles, scaled by tile area for smaller tiles (shorter slices).
 constexpr int fixup_slices_for(int bm, int bn) { return (128 * 128) / (bm * bn); }

@@ -34,6 +34,7 @@ FAMILY = [
     (r"conv_stem_rows_", "conv_stem_k"),
     (r"conv_stem_pool_w", "conv_stem_pool_k"),
     (r"conv_igemm_.*_dma$", "conv_dma_k"),
+    (r"conv_ws_32x32_", "conv_ws_k"),
     (r"conv_igemm_", "conv_streamk_k"),
     (r"conv_streamk_fixup$", "conv_fixup_k"),
     (r"gemm_dma_", "gemm_dma_k"),

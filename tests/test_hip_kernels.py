@@ -149,20 +149,41 @@ def _packed_case(rng, n, ci, h, co, k, s, p, act=1, bias=True, res=True, w_ref=N
 
 
 # every tile configuration of the direct-to-LDS kernels, tails in Co and
-# pixels, stride 2, no padding, 1x1
+# pixels, stride 2, no padding, 1x1; batches large enough (over 0.5 GFLOP or
+# 256 tiles of 64 x 64) that the short-convolution kernel does not take them
 PACKED_SHAPES = [
-    (2, 64, 28, 64, 3, 1, 1),     # 64x64 tiles
+    (32, 32, 28, 64, 3, 1, 1),    # 64x64 tiles (K = 288)
     (4, 64, 56, 64, 3, 1, 1),     # 64x128 tiles, stream-K
     (8, 128, 28, 128, 3, 1, 1),   # 128x128 tiles, stream-K
     (16, 256, 14, 256, 3, 1, 1),  # 128x128 with a partial last pixel tile
-    (2, 256, 14, 512, 3, 2, 1),   # stride 2, many M tiles
+    (8, 256, 14, 512, 3, 2, 1),   # stride 2, many M tiles
     (4, 512, 7, 512, 3, 1, 1),    # K = 4608: many partials per tile
-    (3, 32, 13, 96, 3, 2, 1),     # odd image, Co and pixel tails
-    (3, 64, 19, 198, 3, 1, 1),    # 128x128 tiles: Co % 4 != 0, 1083 pixels of 361-pixel images
-    (2, 32, 9, 40, 3, 1, 1),      # Co < tile
+    (170, 32, 13, 96, 3, 2, 1),   # odd image, Co and pixel tails
+    (7, 64, 19, 198, 3, 1, 1),    # 128x128 tiles: Co % 4 != 0, 2527 pixels of 361-pixel images
+    (210, 32, 9, 40, 3, 1, 1),    # Co < tile
+    (200, 64, 10, 64, 3, 1, 0),   # no padding
+    (64, 64, 14, 128, 1, 1, 0),   # 1x1
+    (32, 128, 28, 256, 1, 2, 0),  # 1x1 stride 2
+]
+
+# the short-convolution kernel (conv_ws_k: 32x32 tiles, waves splitting K,
+# S workgroups per tile finished in-kernel): ResNet-18's layers at batch 1
+# (S = 1, 2, 4, 8; 49-pixel images), batch 2 (images straddling tiles),
+# tails in Co and pixels, stride 2, no padding, 1x1, a single tile
+WS_SHAPES = [
+    (1, 64, 56, 64, 3, 1, 1),     # S = 1, five slices per wave
+    (1, 64, 56, 128, 3, 2, 1),    # stride 2, S = 1
+    (1, 128, 28, 128, 3, 1, 1),   # S = 2
+    (1, 256, 14, 256, 3, 1, 1),   # S = 4
+    (1, 512, 7, 512, 3, 1, 1),    # S = 8, K = 4608, 49 pixels (scalar stores)
+    (2, 512, 7, 512, 3, 1, 1),    # two images across one 32-pixel tile
+    (3, 32, 13, 96, 3, 2, 1),     # odd image, pixel tail
+    (3, 64, 19, 198, 3, 1, 1),    # Co % 32 != 0
+    (2, 32, 9, 40, 3, 1, 1),      # second channel tile of 8 rows
     (2, 64, 10, 64, 3, 1, 0),     # no padding
     (4, 64, 14, 128, 1, 1, 0),    # 1x1
     (4, 128, 28, 256, 1, 2, 0),   # 1x1 stride 2
+    (1, 32, 5, 32, 3, 1, 1),      # one tile, 9 slices
 ]
 
 
@@ -173,6 +194,33 @@ def test_conv_packed_shapes(shape, hip, dmem, abi, oracle_lib):
     exp = caserun.run_case(oracle_lib, case, abi)["out"]
     got = caserun.run_case(hip, case, abi, dmem)["out"]
     _check(got, exp, case["name"])
+
+
+@pytest.mark.parametrize("shape", WS_SHAPES, ids=[str(s) for s in WS_SHAPES])
+def test_conv_ws_shapes(shape, hip, dmem, abi, oracle_lib):
+    """conv_ws_k against the oracle, and run again on the same input: bit
+    for bit the same (the split tiles' sums are added in range order
+    whichever workgroup finishes)."""
+    case = _packed_case(np.random.default_rng(37), *shape)
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    _check(got, exp, case["name"])
+    again = caserun.run_case(hip, case, abi, dmem)["out"]
+    assert caserun.same_bits(again, got)
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("bias,res", [(True, True), (False, True), (True, False), (False, False)])
+def test_conv_ws_epilogues(act, bias, res, hip, dmem, abi, oracle_lib):
+    """Each activation, with and without bias and residual, on a whole tile
+    (S = 1) and a split one (S = 8)."""
+    for shape in ((1, 64, 12, 64, 3, 1, 1), (1, 512, 7, 512, 3, 1, 1)):
+        case = _packed_case(np.random.default_rng(43), *shape, act=act, bias=bias, res=res)
+        print(f"case {case['name']}", flush=True)
+        exp = caserun.run_case(oracle_lib, case, abi)["out"]
+        got = caserun.run_case(hip, case, abi, dmem)["out"]
+        _check(got, exp, case["name"])
 
 
 @pytest.mark.parametrize("n,h", [(2, 64), (1, 224), (3, 37), (5, 224), (16, 64)])
@@ -377,7 +425,8 @@ def test_gemm_layouts_and_streamk(shape, hip, dmem, abi, oracle_lib):
 # 2048x1024x256 (128x128 tiles, 128 tiles of 8 slices); and the stem's fused
 # max pool at 10 x 224x224, whose 512 ranges of two or three conv rows
 # finish the pool rows they share with their neighbours in the kernel.
-IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "gemm_512x512x288", "gemm_2048x1024x256", "stem_pool_b10"]
+IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "conv_ws_b1_512c_7", "gemm_512x512x288", "gemm_2048x1024x256",
+                          "stem_pool_b10"]
 
 
 @pytest.mark.parametrize("which", IN_KERNEL_FINISH_CASES)
@@ -391,6 +440,8 @@ def test_in_kernel_finish_alternating_inputs(which, hip, dmem, abi, oracle_lib):
         rng = np.random.default_rng(seed)
         if which == "conv_b8_64c_56":
             return _packed_case(rng, 8, 64, 56, 64, 3, 1, 1)
+        if which == "conv_ws_b1_512c_7":
+            return _packed_case(rng, 1, 512, 7, 512, 3, 1, 1)
         if which == "stem_pool_b10":
             return _conv_maxpool_case(rng, 10, 224, 224, 64, True)
         m, n, k = {"gemm_512x512x288": (512, 512, 288), "gemm_2048x1024x256": (2048, 1024, 256)}[which]
