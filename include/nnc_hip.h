@@ -281,6 +281,26 @@ void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis);
  * then 1531-1581 nnc_transpose). */
 void nnc_hip_transpose_slice(Tensor* in, Tensor* out, int64_t* perm, int ndim, int col0, int width);
 
+/* nnc_hip_attention: a transformer layer's attention block in one kernel.
+ * qkv holds batch * seq rows of ld = qkv.shape[-1] floats (the fused QKV
+ * projection's output); head h of Q is columns q_col + h * head_dim ..
+ * + head_dim of a batch's seq rows, K and V likewise from k_col and v_col.
+ * For every batch b and head h: out[b * seq + i][h * head_dim + d] =
+ * sum_j P[i][j] V[j][d], P = softmax over j of (Q K^T)[i][j] / div[0] - the
+ * context in the merged-head layout the output projection reads, out of
+ * batch * seq rows of heads * head_dim floats. Float32; div one element;
+ * head_dim 32 or 64; seq a multiple of 32 up to 128; qkv rows, ld and the
+ * three column offsets 16-byte aligned (NNC_HIP_EUNSUPP otherwise). fp32
+ * MFMA products and the hardware exponential: within 1e-4 abs / 1e-3 rel of
+ * the calls it replaces. Emitted by the mi355x target's O3 pass for the
+ * head split (nnc_hip_transpose_slice of the QKV projection), Q K^T, the
+ * scaled softmax, the product with V and the head merge. No counterpart in
+ * the reference ABI (runtime/x86/ops.c:2183-2251 nnc_split, 1531-1581
+ * nnc_transpose, 1607-1730 nnc_matmul, 82-224 nnc_div, 260-310 nnc_softmax;
+ * tests/__snapshots__/test_snapshots_simple_transformer.ambr:114-216). */
+void nnc_hip_attention(Tensor* qkv, Tensor* div, Tensor* out, int batch, int seq, int heads, int head_dim, int q_col,
+                       int k_col, int v_col);
+
 /* nnc_hip_conv_packed_noalloc: nnc_hip_conv_packed for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference ABI.
@@ -288,9 +308,12 @@ void nnc_hip_transpose_slice(Tensor* in, Tensor* out, int64_t* perm, int ndim, i
  * but it allocates nothing: its stream-K partial tiles and tile counters
  * live in a static device array of 64 MiB + 16384 counters that each GPU
  * holds until the process ends; a shape needing more fails with
- * NNC_HIP_EUNSUPP before any launch. Calls that overlap on one GPU (other
- * threads, other streams) share that array and race. The calling thread must
- * have its library state already (nnc_hip_init on that thread, or any
+ * NNC_HIP_EUNSUPP before any launch. Calls on one GPU share that array, so
+ * they are ordered on the device: each call's stream first waits for the
+ * previous call's work (an event recorded after every call, whatever thread
+ * or stream made it); inside a graph capture the captured calls are ordered
+ * by the graph, and a replay is not ordered against calls made outside it.
+ * The calling thread must have its library state already (nnc_hip_init on that thread, or any
  * earlier nnc_* call there): NNC_HIP_ESTATE otherwise. */
 void nnc_hip_conv_packed_noalloc(Tensor* in, Tensor* w, Tensor* b, Tensor* res, Tensor* out, int kh, int kw,
                                  int sh, int sw, int ph, int pw, int act);

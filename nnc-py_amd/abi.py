@@ -128,6 +128,7 @@ TARGET_SIGNATURES = {
     "nnc_hip_fused_eltwise": [TPP, c_int, I32P, c_int, F32P, TP],
     "nnc_hip_add_layernorm": [TP, TP, TP, TP, TP, c_int, c_float],
     "nnc_hip_scaled_softmax": [TP, TP, TP, c_int],
+    "nnc_hip_attention": [TP, TP, TP, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
     "nnc_hip_transpose_slice": [TP, TP, I64P, c_int, c_int, c_int],
 }
 

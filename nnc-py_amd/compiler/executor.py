@@ -26,7 +26,7 @@ from .passes import (SPILL_OPS, Branch, MemoryPlan, branch_calls, check_plan, el
                      eliminate_identity, find_branches, fit_memory, fuse_matmul_bias, fuse_patterns, fuse_projection,
                      fuse_residual, pack_conv_weights, plan_memory, prepack_lowering, stream_tiles,
                      eliminate_concat_split, fuse_eltwise_chains, compose_transposes, fuse_add_layernorm,
-                     fuse_scaled_softmax, fuse_split_transposes)
+                     fuse_scaled_softmax, fuse_split_transposes, fuse_attention)
 
 
 @dataclass
@@ -64,6 +64,9 @@ ELTWISE_FUSION = True
 # overlapped 1x1 convolution slows from 10.8 to 14.2 us and the cross-stream
 # edges of the captured graph cost more than the overlap saves.
 BRANCH_STREAMS = False
+# At O3 (mi355x target) a transformer layer's attention block becomes one
+# nnc_hip_attention call (passes.fuse_attention).
+ATTENTION_FUSION = True
 BRANCH_MAX_FLOPS = 1e9
 
 
@@ -101,6 +104,8 @@ def build_program(graph: Graph, opt_level: int = 1, memory_strategy: str | None 
             fuse_split_transposes(graph)
             fuse_add_layernorm(graph)
             fuse_scaled_softmax(graph)
+            if ATTENTION_FUSION:
+                fuse_attention(graph)
             fuse_eltwise_chains(graph)
     order = graph.topological_sort()
     branches = find_branches(graph, order, BRANCH_MAX_FLOPS) if use_branches else []

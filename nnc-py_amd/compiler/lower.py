@@ -191,6 +191,11 @@ def lower_node(g: Graph, node: Node) -> Call:
         return Call("nnc_hip_transpose_slice", [_t(ins[0]), _t(outs[0]), ("i64", perm), ("i", len(perm)),
                                                 ("i", int(node.attrs["col0"])), ("i", int(node.attrs["width"]))],
                     node.name)
+    if op == "Attention":  # a transformer layer's attention block in one kernel (include/nnc_hip.h)
+        a = node.attrs
+        return Call("nnc_hip_attention", [_t(ins[0]), _t(ins[1]), _t(outs[0])]
+                    + [("i", int(a[k])) for k in ("batch", "seq", "heads", "head_dim", "q_col", "k_col", "v_col")],
+                    node.name)
     if op == "ScaledSoftmax":  # Div by one element + softmax in one pass (include/nnc_hip.h)
         return Call("nnc_hip_scaled_softmax", [_t(ins[0]), _t(ins[1]), _t(outs[0]),
                                                ("i", int(node.attrs.get("axis", -1)))], node.name)

@@ -678,6 +678,96 @@ def fuse_split_transposes(g: Graph) -> int:
     return fused
 
 
+ATTENTION_HEAD_DIMS = (32, 64)
+ATTENTION_MAX_SEQ = 128
+
+
+def _only_reader(g: Graph, tensor: str, op_type: str, index: int | None = 0):
+    """The one node reading `tensor` (no graph output), if it is an
+    `op_type` reading it at input `index` (any input if None)."""
+    if tensor in g.outputs:
+        return None
+    users = g.consumers(tensor)
+    if len(users) != 1 or users[0].op_type != op_type:
+        return None
+    if index is not None and (len(users[0].inputs) <= index or users[0].inputs[index] != tensor):
+        return None
+    return users[0]
+
+
+def fuse_attention(g: Graph) -> int:
+    """A transformer layer's attention block - after fuse_split_transposes,
+    compose_transposes and fuse_scaled_softmax: SliceTranspose Q (perm
+    0,2,1,3) and K^T (perm 0,2,3,1) of one QKV tensor into a MatMul, a
+    ScaledSoftmax of its scores over the last axis, a MatMul with
+    SliceTranspose V (perm 0,2,1,3), and the head merge Transpose (perm
+    0,2,1,3), each intermediate read only by the next node - becomes one
+    Attention node (inputs: the QKV tensor, the divisor; attrs batch, seq,
+    heads, head_dim, q_col, k_col, v_col), lowered to nnc_hip_attention.
+    Taken for float32, head_dim in ATTENTION_HEAD_DIMS, seq a multiple of 32
+    up to ATTENTION_MAX_SEQ, QKV rows and column offsets multiples of four
+    floats; the intermediates (scores, probabilities, per-head Q, K^T, V and
+    context) never reach HBM."""
+    fused = 0
+    for mm1 in list(g.nodes):
+        if mm1.op_type != "MatMul" or len(mm1.inputs) != 2:
+            continue
+        tq, tk = (g.producer(i) for i in mm1.inputs)
+        if tq is None or tk is None or tq.op_type != "SliceTranspose" or tk.op_type != "SliceTranspose":
+            continue
+        if tq.inputs[0] != tk.inputs[0] or [int(v) for v in tq.attrs["perm"]] != [0, 2, 1, 3] or \
+                [int(v) for v in tk.attrs["perm"]] != [0, 2, 3, 1]:
+            continue
+        if _only_reader(g, tq.outputs[0], "MatMul", 0) is not mm1 or _only_reader(g, tk.outputs[0], "MatMul", 1) is not mm1:
+            continue
+        sm = _only_reader(g, mm1.outputs[0], "ScaledSoftmax")
+        if sm is None or int(sm.attrs.get("axis", -1)) not in (-1, 3):
+            continue
+        mm2 = _only_reader(g, sm.outputs[0], "MatMul", 0)
+        if mm2 is None:
+            continue
+        tv = g.producer(mm2.inputs[1])
+        if tv is None or tv.op_type != "SliceTranspose" or tv.inputs[0] != tq.inputs[0] or \
+                [int(v) for v in tv.attrs["perm"]] != [0, 2, 1, 3] or \
+                _only_reader(g, tv.outputs[0], "MatMul", 1) is not mm2:
+            continue
+        tr = _only_reader(g, mm2.outputs[0], "Transpose")
+        if tr is None or [int(v) for v in (tr.attrs.get("perm") or [])] != [0, 2, 1, 3]:
+            continue
+        qkv = g.tensors[tq.inputs[0]]
+        qt = g.tensors[tq.outputs[0]]
+        if len(qt.shape) != 4 or any(g.tensors[t].dtype != "float32"
+                                     for t in (tq.inputs[0], sm.inputs[1], tr.outputs[0])):
+            continue
+        batch, heads, seq, dh = (int(v) for v in qt.shape)
+        width = int(qkv.shape[-1])
+        if g.tensors[sm.inputs[1]].numel != 1 or qkv.numel != batch * seq * width:
+            continue
+        if dh not in ATTENTION_HEAD_DIMS or seq % 32 or seq > ATTENTION_MAX_SEQ or width % 4:
+            continue
+        cols = [int(t.attrs["col0"]) for t in (tq, tk, tv)]
+        if any(c % 4 or int(t.attrs["width"]) != heads * dh for c, t in zip(cols, (tq, tk, tv))):
+            continue
+        if list(g.tensors[tk.outputs[0]].shape) != [batch, heads, dh, seq] or \
+                list(g.tensors[tv.outputs[0]].shape) != [batch, heads, seq, dh]:
+            continue
+        dead = [tq, tk, tv, mm1, sm, mm2]
+        mids = [tq.outputs[0], tk.outputs[0], tv.outputs[0], mm1.outputs[0], sm.outputs[0], mm2.outputs[0]]
+        tr.op_type = "Attention"
+        tr.inputs = [tq.inputs[0], sm.inputs[1]]
+        tr.attrs = {"batch": batch, "seq": seq, "heads": heads, "head_dim": dh,
+                    "q_col": cols[0], "k_col": cols[1], "v_col": cols[2]}
+        tr.metadata["fused_from"] = [n.name for n in dead] + [tr.name]
+        tr.metadata["tile_stream"] = {"intermediate": mids,
+                                      "hbm_bytes_saved": 2 * sum(g.tensors[t].nbytes for t in mids)}
+        for n in dead:
+            g.nodes.remove(n)
+        for t in mids:
+            g.tensors.pop(t, None)
+        fused += 1
+    return fused
+
+
 def compose_transposes(g: Graph) -> int:
     """A Transpose whose input is another Transpose's output read by nothing
     else (and no graph output) becomes one Transpose of the first's input

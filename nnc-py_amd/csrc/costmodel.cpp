@@ -315,6 +315,20 @@ void gemm(const char* op, int M, int N, int K, int batches, bool a_kc, bool b_kc
                kLaunchUs + 0.5 + chain_us + b / (kHbm * kStreamEff) * 1e6, flops, b);
         return;
     }
+    {
+        // gemm.hip gemm_ws_k (plan_gemm_ws): k-contiguous operands need K % 4
+        // == 0 (16-byte rows), x-contiguous ones take any layout
+        nnc::WsPlan p;
+        if ((!a_kc || K % 4 == 0) && (!b_kc || K % 4 == 0) && nnc::plan_gemm_ws(M, N, K, batches, p)) {
+            char name[48];
+            snprintf(name, sizeof name, "gemm_ws_32x32_%s%s", a_kc ? "k4" : "x1", b_kc ? "k4" : "x1");
+            const int r = (int)ceil_div(p.tiles * p.S, kCUs);  // workgroups sharing a CU
+            double us = kLaunchUs + r * p.NS * kWsSliceUs + kColdUsPerMB * b_bytes * 1e-6;
+            if (p.S > 1) us += kWsFinishUs + kWsFinishUsPerPart * p.S;
+            record(op, name, fmax(us, kLaunchUs + bytes / (kHbm * kStreamEff) * 1e6), flops, bytes);
+            return;
+        }
+    }
     const bool a4 = a_kc ? K % 4 == 0 : M % 4 == 0;  // 16-byte loads along the contiguous axis
     const bool b4 = b_kc ? K % 4 == 0 : N % 4 == 0;
     const bool big = (int64_t)M * N * batches >= (int64_t)128 * 128 * 2 * kCUs / 4 && M >= 128 && N >= 128;
@@ -713,6 +727,19 @@ void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis) {
     (void)axis;
     if (in && div && out && numel(out) > 0)
         stream_kernel("nnc_hip_scaled_softmax", "nnc_hip_scaled_softmax", nbytes(in) + nbytes(out), 0.40);
+}
+// attention.hip nnc_hip_attention: one workgroup per (batch, head, 32 query
+// rows) on its own CU, staging Q, K and V and running two MFMA products;
+// the body fitted to the transformer encoder at batch 8, sequence 128
+constexpr double kAttnBodyUs = 4.3;
+void nnc_hip_attention(Tensor* qkv, Tensor* div, Tensor* out, int batch, int seq, int heads, int head_dim, int q_col,
+                       int k_col, int v_col) {
+    (void)q_col, (void)k_col, (void)v_col;
+    if (!qkv || !div || !out || batch <= 0 || seq <= 0 || heads <= 0) return;
+    const int64_t blocks = (int64_t)batch * heads * ((seq + 31) / 32);
+    const double flops = 4.0 * batch * heads * (double)seq * seq * head_dim;
+    record("nnc_hip_attention", "nnc_hip_attention", kLaunchUs + kAttnBodyUs * ceil_div(blocks, kCUs), flops,
+           nbytes(qkv) + nbytes(out));
 }
 // eltwise.hip nnc_hip_fused_eltwise: one streaming pass, each input read and
 // the output written once

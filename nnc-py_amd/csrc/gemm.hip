@@ -833,6 +833,145 @@ static void dispatch_b_small(GemmArgs& g, int bkind, int batches, const char* na
     }
 }
 
+// ---------------------------------------------------------------------------
+// Short GEMMs: gemm_ws_k, the GEMM form of conv.hip's conv_ws_k. A
+// workgroup owns one 32 x 32 output tile of one batch over a contiguous
+// range of K slices; its four waves split the range (wave w takes slices w,
+// w + 4, ...), each computing the whole tile with v_mfma_f32_32x32x2_f32, and
+// the four sums are added through LDS in wave order. Operands go straight
+// into the MFMA operand registers: lane half h takes k = 16h .. 16h + 15 of
+// each 32-wide slice, so a k-contiguous operand row is four 16-byte loads
+// per slice and an x-contiguous one sixteen 4-byte loads coalesced across
+// the lanes' rows. All of a wave's slices (NS) are loaded before its first
+// MFMA. A tile split over S workgroups is finished in the kernel by the last
+// to arrive (store_partial4 / finish_arrive / load_partial4, the stream-K
+// protocol of mfma_tile.h), the partials added in range order. Epilogue as
+// gemm_finish.
+// ---------------------------------------------------------------------------
+typedef unsigned int gws_u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NS, bool A_KC, bool B_KC>
+__global__ void __launch_bounds__(256, 2) gemm_ws_k(GemmArgs g, int S, int iters, int tiles) {
+    __shared__ __align__(16) float red[4][32 * 32];
+    const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int part = blockIdx.x % S, rest = blockIdx.x / S;
+    const int t = rest % tiles, batch = rest / tiles;
+    const int i0 = (t % g.tiles_m) * 32, j0 = (t / g.tiles_m) * 32;
+    const int kb = (int)((int64_t)part * iters / S), ke = (int)((int64_t)(part + 1) * iters / S);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A + batch * g.sa), rb = make_rsrc(g.B + batch * g.sb);
+    const int i = i0 + l32, j = j0 + l32;
+    const bool iok = i < g.M, jok = j < g.N;
+    const int lda = (int)g.lda, ldb = (int)g.ldb;
+
+    float av[NS][16], bv[NS][16];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const int sl = kb + wave + 4 * q;  // wave-uniform
+        const bool on = sl < ke;
+        const int k0 = sl * 32 + 16 * h;
+        if constexpr (A_KC) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool ok = on && iok && k0 + 4 * u < g.K;
+                const f32x4 v = load_f32x4(ra, ok ? (uint32_t)(i * lda + k0 + 4 * u) * 4u : kOutOfRange);
+                av[q][4 * u] = v[0], av[q][4 * u + 1] = v[1], av[q][4 * u + 2] = v[2], av[q][4 * u + 3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const bool ok = on && iok && k0 + c < g.K;
+                av[q][c] = load_f32(ra, ok ? (uint32_t)((k0 + c) * lda + i) * 4u : kOutOfRange);
+            }
+        }
+        if constexpr (B_KC) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool ok = on && jok && k0 + 4 * u < g.K;
+                const f32x4 v = load_f32x4(rb, ok ? (uint32_t)(j * ldb + k0 + 4 * u) * 4u : kOutOfRange);
+                bv[q][4 * u] = v[0], bv[q][4 * u + 1] = v[1], bv[q][4 * u + 2] = v[2], bv[q][4 * u + 3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const bool ok = on && jok && k0 + c < g.K;
+                bv[q][c] = load_f32(rb, ok ? (uint32_t)((k0 + c) * ldb + j) * 4u : kOutOfRange);
+            }
+        }
+    }
+    // every load above is issued before the first MFMA (a wave with fewer
+    // slices multiplies zeros in its last one: straight-line code)
+    __builtin_amdgcn_sched_barrier(0);
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int q = 0; q < NS; ++q)
+#pragma unroll
+        for (int c = 0; c < 16; ++c) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][c], bv[q][c], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float x = acc[r];  // (element copied first: see store_tile)
+        red[wave][(8 * (r >> 2) + 4 * h + (r & 3)) * 32 + l32] = x;
+    }
+    __syncthreads();
+    const int row = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
+    f32x4 v = *reinterpret_cast<const f32x4*>(&red[0][row * 32 + c4]);
+#pragma unroll
+    for (int w = 1; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(&red[w][row * 32 + c4]);
+    if (S > 1) {
+        const __amdgpu_buffer_rsrc_t rws = make_rsrc(g.ws);
+        const uint32_t slot = (uint32_t)rest * (uint32_t)S * 4096u + threadIdx.x * 16u;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gws_u32x4, v), rws,
+                                               (int)(slot + (uint32_t)part * 4096u), 0, kDeviceScope);
+        if (!finish_arrive(g.cnt + rest, S - 1)) return;  // uniform
+        f32x4 p[kWsMaxSplit];
+#pragma unroll
+        for (int q = 0; q < kWsMaxSplit; ++q)
+            p[q] = load_partial4(rws, q < S && q != part ? slot + (uint32_t)q * 4096u : kOutOfRange);
+        f32x4 sum = part == 0 ? v : p[0];
+#pragma unroll
+        for (int q = 1; q < kWsMaxSplit; ++q)
+            if (q < S) sum += q == part ? v : p[q];
+        v = sum;
+    }
+    const int oi = i0 + row;
+    if (oi >= g.M) return;
+    float* o = g.out + batch * g.so + (int64_t)oi * g.N;
+    // The C row is chosen once (C[j] or C[oi*N + j]) rather than per element
+    // through gemm_finish: with the per-element form, hipcc 7.2 addressed
+    // elements 1..3 of a bias row (c_mode 1) at C + oi*N, past the end of C.
+    const float* crow = g.C + (g.c_mode == 2 ? (int64_t)oi * g.N : (int64_t)0);
+    const bool has_c = g.c_mode != 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int oj = j0 + c4 + e;
+        if (oj < g.N) {
+            float x = g.alpha * v[e];
+            if (has_c) x += g.beta * crow[oj];
+            if (g.relu) x = x > 0.0f ? x : 0.0f;
+            o[oj] = x;
+        }
+    }
+}
+
+template <int NS, bool A_KC, bool B_KC>
+static void launch_gws_ns(const GemmArgs& g, int S, int iters, int tiles, unsigned grid, const char* kname) {
+    launch(kname, gemm_ws_k<NS, A_KC, B_KC>, dim3(grid), dim3(256), 0, g, S, iters, tiles);
+}
+
+template <bool A_KC, bool B_KC>
+static void launch_gws(const GemmArgs& g, int NS, int S, int iters, int tiles, unsigned grid, const char* kname) {
+    switch (NS) {
+        case 1: return launch_gws_ns<1, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
+        case 2: return launch_gws_ns<2, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
+        case 3: return launch_gws_ns<3, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
+        case 4: return launch_gws_ns<4, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
+        case 5: return launch_gws_ns<5, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
+        default: return launch_gws_ns<6, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
+    }
+}
+
 // Describe operands as: A element (i, k) = A[i*lda + k] if a_kc else A[k*lda + i];
 // B element (k, j) = B[j*ldb + k] if b_kc else B[k*ldb + j].
 struct GemmProblem {
@@ -920,6 +1059,44 @@ static void gemm_run(const GemmProblem& p, const char* name) {
         if (p.M <= 16) launch("gemm_skinny_nt_16", gemm_skinny_nt_k<1>, grid, block, 0, g);
         else launch("gemm_skinny_nt_32", gemm_skinny_nt_k<2>, grid, block, 0, g);
         return;
+    }
+    // short products: gemm_ws_k, where plan_gemm_ws takes them and each
+    // operand is either k-contiguous with 16-byte rows (and K % 4 == 0) or
+    // x-contiguous, one batch of each below 2 GiB (32-bit buffer offsets)
+    {
+        WsPlan wp;
+        const bool a_kc4 = p.a_kc && aligned16(p.A) && p.lda % 4 == 0 && p.sa % 4 == 0 && p.K % 4 == 0;
+        const bool b_kc4 = p.b_kc && aligned16(p.B) && p.ldb % 4 == 0 && p.sb % 4 == 0 && p.K % 4 == 0;
+        const int64_t a_elems = p.a_kc ? (int64_t)p.M * p.lda : (int64_t)p.K * p.lda;
+        const int64_t b_elems = p.b_kc ? (int64_t)p.N * p.ldb : (int64_t)p.K * p.ldb;
+        if ((a_kc4 || !p.a_kc) && (b_kc4 || !p.b_kc) && a_elems * 4 < ((int64_t)1 << 31) &&
+            b_elems * 4 < ((int64_t)1 << 31) && plan_gemm_ws(p.M, p.N, p.K, p.batches, wp)) {
+            g.tiles_m = (int)ceil_div(p.M, 32);
+            g.tiles_n = (int)ceil_div(p.N, 32);
+            const int tiles = g.tiles_m * g.tiles_n;
+            bool ok = true;
+            if (wp.S > 1) {
+                g.ws = workspace((size_t)wp.tiles * wp.S * 4096);
+                g.cnt = g.ws ? tile_counters((size_t)wp.tiles) : nullptr;
+                ok = g.cnt != nullptr;
+                if (ok && ts().fixed)
+                    launch("zero_tile_counters", gemm_zero_counters_k, dim3((unsigned)ceil_div(wp.tiles, 256)),
+                           dim3(256), 0, g.cnt, (int)wp.tiles);
+            }
+            if (ok) {
+                char kname[48];
+                snprintf(kname, sizeof kname, "gemm_ws_32x32_%s%s", p.a_kc ? "k4" : "x1", p.b_kc ? "k4" : "x1");
+                set_work(2.0 * p.M * (double)p.N * p.K * p.batches, 0.0);
+                const unsigned grid = (unsigned)(wp.tiles * wp.S);
+                if (p.a_kc && p.b_kc) launch_gws<true, true>(g, wp.NS, wp.S, wp.iters, tiles, grid, kname);
+                else if (p.a_kc) launch_gws<true, false>(g, wp.NS, wp.S, wp.iters, tiles, grid, kname);
+                else if (p.b_kc) launch_gws<false, true>(g, wp.NS, wp.S, wp.iters, tiles, grid, kname);
+                else launch_gws<false, false>(g, wp.NS, wp.S, wp.iters, tiles, grid, kname);
+                return;
+            }
+            g.ws = nullptr;
+            g.cnt = nullptr;
+        }
     }
     // MFMA tiles address each operand tile with 32-bit byte offsets from the
     // tile origin: at most 128 rows of lda (k-contiguous) or K rows of lda

@@ -135,6 +135,28 @@ inline bool plan_ws(int64_t Co, int64_t Npix, int64_t K, WsPlan& p) {
     return true;
 }
 
+// Short GEMMs (gemm.hip gemm_ws_k, the GEMM form of conv_ws_k): products of
+// at most kGwsMaxFlops (a transformer encoder's projections and FFN at batch
+// 8, sequence 128; batched attention-sized MatMuls), on 32 x 32 tiles of every
+// batch with the same split rule.
+constexpr double kGwsMaxFlops = 1e9;
+
+inline bool plan_gemm_ws(int64_t M, int64_t N, int64_t K, int64_t batches, WsPlan& p) {
+    if (M <= 0 || N <= 0 || K <= 0 || batches <= 0) return false;
+    if (2.0 * M * (double)N * K * batches > kGwsMaxFlops) return false;
+    p.tiles = ((M + 31) / 32) * ((N + 31) / 32) * batches;
+    p.iters = (int)((K + 31) / 32);
+    int S = 1;
+    while (S < kWsMaxSplit && (p.iters + S - 1) / S > 4 * kWsMaxSlices) S *= 2;
+    if (S > 1)
+        while (S < kWsMaxSplit && p.tiles * 2 * S <= kWsGroups && p.iters / (2 * S) >= 8) S *= 2;
+    const int per = (p.iters + S - 1) / S;
+    if (per > 4 * kWsMaxSlices || p.tiles * S >= ((int64_t)1 << 31)) return false;
+    p.S = S;
+    p.NS = (per + 3) / 4;
+    return true;
+}
+
 // Fixup cost in slice times of a BM x BN tile: about one slice for 128x128
 // tiles, scaled by tile area for smaller tiles (shorter slices).
 constexpr int fixup_slices_for(int bm, int bn) { return (128 * 128) / (bm * bn); }

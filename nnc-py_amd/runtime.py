@@ -75,6 +75,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_add_layernorm": (abi.TARGET_SIGNATURES["nnc_hip_add_layernorm"], None),
     "nnc_hip_scaled_softmax": (abi.TARGET_SIGNATURES["nnc_hip_scaled_softmax"], None),
     "nnc_hip_transpose_slice": (abi.TARGET_SIGNATURES["nnc_hip_transpose_slice"], None),
+    "nnc_hip_attention": (abi.TARGET_SIGNATURES["nnc_hip_attention"], None),
 }
 
 

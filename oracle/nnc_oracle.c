@@ -1205,3 +1205,54 @@ void nnc_hip_transpose_slice(Tensor* in, Tensor* out, int64_t* perm, int ndim, i
     nnc_transpose(&t, out, perm, ndim);
     free(tmp);
 }
+
+/* ------------------------------------------------------------------------
+ * nnc_hip_attention (include/nnc_hip.h): target-only, no reference
+ * counterpart. Restated, per batch b and head h, as the calls of the
+ * attention block it replaces on two-dimensional operands (the reference's
+ * batched MatMul stepping, ops.c:1687-1704, is not the model's arithmetic
+ * for more than one batch): the head's Q, K^T and V copied out of the qkv
+ * rows (the Split / Reshape / Transpose copies, ops.c:2183-2251,
+ * 1531-1581), S = nnc_matmul(Q, K^T) (ops.c:1607-1730), nnc_div(S, div)
+ * (ops.c:82-224), nnc_softmax over the keys (ops.c:260-310), C =
+ * nnc_matmul(P, V), and C copied into columns h * dh .. of the batch's rows
+ * of out (the head merge). Pinned against float64 numpy in
+ * tests/test_oracle.py.
+ * ---------------------------------------------------------------------- */
+void nnc_hip_attention(Tensor* qkv, Tensor* div, Tensor* out, int batch, int seq, int heads, int head_dim, int q_col,
+                       int k_col, int v_col) {
+    const int64_t ld = qkv->shape[qkv->ndim - 1], width = (int64_t)heads * head_dim;
+    const int64_t sd = (int64_t)seq * head_dim, ss = (int64_t)seq * seq;
+    float* q = (float*)malloc((size_t)(sd > 0 ? sd : 1) * sizeof(float));
+    float* kt = (float*)malloc((size_t)(sd > 0 ? sd : 1) * sizeof(float));
+    float* v = (float*)malloc((size_t)(sd > 0 ? sd : 1) * sizeof(float));
+    float* s = (float*)malloc((size_t)(ss > 0 ? ss : 1) * sizeof(float));
+    float* s2 = (float*)malloc((size_t)(ss > 0 ? ss : 1) * sizeof(float));
+    float* p = (float*)malloc((size_t)(ss > 0 ? ss : 1) * sizeof(float));
+    float* c = (float*)malloc((size_t)(sd > 0 ? sd : 1) * sizeof(float));
+    int64_t sh_q[2] = {seq, head_dim}, sh_kt[2] = {head_dim, seq}, sh_s[2] = {seq, seq};
+    Tensor tq = {q, NNC_DTYPE_FLOAT32, sh_q, 2, sd * 4}, tkt = {kt, NNC_DTYPE_FLOAT32, sh_kt, 2, sd * 4};
+    Tensor tv = {v, NNC_DTYPE_FLOAT32, sh_q, 2, sd * 4}, tc = {c, NNC_DTYPE_FLOAT32, sh_q, 2, sd * 4};
+    Tensor ts = {s, NNC_DTYPE_FLOAT32, sh_s, 2, ss * 4}, ts2 = {s2, NNC_DTYPE_FLOAT32, sh_s, 2, ss * 4};
+    Tensor tp = {p, NNC_DTYPE_FLOAT32, sh_s, 2, ss * 4};
+    const float* x = (const float*)qkv->data;
+    float* y = (float*)out->data;
+    for (int b = 0; b < batch; ++b)
+        for (int h = 0; h < heads; ++h) {
+            for (int i = 0; i < seq; ++i)
+                for (int d = 0; d < head_dim; ++d) {
+                    const float* row = x + ((int64_t)b * seq + i) * ld + (int64_t)h * head_dim + d;
+                    q[(int64_t)i * head_dim + d] = row[q_col];
+                    kt[(int64_t)d * seq + i] = row[k_col];
+                    v[(int64_t)i * head_dim + d] = row[v_col];
+                }
+            nnc_matmul(&tq, &tkt, &ts);
+            nnc_div(&ts, div, &ts2);
+            nnc_softmax(&ts2, &tp, -1);
+            nnc_matmul(&tp, &tv, &tc);
+            for (int i = 0; i < seq; ++i)
+                for (int d = 0; d < head_dim; ++d)
+                    y[((int64_t)b * seq + i) * width + (int64_t)h * head_dim + d] = c[(int64_t)i * head_dim + d];
+        }
+    free(q), free(kt), free(v), free(s), free(s2), free(p), free(c);
+}

@@ -16,6 +16,8 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+import caserun
+
 GOLDEN = Path(__file__).resolve().parent / "golden" / "snapshot_calls.json"
 
 
@@ -437,6 +439,7 @@ def test_transformer_add_layernorm_and_transposes(pkg, oracle_lib, monkeypatch):
     assert ops.count("nnc_hip_transpose_slice") == 6 and "nnc_split" not in ops
     perms = [c.args[2][1] for c in prog.calls if c.op in ("nnc_transpose", "nnc_hip_transpose_slice")]
     assert perms.count([0, 2, 3, 1]) == 2 and [0, 1, 3, 2] not in perms
+    monkeypatch.setattr(executor, "ATTENTION_FUSION", False)
     assert len(build_program(zoo.transformer_encoder(seed=1), opt_level=3).calls) == 26
     monkeypatch.setattr(executor, "ELTWISE_FUSION", False)
     ref = build_program(zoo.transformer_encoder(**kw), opt_level=3)
@@ -449,3 +452,60 @@ def test_transformer_add_layernorm_and_transposes(pkg, oracle_lib, monkeypatch):
         ex.run()
         outs.append(ex.get(p.graph.outputs[0]))
     assert outs[0].tobytes() == outs[1].tobytes()
+
+
+def test_transformer_attention_fusion(pkg, oracle_lib, monkeypatch):
+    """O3 (mi355x target) on the transformer encoder: each layer's attention
+    block - the head split transposes of Q, K^T and V, Q K^T, the scaled
+    softmax, the product with V and the head merge - becomes one Attention
+    node (nnc_hip_attention) reading the QKV projection's output and
+    writing the merged heads the output projection reads: 26 -> 14 calls at
+    batch 8, sequence 128. On the oracle, with one batch and one head (where
+    the reference's batched MatMul stepping is the model's arithmetic), the
+    output has the bits of the same O3 program without the fusion; with
+    four heads (four attention batches, which the unfused program's
+    reference-stepped MatMul gets wrong) it is within the fp bar of the
+    float64 model.
+    Heads of 16 or sequences that are no multiple of 32 are left alone."""
+    from nnc_py_amd.compiler import Executor, build_program, executor, zoo
+    prog = build_program(zoo.transformer_encoder(seed=1), opt_level=3)
+    ops = [c.op for c in prog.calls]
+    assert len(ops) == 14 and ops.count("nnc_hip_attention") == 2
+    assert not {"nnc_hip_transpose_slice", "nnc_matmul", "nnc_hip_scaled_softmax", "nnc_transpose"} & set(ops)
+    att = next(c for c in prog.calls if c.op == "nnc_hip_attention")
+    assert [a[1] for a in att.args[3:]] == [8, 128, 4, 64, 0, 256, 512]
+    assert att.args[0][1].endswith("qkv/Add_output")
+    out_proj = prog.calls[ops.index("nnc_hip_attention") + 1]
+    # the output projection reads the merged heads through the Reshape's view (same arena offset)
+    assert out_proj.op == "nnc_gemm_nt"
+    assert prog.plan.offsets[out_proj.args[0][1]] == prog.plan.offsets[att.args[2][1]]
+
+    kw = dict(batch=1, seq=32, d_model=64, heads=1, ffn=128, seed=4)
+    fused = build_program(zoo.transformer_encoder(**kw), opt_level=3)
+    assert [c.op for c in fused.calls].count("nnc_hip_attention") == 2
+    monkeypatch.setattr(executor, "ATTENTION_FUSION", False)
+    plain = build_program(zoo.transformer_encoder(**kw), opt_level=3)
+    assert "nnc_hip_attention" not in [c.op for c in plain.calls]
+    monkeypatch.setattr(executor, "ATTENTION_FUSION", True)
+    x = (np.random.default_rng(6).standard_normal((1, 32, 64)) * 0.5).astype(np.float32)
+    outs = []
+    for p in (fused, plain):
+        ex = Executor(p, device=False, lib=oracle_lib)
+        ex.set_input("input", x)
+        ex.run()
+        outs.append(ex.get(p.graph.outputs[0]))
+    assert outs[0].tobytes() == outs[1].tobytes()
+
+    kw = dict(batch=1, seq=64, d_model=128, heads=4, ffn=256, seed=5)
+    multi = build_program(zoo.transformer_encoder(**kw), opt_level=3)
+    assert [c.op for c in multi.calls].count("nnc_hip_attention") == 2
+    x = (np.random.default_rng(7).standard_normal((1, 64, 128)) * 0.5).astype(np.float32)
+    ex = Executor(multi, device=False, lib=oracle_lib)
+    ex.set_input("input", x)
+    ex.run()
+    ref = zoo.transformer_encoder_reference(zoo.transformer_encoder(**kw), x, heads=4)
+    assert caserun.fp_violations(ex.get("output"), ref, 1e-4, 1e-3).size == 0
+
+    for kw in (dict(batch=1, seq=32, d_model=64, heads=4, ffn=64), dict(batch=1, seq=48, d_model=64, heads=1, ffn=64)):
+        ops = [c.op for c in build_program(zoo.transformer_encoder(**kw), opt_level=3).calls]
+        assert "nnc_hip_attention" not in ops and "nnc_matmul" in ops

@@ -406,6 +406,19 @@ GEMM_SHAPES = [
     (17, 333, 1020, 0, 1, False),
     (32, 50, 36, 0, 1, True),
     (3, 40, 1024, 0, 1, True),
+    # products up to 1 GFLOP run on gemm_ws_k (32x32 tiles, waves splitting
+    # K; every layout above that is not skinny or a dot/GEMV); these keep
+    # the other kernels covered: register-staged tiles (A k-contiguous with
+    # K % 4 != 0), direct-to-LDS 64x64 with a K tail of one 16-byte chunk,
+    # and 128x128 with a K tail of 4
+    (300, 200, 777, 0, 1, True),
+    (1024, 1100, 996, 0, 1, True),
+    (2048, 2048, 132, 0, 1, True),
+    # gemm_ws_k: tiles split over 8 workgroups (K = 4096), a split tile with
+    # M and N tails, x-contiguous operands on both sides with a split
+    (256, 256, 4096, 0, 1, True),
+    (100, 70, 3000, 0, 0, False),
+    (96, 160, 2500, 1, 0, True),
 ]
 
 
@@ -418,15 +431,17 @@ def test_gemm_layouts_and_streamk(shape, hip, dmem, abi, oracle_lib):
     _check(got, exp, case["name"])
 
 
-# Shapes whose split tiles are finished inside the direct-to-LDS kernel by
-# the last of their 3-4 workgroups (stream-K plan with 256 or 512 resident
-# workgroups): 64 channels 3x3 over 8 x 56x56 (64x128 tiles, 196 tiles of 18
-# slices), GEMM 512x512x288 (64x64 tiles, 64 tiles of 9 slices) and
-# 2048x1024x256 (128x128 tiles, 128 tiles of 8 slices); and the stem's fused
-# max pool at 10 x 224x224, whose 512 ranges of two or three conv rows
-# finish the pool rows they share with their neighbours in the kernel.
-IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "conv_ws_b1_512c_7", "gemm_512x512x288", "gemm_2048x1024x256",
-                          "stem_pool_b10"]
+# Shapes whose split tiles are finished inside the kernel by the last of
+# their workgroups: 64 channels 3x3 over 8 x 56x56 (direct-to-LDS 64x128
+# tiles, 196 tiles of 18 slices), GEMM 1024x768x1024 (direct-to-LDS 64x64
+# tiles at one workgroup per CU, 192 tiles of 32 slices) and 2048x1024x256
+# (128x128 tiles, 128 tiles of 8 slices); the short-product kernels' tiles
+# split over 8 workgroups (conv 512 channels 3x3 over 7x7, GEMM
+# 256x256x4096); and the stem's fused max pool at 10 x 224x224, whose 512
+# ranges of two or three conv rows finish the pool rows they share with
+# their neighbours in the kernel.
+IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "conv_ws_b1_512c_7", "gemm_1024x768x1024", "gemm_2048x1024x256",
+                          "gemm_ws_256x256x4096", "stem_pool_b10"]
 
 
 @pytest.mark.parametrize("which", IN_KERNEL_FINISH_CASES)
@@ -444,7 +459,8 @@ def test_in_kernel_finish_alternating_inputs(which, hip, dmem, abi, oracle_lib):
             return _packed_case(rng, 1, 512, 7, 512, 3, 1, 1)
         if which == "stem_pool_b10":
             return _conv_maxpool_case(rng, 10, 224, 224, 64, True)
-        m, n, k = {"gemm_512x512x288": (512, 512, 288), "gemm_2048x1024x256": (2048, 1024, 256)}[which]
+        m, n, k = {"gemm_1024x768x1024": (1024, 768, 1024), "gemm_2048x1024x256": (2048, 1024, 256),
+                   "gemm_ws_256x256x4096": (256, 256, 4096)}[which]
         return _gemm_case(rng, m, n, k, 0, 1, True)
     cases = [make(41), make(42)]
     exp = [caserun.run_case(oracle_lib, c, abi)["out"] for c in cases]
@@ -884,4 +900,59 @@ def test_add_layernorm_matches_add_then_layernorm(shape, axis, hip, dmem, abi):
     runtime.clear_error()
     out = caserun.run_case(hip, short, abi, dmem)["out"]
     assert runtime.last_error()[0] == 1 and (out == 7.0).all()
+    runtime.clear_error()
+
+
+ATTENTION_SHAPES = [
+    (8, 128, 4, 64, (0, 256, 512), 8.0, 0),     # the encoder: batch 8, sequence 128, 4 heads of 64
+    (2, 32, 2, 32, (0, 64, 128), 5.65, 0),      # one key wave, heads of 32 (four key groups)
+    (3, 96, 1, 64, (128, 0, 64), -1.5, 4),      # keys past 96 masked, Q after K and V, a wider row
+    (1, 64, 3, 32, (0, 96, 192), 2.0, 0),
+]
+
+
+@pytest.mark.parametrize("shape", ATTENTION_SHAPES, ids=[str(s[:4]) for s in ATTENTION_SHAPES])
+def test_attention_matches_oracle(shape, hip, dmem, abi, oracle_lib):
+    """nnc_hip_attention on the GPU against the oracle's composition (per
+    batch and head: Q K^T, the division, the softmax, the product with V,
+    heads merged) within the fp bar, and the same bits on a second run."""
+    from test_oracle import attention_case
+    batch, seq, heads, dh, cols, d, extra = shape
+    case = attention_case(np.random.default_rng(47), batch, seq, heads, dh, cols, d, extra)
+    print(f"case attention {shape}", flush=True)
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    from nnc_py_amd import runtime
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    _check(got, caserun.run_case(oracle_lib, case, abi)["out"], f"attention {shape}")
+    assert caserun.same_bits(caserun.run_case(hip, case, abi, dmem)["out"], got)
+
+
+def test_attention_rejects(hip, dmem, abi):
+    """Refused before any launch, the output untouched: a sequence that is
+    no multiple of 32 or longer than 128, a head of 48, a column offset
+    that is no multiple of 4 floats, columns past the row, a two-element
+    divisor, an output of the wrong size, int32 qkv."""
+    from nnc_py_amd import runtime
+    from test_oracle import attention_case
+
+    def variant(seq=64, dh=32, cols=(0, 64, 128), div=None, out=None, qkv_dtype=None):
+        c = attention_case(np.random.default_rng(1), 1, seq, 2, dh, cols, 2.0, extra=8)
+        if div is not None:
+            c["tensors"]["d"] = div
+        if out is not None:
+            c["tensors"]["out"] = out
+        if qkv_dtype is not None:
+            c["tensors"]["qkv"] = c["tensors"]["qkv"].astype(qkv_dtype)
+        c["tensors"]["out"] = np.full_like(c["tensors"]["out"], 7.0)
+        return c
+    bad = [("seq 100", variant(seq=100), 4), ("seq 160", variant(seq=160), 4), ("head 48", variant(dh=48), 4),
+           ("column 2", variant(cols=(2, 64, 128)), 4), ("past the row", variant(cols=(0, 64, 140)), 1),
+           ("two-element divisor", variant(div=np.array([2.0, 2.0], np.float32)), 1),
+           ("short output", variant(out=np.zeros((63, 64), np.float32)), 1),
+           ("int32 qkv", variant(qkv_dtype=np.int32), 4)]
+    for why, c, code in bad:
+        runtime.clear_error()
+        out = caserun.run_case(hip, c, abi, dmem)["out"]
+        assert runtime.last_error()[0] == code, (why, runtime.last_error())
+        assert (out == 7.0).all(), why
     runtime.clear_error()

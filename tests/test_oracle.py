@@ -511,3 +511,44 @@ def test_oracle_add_layernorm_composition(shape, axis, oracle_lib, abi):
     inner = int(np.prod(shape[ax + 1:]))
     ref = (x - mean) / np.sqrt(var + 1e-5) * np.repeat(g, inner) + np.repeat(bb, inner)
     np.testing.assert_allclose(got.reshape(ref.shape), ref, rtol=1e-4, atol=1e-5)
+
+
+def attention_f64(qkv, d, batch, seq, heads, dh, q_col, k_col, v_col):
+    """Multi-head attention in float64: softmax(Q K^T / d) V per batch and
+    head, heads merged along the columns."""
+    x = qkv.astype(np.float64).reshape(batch, seq, -1)
+    out = np.zeros((batch, seq, heads * dh))
+    for h in range(heads):
+        q, k, v = (x[:, :, c + h * dh:c + (h + 1) * dh] for c in (q_col, k_col, v_col))
+        s = q @ k.transpose(0, 2, 1) / d
+        e = np.exp(s - s.max(axis=-1, keepdims=True))
+        out[:, :, h * dh:(h + 1) * dh] = (e / e.sum(axis=-1, keepdims=True)) @ v
+    return out.reshape(batch * seq, heads * dh)
+
+
+def attention_case(rng, batch, seq, heads, dh, cols, d, extra=0):
+    """nnc_hip_attention case: qkv rows of 3 * heads * dh (+ extra) floats."""
+    ld = 3 * heads * dh + extra
+    qkv = (rng.standard_normal((batch * seq, ld)) * 0.5).astype(F32)
+    return {"name": "attn", "op": "nnc_hip_attention",
+            "tensors": {"qkv": qkv, "d": np.array([d], F32), "out": np.zeros((batch * seq, heads * dh), F32)},
+            "args": [("t", "qkv"), ("t", "d"), ("t", "out")] + [("i", v) for v in (batch, seq, heads, dh, *cols)],
+            "outputs": ["out"]}
+
+
+@pytest.mark.parametrize("batch,seq,heads,dh,cols,d,extra", [
+    (2, 32, 2, 32, (0, 64, 128), 5.65, 0),      # two batches, two heads
+    (1, 128, 4, 64, (0, 256, 512), 8.0, 0),     # the encoder's head shape
+    (3, 64, 1, 64, (128, 0, 64), -1.5, 4),      # Q after K and V, a negative divisor, a wider row
+])
+def test_oracle_attention_composition(batch, seq, heads, dh, cols, d, extra, oracle_lib, abi):
+    """nnc_hip_attention: per batch and head the oracle's nnc_matmul of Q and
+    K^T, nnc_div, nnc_softmax over the keys and nnc_matmul with V (pinned
+    above) on two-dimensional operands copied out of the qkv rows, merged
+    back by head - within float32 rounding of float64 multi-head attention
+    (a wrong column block, K not transposed, a product instead of the
+    division or a softmax over the queries all fail it)."""
+    case = attention_case(np.random.default_rng(9), batch, seq, heads, dh, cols, d, extra)
+    got = caserun.run_case(oracle_lib, case, abi)["out"]
+    ref = attention_f64(case["tensors"]["qkv"], d, batch, seq, heads, dh, *cols)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
