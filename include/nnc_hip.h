@@ -250,6 +250,15 @@ enum { NNC_EW_ADD = 0, NNC_EW_SUB, NNC_EW_MUL, NNC_EW_DIV, NNC_EW_ADD_RELU, NNC_
        NNC_EW_SIGMOID, NNC_EW_TANH, NNC_EW_CLIP, NNC_EW_OPS };
 void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps, const float* consts, Tensor* out);
 
+/* nnc_hip_ew_chain_specialized: 1 if nnc_hip_fused_eltwise runs this chain
+ * (n_in inputs, prog of n_steps steps as that call takes them) on a kernel
+ * compiled for it - its steps as compile-time code, for the chains the
+ * mi355x O3 compiler emits and a few common short ones - and 0 if it runs on
+ * the general kernel that reads the steps at run time (same results). A
+ * table lookup on the host: no GPU, no device call. No counterpart in the
+ * reference ABI. */
+int nnc_hip_ew_chain_specialized(int n_in, const int* prog, int n_steps);
+
 /* nnc_hip_add_layernorm: out = layernorm(a + b) over dims [axis:] with
  * scale and bias indexed by the axis dimension - a transformer's residual
  * add and the normalisation after it in one pass, the sum never written.

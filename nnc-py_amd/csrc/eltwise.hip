@@ -341,6 +341,131 @@ __global__ void __launch_bounds__(256) fused_eltwise_vec4_k(EwProg p, uint32_t n
     }
 }
 
+// ---------------------------------------------------------------------------
+// Chains known when the library is built, one kernel each: the steps are
+// template arguments, so operands are registers named at compile time and
+// each op is its own straight-line code (the interpreter above spends about
+// 4.6 VALU instructions per element on a five-step chain, enough to make an
+// HBM-bound pass VALU-bound). The table holds the chains the mi355x O3
+// compiler emits for its model set (the bandwidth-chain program's two
+// chains) and a few common short ones; any other chain runs on the
+// interpreter. An empty asm statement after each step keeps the step's
+// result a rounded float that the next step reads, as the op-by-op calls
+// do through memory (no multiply-add contraction across steps).
+// ---------------------------------------------------------------------------
+template <int OP, int X, int Y = X>
+struct EwStep {
+    static constexpr int op = OP, x = X, y = Y;
+};
+
+template <int OP>
+__device__ __forceinline__ float ew_op(float x, float y, float lo, float hi) {
+    if constexpr (OP == NNC_EW_ADD) return binop<kAdd>(x, y);
+    else if constexpr (OP == NNC_EW_SUB) return binop<kSub>(x, y);
+    else if constexpr (OP == NNC_EW_MUL) return binop<kMul>(x, y);
+    else if constexpr (OP == NNC_EW_DIV) return binop<kDiv>(x, y);
+    else if constexpr (OP == NNC_EW_ADD_RELU) return binop<kAddRelu>(x, y);
+    else if constexpr (OP == NNC_EW_ADD_SIGMOID) return binop<kAddSigmoid>(x, y);
+    else if constexpr (OP == NNC_EW_RELU) return unop<kRelu>(x, lo, hi);
+    else if constexpr (OP == NNC_EW_SIGMOID) return unop<kSigmoid>(x, lo, hi);
+    else if constexpr (OP == NNC_EW_TANH) return unop<kTanh>(x, lo, hi);
+    else return unop<kClip>(x, lo, hi);
+}
+
+template <int S>
+__device__ __forceinline__ float4 ew_operand(const float4 (&v)[kEwMaxIn], float4 acc) {
+    if constexpr (S < 0) return acc;
+    else return v[S];
+}
+
+template <class St>
+__device__ __forceinline__ float4 ew_step4(const float4 (&v)[kEwMaxIn], float4 acc, float lo, float hi) {
+    const float4 a = ew_operand<St::x>(v, acc), b = ew_operand<St::y>(v, acc);
+    float4 r = make_float4(ew_op<St::op>(a.x, b.x, lo, hi), ew_op<St::op>(a.y, b.y, lo, hi),
+                           ew_op<St::op>(a.z, b.z, lo, hi), ew_op<St::op>(a.w, b.w, lo, hi));
+    asm volatile("" : "+v"(r.x), "+v"(r.y), "+v"(r.z), "+v"(r.w));
+    return r;
+}
+
+template <bool NT, int NIN, class... Steps>
+__global__ void __launch_bounds__(256) ew_chain_k(EwProg p, uint32_t n4) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t g = blockIdx.x * blockDim.x + threadIdx.x; g < n4; g += stride) {
+        float4 v[kEwMaxIn];
+#pragma unroll
+        for (int i = 0; i < kEwMaxIn; ++i)
+            v[i] = i < NIN ? reinterpret_cast<const float4*>(p.in[i])[g] : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        int s = 0;
+        ((acc = ew_step4<Steps>(v, acc, p.lo[s], p.hi[s]), ++s), ...);
+        store_f4<NT>(p.out + 4 * (size_t)g, acc);
+    }
+}
+
+struct EwChainSpec {
+    int n_in, n_steps;
+    int prog[3 * kEwMaxSteps];  // op, x, y per step; x, y -1: the running value; y = x for unary ops
+    void (*launch)(const char* name, const EwProg& p, uint32_t n4, bool nt);
+};
+
+template <int NIN, class... Steps>
+static void launch_ew_chain(const char* name, const EwProg& p, uint32_t n4, bool nt) {
+    if (nt) launch(name, ew_chain_k<true, NIN, Steps...>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
+    else launch(name, ew_chain_k<false, NIN, Steps...>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
+}
+
+template <int NIN, class... Steps>
+static EwChainSpec ew_chain_spec() {
+    static_assert(sizeof...(Steps) >= 1 && sizeof...(Steps) <= kEwMaxSteps, "1 to kEwMaxSteps steps");
+    static_assert(NIN >= 1 && NIN <= kEwMaxIn, "1 to kEwMaxIn inputs");
+    EwChainSpec s{NIN, (int)sizeof...(Steps), {}, &launch_ew_chain<NIN, Steps...>};
+    const int ops[] = {Steps::op...}, xs[] = {Steps::x...}, ys[] = {Steps::y...};
+    for (int i = 0; i < s.n_steps; ++i) {
+        s.prog[3 * i] = ops[i];
+        s.prog[3 * i + 1] = xs[i];
+        s.prog[3 * i + 2] = ys[i];
+    }
+    return s;
+}
+
+// the specialised chains
+static const EwChainSpec* ew_chain_table(int* count) {
+    typedef EwStep<NNC_EW_ADD_RELU, 0, 1> AddRelu01;
+    static const EwChainSpec table[] = {
+        // bandwidth-chain program: relu(x + y) * x, clip(-6, 6), sigmoid, + t
+        ew_chain_spec<3, AddRelu01, EwStep<NNC_EW_MUL, -1, 0>, EwStep<NNC_EW_CLIP, -1>, EwStep<NNC_EW_SIGMOID, -1>,
+                      EwStep<NNC_EW_ADD, -1, 2>>(),
+        // bandwidth-chain program: tanh(x - y)
+        ew_chain_spec<2, EwStep<NNC_EW_SUB, 0, 1>, EwStep<NNC_EW_TANH, -1>>(),
+        // x * y + z, (x + y) * z, relu(x * y), sigmoid(x + y) * y
+        ew_chain_spec<3, EwStep<NNC_EW_MUL, 0, 1>, EwStep<NNC_EW_ADD, -1, 2>>(),
+        ew_chain_spec<3, EwStep<NNC_EW_ADD, 0, 1>, EwStep<NNC_EW_MUL, -1, 2>>(),
+        ew_chain_spec<2, EwStep<NNC_EW_MUL, 0, 1>, EwStep<NNC_EW_RELU, -1>>(),
+        ew_chain_spec<2, EwStep<NNC_EW_ADD_SIGMOID, 0, 1>, EwStep<NNC_EW_MUL, -1, 1>>(),
+    };
+    *count = (int)(sizeof table / sizeof table[0]);
+    return table;
+}
+
+// The table entry for a chain (prog as nnc_hip_fused_eltwise takes it), or
+// null: same input count, steps, ops and operands (a unary step's y is not
+// compared)
+static const EwChainSpec* ew_chain_find(int n_in, const int* prog, int n_steps) {
+    int count = 0;
+    const EwChainSpec* t = ew_chain_table(&count);
+    for (int c = 0; c < count; ++c) {
+        if (t[c].n_in != n_in || t[c].n_steps != n_steps) continue;
+        bool same = true;
+        for (int s = 0; s < n_steps && same; ++s) {
+            const int op = prog[3 * s];
+            same = op == t[c].prog[3 * s] && prog[3 * s + 1] == t[c].prog[3 * s + 1] &&
+                   (op > NNC_EW_ADD_SIGMOID || prog[3 * s + 2] == t[c].prog[3 * s + 2]);
+        }
+        if (same) return &t[c];
+    }
+    return nullptr;
+}
+
 __global__ void __launch_bounds__(256) fused_eltwise_scalar_k(EwProg p, uint32_t begin, uint32_t n) {
     const uint32_t stride = gridDim.x * blockDim.x;
     for (uint32_t i = begin + blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
@@ -486,7 +611,9 @@ void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps,
     uint32_t done = 0;
     if (vec && n >= 4) {
         const uint32_t n4 = (uint32_t)(n / 4);
-        if (4 * n >= kNtStoreBytes)
+        if (const EwChainSpec* spec = ew_chain_find(n_in, prog, n_steps))
+            spec->launch(name, p, n4, 4 * n >= kNtStoreBytes);
+        else if (4 * n >= kNtStoreBytes)
             launch(name, fused_eltwise_vec4_k<true>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
         else
             launch(name, fused_eltwise_vec4_k<false>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
@@ -494,6 +621,11 @@ void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps,
     }
     if (done < n)
         launch(name, fused_eltwise_scalar_k, dim3(grid_for(n - done, 4)), dim3(256), 0, p, done, (uint32_t)n);
+}
+
+int nnc_hip_ew_chain_specialized(int n_in, const int* prog, int n_steps) {
+    if (!prog || n_in < 1 || n_in > kEwMaxIn || n_steps < 1 || n_steps > kEwMaxSteps) return 0;
+    return ew_chain_find(n_in, prog, n_steps) ? 1 : 0;
 }
 
 void nnc_greater(Tensor* a, Tensor* b, Tensor* out) {

@@ -76,6 +76,7 @@ _HIP_SIGNATURES = {
     "nnc_hip_scaled_softmax": (abi.TARGET_SIGNATURES["nnc_hip_scaled_softmax"], None),
     "nnc_hip_transpose_slice": (abi.TARGET_SIGNATURES["nnc_hip_transpose_slice"], None),
     "nnc_hip_attention": (abi.TARGET_SIGNATURES["nnc_hip_attention"], None),
+    "nnc_hip_ew_chain_specialized": ([ctypes.c_int, abi.I32P, ctypes.c_int], ctypes.c_int),
 }
 
 

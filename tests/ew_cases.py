@@ -23,7 +23,18 @@ EW_PROGRAMS = [
     (4, [("DIV", 0, 1), ("ADD_SIGMOID", -1, 2), ("SUB", 3, -1), ("RELU", -1, -1), ("MUL", -1, -1),
          ("CLIP", -1, -1, -0.5, 0.75), ("ADD", 2, -1), ("TANH", -1, -1)]),
     (1, [("RELU", 0, 0), ("SIGMOID", -1, -1)]),
+    # the library's other compiled chains: x * y + z (a multiply then an add:
+    # no contraction into one rounding), (x + y) * z, relu(x * y),
+    # sigmoid(x + y) * y
+    (3, [("MUL", 0, 1), ("ADD", -1, 2)]),
+    (3, [("ADD", 0, 1), ("MUL", -1, 2)]),
+    (2, [("MUL", 0, 1), ("RELU", -1, -1)]),
+    (2, [("ADD_SIGMOID", 0, 1), ("MUL", -1, 1)]),
 ]
+
+# programs with a kernel compiled for them in the library (the rest run on
+# the general kernel)
+EW_SPECIALIZED = [0, 1, 4, 5, 6, 7]
 
 
 def ew_arrays(n_in: int, n: int, seed: int) -> list[np.ndarray]:

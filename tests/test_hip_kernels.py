@@ -704,7 +704,7 @@ def test_conv_maxpool_rejections(hip, dmem, abi):
 
 
 @pytest.mark.parametrize("n", [4099, 1 << 20])
-@pytest.mark.parametrize("prog", range(4))
+@pytest.mark.parametrize("prog", range(8))
 def test_fused_eltwise_matches_op_by_op(prog, n, hip, dmem, abi, oracle_lib):
     """nnc_hip_fused_eltwise against the same program run as single GPU
     calls through temporaries (the same device arithmetic: bit for bit),
@@ -722,6 +722,26 @@ def test_fused_eltwise_matches_op_by_op(prog, n, hip, dmem, abi, oracle_lib):
     _check(got, caserun.run_case(oracle_lib, ew_case(n_in, steps, xs), abi)["out"], f"fused_eltwise {prog}")
     over = caserun.run_case(hip, ew_case(n_in, steps, xs, out_key="i0"), abi, dmem)["i0"]
     assert caserun.same_bits(over, got)
+
+
+@pytest.mark.parametrize("prog", [0, 1, 4, 5, 6, 7])
+def test_fused_eltwise_compiled_chain_matches_general_kernel(prog, hip, dmem, abi):
+    """A chain with a kernel compiled for it against the same chain on the
+    general kernel, which reads the steps at run time: the same program
+    given one more (unused) input no longer matches the library's table.
+    Same bits; the output large enough for streaming stores."""
+    from ew_cases import EW_PROGRAMS, EW_SPECIALIZED, ew_arrays, ew_case
+    from nnc_py_amd import runtime
+    n_in, steps = EW_PROGRAMS[prog]
+    assert prog in EW_SPECIALIZED
+    n = (20 << 20) + 4
+    print(f"case fused_eltwise compiled chain {prog} n {n}", flush=True)
+    xs = ew_arrays(n_in + 1, n, 90 + prog)
+    got = caserun.run_case(hip, ew_case(n_in, steps, xs[:n_in]), abi, dmem)["out"]
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    general = caserun.run_case(hip, ew_case(n_in + 1, steps, xs), abi, dmem)["out"]
+    assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+    assert caserun.same_bits(got, general)
 
 
 def test_fused_eltwise_rejects_malformed_programs(hip, dmem, abi):

@@ -416,7 +416,7 @@ def test_oracle_gap_gemm_nt_composition(n, c, h, w, o, bias, oracle_lib, abi):
     np.testing.assert_allclose(got, ref.astype(F32), rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("prog", range(4))
+@pytest.mark.parametrize("prog", range(8))
 def test_oracle_fused_eltwise_composition(prog, oracle_lib, abi):
     """nnc_hip_fused_eltwise: each program equals its steps run as single
     nnc_* calls through temporaries (the oracle's own binary / unary / clip
