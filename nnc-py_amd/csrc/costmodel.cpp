@@ -37,6 +37,7 @@
 #include "nnc_costmodel.h"
 #include "nnc_hip.h"
 #include "nnc_ops.h"
+#include "ew_chains.h"
 #include "plan.h"
 
 namespace {
@@ -749,6 +750,9 @@ void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps,
     double bytes = nbytes(out);
     for (int i = 0; i < n_in; ++i) bytes += nbytes(ins[i]);
     stream_kernel("nnc_hip_fused_eltwise", "nnc_hip_fused_eltwise", bytes);
+}
+int nnc_hip_ew_chain_specialized(int n_in, const int* prog, int n_steps) {
+    return nnc::ew_chain_index(n_in, prog, n_steps) >= 0 ? 1 : 0;
 }
 void nnc_sqrt(Tensor* in, Tensor* out) { unary("nnc_sqrt", in, out); }
 void nnc_pow(Tensor* in, Tensor* out) { unary("nnc_pow", in, out); }

@@ -11,7 +11,10 @@
 // alias an input of the same size (the cost_aware planner does this).
 #include <math.h>
 
+#include <utility>
+
 #include "common.h"
+#include "ew_chains.h"
 
 namespace nnc {
 
@@ -244,6 +247,7 @@ static void unary_entry(const char* name, Tensor* in, Tensor* out, float lo = 0.
 // grid, so its switch is a scalar branch.
 // ---------------------------------------------------------------------------
 static constexpr int kEwMaxIn = 4, kEwMaxSteps = 8;
+static_assert(kEwChainMaxSteps == kEwMaxSteps, "ew_chains.h and the interpreter take the same step count");
 struct EwProg {
     const float* in[kEwMaxIn];
     float* out;
@@ -346,10 +350,9 @@ __global__ void __launch_bounds__(256) fused_eltwise_vec4_k(EwProg p, uint32_t n
 // template arguments, so operands are registers named at compile time and
 // each op is its own straight-line code (the interpreter above spends about
 // 4.6 VALU instructions per element on a five-step chain, enough to make an
-// HBM-bound pass VALU-bound). The table holds the chains the mi355x O3
-// compiler emits for its model set (the bandwidth-chain program's two
-// chains) and a few common short ones; any other chain runs on the
-// interpreter. An empty asm statement after each step keeps the step's
+// HBM-bound pass VALU-bound). The chains are ew_chains.h's kEwChains (those
+// the mi355x O3 compiler emits for its model set and a few common short
+// ones); any other chain runs on the interpreter. An empty asm statement after each step keeps the step's
 // result a rounded float that the next step reads, as the op-by-op calls
 // do through memory (no multiply-add contraction across steps).
 // ---------------------------------------------------------------------------
@@ -402,68 +405,32 @@ __global__ void __launch_bounds__(256) ew_chain_k(EwProg p, uint32_t n4) {
     }
 }
 
-struct EwChainSpec {
-    int n_in, n_steps;
-    int prog[3 * kEwMaxSteps];  // op, x, y per step; x, y -1: the running value; y = x for unary ops
-    void (*launch)(const char* name, const EwProg& p, uint32_t n4, bool nt);
-};
-
 template <int NIN, class... Steps>
 static void launch_ew_chain(const char* name, const EwProg& p, uint32_t n4, bool nt) {
     if (nt) launch(name, ew_chain_k<true, NIN, Steps...>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
     else launch(name, ew_chain_k<false, NIN, Steps...>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
 }
 
-template <int NIN, class... Steps>
-static EwChainSpec ew_chain_spec() {
-    static_assert(sizeof...(Steps) >= 1 && sizeof...(Steps) <= kEwMaxSteps, "1 to kEwMaxSteps steps");
-    static_assert(NIN >= 1 && NIN <= kEwMaxIn, "1 to kEwMaxIn inputs");
-    EwChainSpec s{NIN, (int)sizeof...(Steps), {}, &launch_ew_chain<NIN, Steps...>};
-    const int ops[] = {Steps::op...}, xs[] = {Steps::x...}, ys[] = {Steps::y...};
-    for (int i = 0; i < s.n_steps; ++i) {
-        s.prog[3 * i] = ops[i];
-        s.prog[3 * i + 1] = xs[i];
-        s.prog[3 * i + 2] = ys[i];
-    }
-    return s;
+// the kernel of kEwChains[C] (ew_chains.h): its steps as template arguments
+template <int C, size_t... S>
+static void launch_ew_chain_c(const char* name, const EwProg& p, uint32_t n4, bool nt, std::index_sequence<S...>) {
+    constexpr EwChainDef d = kEwChains[C];
+    launch_ew_chain<d.n_in, EwStep<d.prog[3 * S], d.prog[3 * S + 1], d.prog[3 * S + 2]>...>(name, p, n4, nt);
 }
 
-// the specialised chains
-static const EwChainSpec* ew_chain_table(int* count) {
-    typedef EwStep<NNC_EW_ADD_RELU, 0, 1> AddRelu01;
-    static const EwChainSpec table[] = {
-        // bandwidth-chain program: relu(x + y) * x, clip(-6, 6), sigmoid, + t
-        ew_chain_spec<3, AddRelu01, EwStep<NNC_EW_MUL, -1, 0>, EwStep<NNC_EW_CLIP, -1>, EwStep<NNC_EW_SIGMOID, -1>,
-                      EwStep<NNC_EW_ADD, -1, 2>>(),
-        // bandwidth-chain program: tanh(x - y)
-        ew_chain_spec<2, EwStep<NNC_EW_SUB, 0, 1>, EwStep<NNC_EW_TANH, -1>>(),
-        // x * y + z, (x + y) * z, relu(x * y), sigmoid(x + y) * y
-        ew_chain_spec<3, EwStep<NNC_EW_MUL, 0, 1>, EwStep<NNC_EW_ADD, -1, 2>>(),
-        ew_chain_spec<3, EwStep<NNC_EW_ADD, 0, 1>, EwStep<NNC_EW_MUL, -1, 2>>(),
-        ew_chain_spec<2, EwStep<NNC_EW_MUL, 0, 1>, EwStep<NNC_EW_RELU, -1>>(),
-        ew_chain_spec<2, EwStep<NNC_EW_ADD_SIGMOID, 0, 1>, EwStep<NNC_EW_MUL, -1, 1>>(),
-    };
-    *count = (int)(sizeof table / sizeof table[0]);
+template <int C>
+static void launch_ew_chain_at(const char* name, const EwProg& p, uint32_t n4, bool nt) {
+    static_assert(kEwChains[C].n_steps >= 1 && kEwChains[C].n_steps <= kEwMaxSteps, "1 to kEwMaxSteps steps");
+    static_assert(kEwChains[C].n_in >= 1 && kEwChains[C].n_in <= kEwMaxIn, "1 to kEwMaxIn inputs");
+    launch_ew_chain_c<C>(name, p, n4, nt, std::make_index_sequence<kEwChains[C].n_steps>{});
+}
+
+typedef void (*EwChainLaunch)(const char*, const EwProg&, uint32_t, bool);
+
+template <size_t... C>
+static const EwChainLaunch* ew_chain_launchers(std::index_sequence<C...>) {
+    static const EwChainLaunch table[] = {&launch_ew_chain_at<(int)C>...};
     return table;
-}
-
-// The table entry for a chain (prog as nnc_hip_fused_eltwise takes it), or
-// null: same input count, steps, ops and operands (a unary step's y is not
-// compared)
-static const EwChainSpec* ew_chain_find(int n_in, const int* prog, int n_steps) {
-    int count = 0;
-    const EwChainSpec* t = ew_chain_table(&count);
-    for (int c = 0; c < count; ++c) {
-        if (t[c].n_in != n_in || t[c].n_steps != n_steps) continue;
-        bool same = true;
-        for (int s = 0; s < n_steps && same; ++s) {
-            const int op = prog[3 * s];
-            same = op == t[c].prog[3 * s] && prog[3 * s + 1] == t[c].prog[3 * s + 1] &&
-                   (op > NNC_EW_ADD_SIGMOID || prog[3 * s + 2] == t[c].prog[3 * s + 2]);
-        }
-        if (same) return &t[c];
-    }
-    return nullptr;
 }
 
 __global__ void __launch_bounds__(256) fused_eltwise_scalar_k(EwProg p, uint32_t begin, uint32_t n) {
@@ -611,8 +578,9 @@ void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps,
     uint32_t done = 0;
     if (vec && n >= 4) {
         const uint32_t n4 = (uint32_t)(n / 4);
-        if (const EwChainSpec* spec = ew_chain_find(n_in, prog, n_steps))
-            spec->launch(name, p, n4, 4 * n >= kNtStoreBytes);
+        const int chain = ew_chain_index(n_in, prog, n_steps);
+        if (chain >= 0)
+            ew_chain_launchers(std::make_index_sequence<kEwChainCount>{})[chain](name, p, n4, 4 * n >= kNtStoreBytes);
         else if (4 * n >= kNtStoreBytes)
             launch(name, fused_eltwise_vec4_k<true>, dim3(grid_for(n4, 4)), dim3(256), 0, p, n4);
         else
@@ -625,7 +593,7 @@ void nnc_hip_fused_eltwise(Tensor** ins, int n_in, const int* prog, int n_steps,
 
 int nnc_hip_ew_chain_specialized(int n_in, const int* prog, int n_steps) {
     if (!prog || n_in < 1 || n_in > kEwMaxIn || n_steps < 1 || n_steps > kEwMaxSteps) return 0;
-    return ew_chain_find(n_in, prog, n_steps) ? 1 : 0;
+    return ew_chain_index(n_in, prog, n_steps) >= 0 ? 1 : 0;
 }
 
 void nnc_greater(Tensor* a, Tensor* b, Tensor* out) {
