@@ -44,7 +44,7 @@ METRIC = "ResNet-18 fp32 images/s (b1,b32) on 1 GPU; per-op % HBM/MFMA roofline"
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 PEAK_FP32_MFMA_TF = 157.3  # MI355X dense fp32 matrix
 # kernel-table names of the MFMA kernels (their work is priced in FLOP)
-MFMA_KERNELS = ("conv_igemm", "conv_stem", "gemm_mfma", "gemm_dma", "gemm_skinny")
+MFMA_KERNELS = ("conv_igemm", "conv_stem", "conv_ws", "gemm_mfma", "gemm_dma", "gemm_skinny", "gemm_ws", "attention")
 
 
 def load_package():

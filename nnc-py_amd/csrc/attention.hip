@@ -12,7 +12,9 @@
 // context in columns h * dh .. + dh (the merged-head layout the output
 // projection reads).
 //
-// One workgroup of four waves per (batch, head, block of 32 query rows).
+// head_dim 64: attention16_k (below), 16 query rows per workgroup, operands
+// straight into registers. head_dim 32: attention_k, one workgroup of four
+// waves per (batch, head, block of 32 query rows).
 // The block's Q rows and the head's K and V rows go into LDS with 16-byte
 // loads (rows padded to dh + 4 floats). Scores: wave w computes the 32 x 32
 // block of keys 32w .. 32w + 31 with v_mfma_f32_32x32x2_f32 (lane half h
@@ -200,6 +202,112 @@ __global__ void __launch_bounds__(256) attention_k(AttnArgs a) {
     }
 }
 
+// head_dim 64: one workgroup per (batch, head, block of 16 query rows) with
+// v_mfma_f32_16x16x4f32 (lane (li = lane % 16, g = lane / 16): A[li][g],
+// B[g][li]; accumulator r is row 4g + r, column li). The dot products'
+// terms are taken in any order both operands agree on: lane group g takes
+// d = 16g + t (Q K^T) and keys 64c + 16g + t (P V) at step t, so Q, K and P
+// rows are 16-byte loads. Q, K and V go straight from global memory into
+// the operand registers (no LDS staging): wave w computes the scores of keys
+// 32w .. 32w + 31 (two 16 x 16 blocks over the 16 d steps) and, after the
+// softmax, output columns 16w .. 16w + 15 over all keys (two chunks of 64).
+// The scaled scores go to LDS, 16 threads per row take its maximum and sum
+// (eight keys each, four xor shuffles) and write exp(s - max) / sum back.
+__global__ void __launch_bounds__(256) attention16_k(AttnArgs a) {
+    constexpr int DH = 64, LDP = kAttnMaxSeq + 4;
+    __shared__ __align__(16) float ps[16 * LDP];
+    const int lane = threadIdx.x & 63, li = lane & 15, g4 = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int qblocks = a.seq / 16;
+    const int qb = blockIdx.x % qblocks, bh = blockIdx.x / qblocks;
+    const int h = bh % a.heads, b = bh / a.heads;
+    const int64_t row0 = (int64_t)b * a.seq;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qkv);
+    // operands: every load issued before the first MFMA
+    f32x4 qa[4], kk[2][4];
+    float vv[2][16];
+    {
+        const uint32_t qoff = (uint32_t)(((row0 + qb * 16 + li) * a.ld + a.q_col + h * DH + 16 * g4) * 4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) qa[u] = load_f32x4(rq, qoff + 16u * u);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int key = 32 * wave + 16 * kb + li;
+            const uint32_t koff = (uint32_t)(((row0 + key) * a.ld + a.k_col + h * DH + 16 * g4) * 4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) kk[kb][u] = load_f32x4(rq, key < a.seq ? koff + 16u * u : kOutOfRange);
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int key = 64 * c + 16 * g4 + t;
+                const uint32_t voff = (uint32_t)(((row0 + key) * a.ld + a.v_col + h * DH + 16 * wave + li) * 4);
+                vv[c][t] = load_f32(rq, key < a.seq ? voff : kOutOfRange);
+            }
+    }
+    const float dv = a.div[0];
+    __builtin_amdgcn_sched_barrier(0);
+    // scores of keys 32 wave + 16 kb + li for rows 4 g4 + r
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            // (element copies first: this compiler's ext-vector element reads)
+            const float x = qa[t >> 2][t & 3], y = kk[kb][t >> 2][t & 3];
+            s = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, s, 0, 0, 0);
+        }
+        const int key = 32 * wave + 16 * kb + li;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float x = s[r];
+            ps[(4 * g4 + r) * LDP + key] = key < a.seq ? x / dv : -INFINITY;
+        }
+    }
+    __syncthreads();
+    {
+        // softmax: 16 threads per row (a 16-lane group), 8 keys each
+        float* prow = ps + (threadIdx.x >> 4) * LDP + (threadIdx.x & 15) * 8;
+        f32x4 x0 = *reinterpret_cast<const f32x4*>(prow), x1 = *reinterpret_cast<const f32x4*>(prow + 4);
+        float m = fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])), fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3])));
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        float t = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            x0[c] = __expf(x0[c] - m);
+            x1[c] = __expf(x1[c] - m);
+            t += x0[c] + x1[c];
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) t += __shfl_xor(t, o);
+        const float inv = 1.0f / t;
+        *reinterpret_cast<f32x4*>(prow) = x0 * inv;
+        *reinterpret_cast<f32x4*>(prow + 4) = x1 * inv;
+    }
+    __syncthreads();
+    // context: columns 16 wave + li for rows 4 g4 + r, keys 64 c + 16 g4 + t
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        f32x4 pa[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pa[u] = *reinterpret_cast<const f32x4*>(&ps[li * LDP + 64 * c + 16 * g4 + 4 * u]);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const float x = pa[t >> 2][t & 3];
+            o = __builtin_amdgcn_mfma_f32_16x16x4f32(x, vv[c][t], o, 0, 0, 0);
+        }
+    }
+    float* orow = a.out + (row0 + qb * 16 + 4 * g4) * (int64_t)(a.heads * DH) + h * DH + 16 * wave + li;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float x = o[r];
+        orow[(int64_t)r * (a.heads * DH)] = x;
+    }
+}
+
 template <int DH>
 static void launch_attention(const AttnArgs& a, int blocks, const char* name) {
     auto kernel = attention_k<DH>;
@@ -243,11 +351,10 @@ void nnc_hip_attention(Tensor* qkv, Tensor* div, Tensor* out, int batch, int seq
     AttnArgs a{(const float*)qkv->data, (const float*)div->data, (float*)out->data, seq, heads, (int)ld,
                q_col, k_col, v_col};
     set_work(4.0 * batch * heads * (double)seq * seq * head_dim, 0.0);
-    const int blocks = (int)(batch * heads * (seq / 32));
     if (head_dim == 64)
-        launch_attention<64>(a, blocks, name);
+        launch("attention16_d64", attention16_k, dim3((unsigned)(batch * heads * (seq / 16))), dim3(256), 0, a);
     else
-        launch_attention<32>(a, blocks, name);
+        launch_attention<32>(a, (int)(batch * heads * (seq / 32)), "attention32_d32");
 }
 
 }  // extern "C"

@@ -729,17 +729,20 @@ void nnc_hip_scaled_softmax(Tensor* in, Tensor* div, Tensor* out, int axis) {
     if (in && div && out && numel(out) > 0)
         stream_kernel("nnc_hip_scaled_softmax", "nnc_hip_scaled_softmax", nbytes(in) + nbytes(out), 0.40);
 }
-// attention.hip nnc_hip_attention: one workgroup per (batch, head, 32 query
-// rows) on its own CU, staging Q, K and V and running two MFMA products;
-// the body fitted to the transformer encoder at batch 8, sequence 128
-constexpr double kAttnBodyUs = 4.3;
+// attention.hip nnc_hip_attention: one workgroup per (batch, head, 16 query
+// rows) for heads of 64 (attention16_k), 32 rows for heads of 32
+// (attention_k), each on its own CU staging Q, K and V and running two
+// MFMA products; the body fitted to the transformer encoder at batch 8,
+// sequence 128
+constexpr double kAttnBodyUs = 2.7;
 void nnc_hip_attention(Tensor* qkv, Tensor* div, Tensor* out, int batch, int seq, int heads, int head_dim, int q_col,
                        int k_col, int v_col) {
     (void)q_col, (void)k_col, (void)v_col;
     if (!qkv || !div || !out || batch <= 0 || seq <= 0 || heads <= 0) return;
-    const int64_t blocks = (int64_t)batch * heads * ((seq + 31) / 32);
+    const int64_t blocks = (int64_t)batch * heads * (head_dim == 64 ? (seq + 15) / 16 : (seq + 31) / 32);
     const double flops = 4.0 * batch * heads * (double)seq * seq * head_dim;
-    record("nnc_hip_attention", "nnc_hip_attention", kLaunchUs + kAttnBodyUs * ceil_div(blocks, kCUs), flops,
+    record("nnc_hip_attention", head_dim == 64 ? "attention16_d64" : "attention32_d32",
+           kLaunchUs + kAttnBodyUs * ceil_div(blocks, kCUs), flops,
            nbytes(qkv) + nbytes(out));
 }
 // eltwise.hip nnc_hip_fused_eltwise: one streaming pass, each input read and

@@ -966,9 +966,7 @@ static void launch_gws(const GemmArgs& g, int NS, int S, int iters, int tiles, u
         case 1: return launch_gws_ns<1, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
         case 2: return launch_gws_ns<2, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
         case 3: return launch_gws_ns<3, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
-        case 4: return launch_gws_ns<4, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
-        case 5: return launch_gws_ns<5, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
-        default: return launch_gws_ns<6, A_KC, B_KC>(g, S, iters, tiles, grid, kname);
+        default: return launch_gws_ns<4, A_KC, B_KC>(g, S, iters, tiles, grid, kname);  // NS <= kGwsMaxSlices
     }
 }
 

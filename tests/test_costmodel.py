@@ -39,7 +39,8 @@ FAMILY = [
     (r"conv_streamk_fixup$", "conv_fixup_k"),
     (r"gemm_dma_", "gemm_dma_k"),
     (r"gemm_ws_32x32_", "gemm_ws_k"),
-    (r"nnc_hip_attention$", "attention_k"),
+    (r"attention16_d64$", "attention16_k"),
+    (r"attention32_d32$", "attention_k"),
     (r"gemm_mfma_", "gemm_streamk_k"),
     (r"gemm_streamk_fixup$", "gemm_fixup_k"),
     (r"dot_rows_", "dot_k"),

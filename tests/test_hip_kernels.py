@@ -406,8 +406,9 @@ GEMM_SHAPES = [
     (17, 333, 1020, 0, 1, False),
     (32, 50, 36, 0, 1, True),
     (3, 40, 1024, 0, 1, True),
-    # products up to 1 GFLOP run on gemm_ws_k (32x32 tiles, waves splitting
-    # K; every layout above that is not skinny or a dot/GEMV); these keep
+    # products up to 1 GFLOP on fewer than 1024 workgroups run on gemm_ws_k
+    # (32x32 tiles, waves splitting K; every layout above that is not skinny
+    # or a dot/GEMV, except 1024^3 and 1536^2 x 132); these keep
     # the other kernels covered: register-staged tiles (A k-contiguous with
     # K % 4 != 0), direct-to-LDS 64x64 with a K tail of one 16-byte chunk,
     # and 128x128 with a K tail of 4
@@ -928,6 +929,8 @@ ATTENTION_SHAPES = [
     (2, 32, 2, 32, (0, 64, 128), 5.65, 0),      # one key wave, heads of 32 (four key groups)
     (3, 96, 1, 64, (128, 0, 64), -1.5, 4),      # keys past 96 masked, Q after K and V, a wider row
     (1, 64, 3, 32, (0, 96, 192), 2.0, 0),
+    (2, 32, 2, 64, (0, 128, 256), 8.0, 0),      # heads of 64 over 32 keys: the second key chunk masked
+    (1, 64, 8, 64, (0, 512, 1024), 8.0, 0),     # eight heads of 64, half the keys masked
 ]
 
 
