@@ -159,13 +159,32 @@ class ClockSampler:
                 continue
             clk = [r[0] for r in rows]
             act = float(np.mean([r[1] for r in rows]))
+            # samples taken while the GPU reported itself busy: an idle
+            # sample (the clock parked low between activity windows) says
+            # nothing about the clock the kernels ran at
+            busy = [r[0] for r in rows if r[1] >= 50.0]
             if best is None or act > best["gfx_activity_pct"]:
-                best = {"mean_mhz": round(float(np.mean(clk)), 1), "min_mhz": round(min(clk), 1),
-                        "max_mhz": round(max(clk), 1), "samples": len(clk), "gfx_activity_pct": round(act, 1)}
+                best = {"mean_mhz": round(float(np.mean(clk)), 1),
+                        "median_mhz": round(float(np.median(clk)), 1),
+                        "busy_mean_mhz": round(float(np.mean(busy)), 1) if busy else None,
+                        "busy_samples": len(busy),
+                        "min_mhz": round(min(clk), 1), "max_mhz": round(max(clk), 1),
+                        "samples": len(clk), "gfx_activity_pct": round(act, 1)}
         if best is None:
             return {"error": self.error or "no amdsmi samples"}
-        best["source"] = "amdsmi GFX clock, sampled every 10 ms during hipGraph replays of the batch program"
+        best["source"] = ("amdsmi GFX clock and GFX activity, sampled every 10 ms during hipGraph "
+                          "replays of the batch program; busy = samples with activity >= 50%")
         return best
+
+    @staticmethod
+    def kernel_mhz(clock: dict | None) -> float | None:
+        """The clock the kernels ran at: the mean over busy samples where
+        there are at least ten, else the median of all samples."""
+        if not clock or "mean_mhz" not in clock:
+            return None
+        if clock.get("busy_samples", 0) >= 10 and clock.get("busy_mean_mhz"):
+            return clock["busy_mean_mhz"]
+        return clock["median_mhz"]
 
 
 def kernel_table(ex, runtime, steps: int) -> list[dict]:
@@ -663,11 +682,12 @@ def main() -> int:
                 "peak": peak, "unit": dom["unit"], "frac": round(dom["achieved"] / peak, 4),
                 "traffic": traffic, "avg_launch_us": dom["avg_us"],
                 "work_per_launch": dom["work_per_launch"]}
-    if clock and "mean_mhz" in clock:
+    mhz = ClockSampler.kernel_mhz(clock)
+    if mhz:
         # the published peak assumes the 2.4 GHz peak engine clock; the
         # kernel ran at the sampled clock
-        roofline["shader_clock_mhz"] = clock["mean_mhz"]
-        roofline["frac_at_clock"] = round(dom["achieved"] / (peak * clock["mean_mhz"] / 2400.0), 4)
+        roofline["shader_clock_mhz"] = mhz
+        roofline["frac_at_clock"] = round(dom["achieved"] / (peak * mhz / 2400.0), 4)
     if traffic_detail:
         roofline["traffic_detail"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in traffic_detail.items()}
     gpu_ms = sum(r["ms_per_step"] for r in table)
