@@ -441,19 +441,74 @@ def _op_roofline(runtime, fn, reps: int = 10, warmup: int = 3) -> dict:
             "op_frac": round(op_ach / peak, 4)}
 
 
-def _copy_ceiling(runtime, nbytes: int) -> dict:
+def _graph_us(runtime, fns, reps: int, launches: int = 5) -> float:
+    """Microseconds per replay of one hipGraph holding `reps` rounds of the
+    calls in `fns`."""
+    lib = runtime.load()
+    runtime.check(lib.nnc_hip_graph_begin(), "graph_begin")
+    for _ in range(reps):
+        for f in fns:
+            f()
+    runtime.check(lib.nnc_hip_graph_end(), "graph_end")
+    runtime.check(lib.nnc_hip_graph_launch(), "graph_launch")
+    runtime.sync()
+    runtime.profile_reset()
+    runtime.profile_enable(True)
+    for _ in range(launches):
+        runtime.check(lib.nnc_hip_graph_launch(), "graph_launch")
+    runtime.sync()
+    ms = sum(r["ms"] for r in runtime.profile_table() if r["name"] == "graph")
+    runtime.profile_enable(False)
+    lib.nnc_hip_graph_destroy()
+    return ms / launches * 1e3
+
+
+EVICT_BYTES = 320 << 20  # read by the eviction copy: more than the 256 MB Infinity Cache
+
+
+def _cold_op_us(runtime, fn, reps: int = 10, rounds: int = 3) -> float:
+    """Microseconds per call of `fn` with its inputs out of the Infinity
+    Cache: a graph of `reps` x (a 320 MB device copy, then the call) less a
+    graph of the copies alone, medians over `rounds` of each. Ops whose
+    inputs fit the 256 MB cache otherwise read them back from it on every
+    repeated call."""
+    n = EVICT_BYTES // 4
+    src = runtime.DeviceBuffer.empty((n,))
+    dst = runtime.DeviceBuffer.empty((n,))
+    ts, td = src.tensor(), dst.tensor()
+    lib = runtime.load()
+
+    def evict():
+        lib.nnc_identity(ctypes.byref(ts[0]), ctypes.byref(td[0]))
+
+    alone, both = [], []
+    for _ in range(rounds):
+        alone.append(_graph_us(runtime, [evict], reps))
+        both.append(_graph_us(runtime, [evict, fn], reps))
+    src.free()
+    dst.free()
+    return (float(np.median(both)) - float(np.median(alone))) / reps
+
+
+def _copy_ceiling(runtime, nbytes: int, cold: bool = False) -> dict:
     """A plain device copy (copy16_k) that reads and writes `nbytes` each,
     timed like an op: the bandwidth a read-once/write-once kernel of this
-    size reaches, ramp-up and tail included."""
+    size reaches, ramp-up and tail included (and with `cold`, the same copy
+    with its source out of the Infinity Cache, `_cold_op_us`)."""
     n = max(4, nbytes // 4)
     src = runtime.DeviceBuffer.empty((n,))
     dst = runtime.DeviceBuffer.empty((n,))
     ts, td = src.tensor(), dst.tensor()
     lib = runtime.load()
-    res = _op_roofline(runtime, lambda: lib.nnc_identity(ctypes.byref(ts[0]), ctypes.byref(td[0])))
+    fn = lambda: lib.nnc_identity(ctypes.byref(ts[0]), ctypes.byref(td[0]))  # noqa: E731
+    res = _op_roofline(runtime, fn)
+    out = {"bytes": 8 * n, "us": res["op_us"], "GB/s": res["op_achieved"], "frac": res["op_frac"]}
+    if cold:
+        cu = _cold_op_us(runtime, fn)
+        out.update({"cold_us": round(cu, 2), "cold_frac": round(8 * n / (cu * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)})
     src.free()
     dst.free()
-    return {"bytes": 8 * n, "us": res["op_us"], "GB/s": res["op_achieved"], "frac": res["op_frac"]}
+    return out
 
 
 def run_suite() -> int:
@@ -478,9 +533,16 @@ def run_suite() -> int:
         keep.append((buf, t))
         return ctypes.pointer(t[0])
 
-    def emit(suite, workload, res, copy_bytes=None, **extra):
+    def emit(suite, workload, res, copy_bytes=None, cold=None, **extra):
+        """`cold`: the op's call again, timed with its inputs out of the
+        Infinity Cache (`_cold_op_us`), for ops whose data fits it."""
+        if cold:
+            cu = _cold_op_us(runtime, cold)
+            nbytes = res["op_achieved"] * 1e3 * res["op_us"]  # GB/s x us
+            res["cold_op_us"] = round(cu, 2)
+            res["cold_op_frac"] = round(nbytes / (cu * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)
         if copy_bytes:
-            res["copy_ceiling"] = _copy_ceiling(runtime, copy_bytes)
+            res["copy_ceiling"] = _copy_ceiling(runtime, copy_bytes, cold=bool(cold))
         print(json.dumps({"suite": suite, "workload": workload, **extra, **res}), flush=True)
 
     for n in (1024, 2048, 4096):
@@ -518,17 +580,17 @@ def run_suite() -> int:
          _op_roofline(runtime, lambda: lib.nnc_split(tcat, ctypes.cast(pair, abi.TPP), 2, 1)))
     keep.clear()
     ts, tso = dev(rng.standard_normal((4096, 1024)).astype(np.float32)), dev(np.zeros((4096, 1024), np.float32))
-    emit("bandwidth", "nnc_softmax [4096,1024] axis -1", _op_roofline(runtime, lambda: lib.nnc_softmax(ts, tso, -1)),
-         copy_bytes=4 * 4096 * 1024)
+    sm = lambda: lib.nnc_softmax(ts, tso, -1)  # noqa: E731
+    emit("bandwidth", "nnc_softmax [4096,1024] axis -1", _op_roofline(runtime, sm), copy_bytes=4 * 4096 * 1024, cold=sm)
     tl, tg, tb0 = dev(rng.standard_normal((8192, 768)).astype(np.float32)), dev(np.ones(768, np.float32)), dev(np.zeros(768, np.float32))
     tlo = dev(np.zeros((8192, 768), np.float32))
-    emit("bandwidth", "nnc_layernorm [8192,768] eps 1e-5",
-         _op_roofline(runtime, lambda: lib.nnc_layernorm(tl, tg, tb0, tlo, -1, 1e-5)), copy_bytes=4 * 8192 * 768)
+    ln = lambda: lib.nnc_layernorm(tl, tg, tb0, tlo, -1, 1e-5)  # noqa: E731
+    emit("bandwidth", "nnc_layernorm [8192,768] eps 1e-5", _op_roofline(runtime, ln), copy_bytes=4 * 8192 * 768, cold=ln)
     r = rng.standard_normal((32, 512, 28, 28)).astype(np.float32)
     tr, tro = dev(r, (32, 512, 784)), dev(np.zeros((32, 512, 1), np.float32))
     for op in ("nnc_reducemean", "nnc_reducesum"):
-        emit("bandwidth", f"{op} axes (2,3) of [32,512,28,28]",
-             _op_roofline(runtime, lambda op=op: getattr(lib, op)(tr, tro, 2, 1)))
+        rd = lambda op=op: getattr(lib, op)(tr, tro, 2, 1)  # noqa: E731
+        emit("bandwidth", f"{op} axes (2,3) of [32,512,28,28]", _op_roofline(runtime, rd), cold=rd)
     keep.clear()
 
     # the element-wise chain relu(x + y) * x, clip(-6, 6), sigmoid, + t as one

@@ -138,14 +138,16 @@ inline void launch(const char* name, Kernel kernel, dim3 grid, dim3 block, size_
     hip_ok(hipGetLastError(), name, "launch");
 }
 
-// Streaming stores. An output of at least kNtStoreBytes cannot stay
-// cache-resident for its reader anyway (MI355X's Infinity Cache is 256 MB,
-// shared with the inputs being streamed), so the streaming kernels write it
-// with non-temporal stores, which go to HBM without displacing the inputs:
-// a 205 MB device copy measured 5.2 TB/s with ordinary stores and 7.2 TB/s
-// with non-temporal ones; copies under the cache's size ran at the same
-// speed either way.
-static constexpr int64_t kNtStoreBytes = (int64_t)64 << 20;
+// Streaming stores. The streaming kernels (copies, concat/split,
+// element-wise, the softmax and layernorm rows) write an output of at least
+// kNtStoreBytes - twice one XCD's 4 MB L2 - with non-temporal stores, which
+// go to HBM without displacing the inputs being streamed. Measured as
+// hipGraph replays of ten calls: a 205 MB device copy 5.2 -> 7.2 TB/s; a
+// 16 MB copy 5.26 -> 4.32 us, softmax [4096,1024] (16.8 MB out) 6.25 ->
+// 4.90 us, layernorm [8192,768] (25 MB out) 9.34 -> 7.03 us; outputs of 1
+// MB, read by the next GEMM, the same either way, and so was a threshold of
+// 0 against this one.
+static constexpr int64_t kNtStoreBytes = (int64_t)8 << 20;
 typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
 

@@ -6,8 +6,9 @@
 // inner == 1 (the reduced / normalised elements are contiguous): one wave64
 // per row. Rows of up to 4096 floats are read once with 16-byte loads into
 // registers; max / sums are combined across the wave with DPP lane moves, and
-// the row is written once: one HBM read + one HBM write per element. Longer
-// rows loop over global memory (re-reads come from L2).
+// the row is written once: one HBM read + one HBM write per element
+// (non-temporal stores for outputs of kNtStoreBytes or more). Longer rows
+// loop over global memory (re-reads come from L2).
 //
 // inner > 1 (strided axis): one thread per (outer, inner) column, lanes along
 // inner so every load coalesces; the column is walked in the reference's
@@ -74,30 +75,34 @@ __device__ __forceinline__ float wave_max(float v) {
 template <int PER>
 constexpr bool kPrefetch = PER <= 8;
 
-template <int PER>
+// FULL: the row is exactly 64 * PER float4 (every lane's PER float4 inside
+// it), so no lane is masked off and the kernels carry no per-lane bounds
+// tests - the exec-mask branches they cost made the row kernels' arithmetic
+// phase, which runs between all rows' loads and stores, the longer
+template <int PER, bool FULL = false>
 __device__ __forceinline__ void load_row4(float4 (&v)[PER], const float* base, int n4, int lane, float fill) {
     const float4* x = reinterpret_cast<const float4*>(base);
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
         const int idx = lane + 64 * q;
-        v[q] = idx < n4 ? x[idx] : make_float4(fill, fill, fill, fill);
+        v[q] = FULL || idx < n4 ? x[idx] : make_float4(fill, fill, fill, fill);
     }
 }
 
 // DIV: the row's elements divided by the scalar *dv first (nnc_div's x / y)
 // - the attention score scaling of nnc_hip_scaled_softmax; the -inf fill of
 // lanes past the row stays as it is
-template <int PER, bool DIV>
+template <int PER, bool DIV, bool FULL>
 __device__ __forceinline__ void load_sm_row(float4 (&v)[PER], const float* base, int d4, int lane, float dv) {
-    load_row4<PER>(v, base, d4, lane, -INFINITY);
+    load_row4<PER, FULL>(v, base, d4, lane, -INFINITY);
     if (DIV) {
 #pragma unroll
         for (int q = 0; q < PER; ++q)
-            if (lane + 64 * q < d4) v[q] = make_float4(v[q].x / dv, v[q].y / dv, v[q].z / dv, v[q].w / dv);
+            if (FULL || lane + 64 * q < d4) v[q] = make_float4(v[q].x / dv, v[q].y / dv, v[q].z / dv, v[q].w / dv);
     }
 }
 
-template <int PER, bool DIV>
+template <int PER, bool DIV, bool FULL, bool NT>
 __global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, const float* div, float* out,
                                                          int64_t rows, int dim) {
     const int lane = threadIdx.x & 63;
@@ -107,16 +112,16 @@ __global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, const 
     if (row >= rows) return;
     const float dv = DIV ? div[0] : 1.0f;
     float4 v[PER];
-    load_sm_row<PER, DIV>(v, in + row * dim, d4, lane, dv);
+    load_sm_row<PER, DIV, FULL>(v, in + row * dim, d4, lane, dv);
     while (true) {
         const int64_t nrow = row + wstride;
         const bool more = nrow < rows;
         float4 nx[PER];
-        if (kPrefetch<PER> && more) load_sm_row<PER, DIV>(nx, in + nrow * dim, d4, lane, dv);
+        if (kPrefetch<PER> && more) load_sm_row<PER, DIV, FULL>(nx, in + nrow * dim, d4, lane, dv);
         float m = -INFINITY;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-            if (lane + 64 * q < d4) {
+            if (FULL || lane + 64 * q < d4) {
                 if (v[q].x > m) m = v[q].x;
                 if (v[q].y > m) m = v[q].y;
                 if (v[q].z > m) m = v[q].z;
@@ -127,7 +132,7 @@ __global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, const 
         float s = 0.f;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-            if (lane + 64 * q < d4) {
+            if (FULL || lane + 64 * q < d4) {
                 v[q].x = __expf(v[q].x - m);
                 v[q].y = __expf(v[q].y - m);
                 v[q].z = __expf(v[q].z - m);
@@ -141,10 +146,11 @@ __global__ void __launch_bounds__(256) softmax_rows_v4_k(const float* in, const 
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             const int idx = lane + 64 * q;
-            if (idx < d4) y[idx] = make_float4(v[q].x * rs, v[q].y * rs, v[q].z * rs, v[q].w * rs);
+            if (FULL || idx < d4)
+                store_f4<NT>(reinterpret_cast<float*>(y + idx), make_float4(v[q].x * rs, v[q].y * rs, v[q].z * rs, v[q].w * rs));
         }
         if (!more) break;
-        if (!kPrefetch<PER>) load_sm_row<PER, DIV>(nx, in + nrow * dim, d4, lane, dv);
+        if (!kPrefetch<PER>) load_sm_row<PER, DIV, FULL>(nx, in + nrow * dim, d4, lane, dv);
 #pragma unroll
         for (int q = 0; q < PER; ++q) v[q] = nx[q];
         row = nrow;
@@ -193,19 +199,19 @@ __global__ void __launch_bounds__(256) softmax_cols_k(const float* in, float* ou
 // ---------------------------------------------------------------------------
 // ADD: the row is in + in2 (same size, nnc_add's element-wise sum) - the
 // residual add of nnc_hip_add_layernorm, summed in registers
-template <int PER, bool ADD>
+template <int PER, bool ADD, bool FULL>
 __device__ __forceinline__ void load_ln_row(float4 (&v)[PER], const float* in, const float* in2, int64_t off, int s4,
                                             int lane) {
-    load_row4<PER>(v, in + off, s4, lane, 0.f);
+    load_row4<PER, FULL>(v, in + off, s4, lane, 0.f);
     if (ADD) {
         float4 w[PER];
-        load_row4<PER>(w, in2 + off, s4, lane, 0.f);
+        load_row4<PER, FULL>(w, in2 + off, s4, lane, 0.f);
 #pragma unroll
         for (int q = 0; q < PER; ++q) v[q] = make_float4(v[q].x + w[q].x, v[q].y + w[q].y, v[q].z + w[q].z, v[q].w + w[q].w);
     }
 }
 
-template <int PER, bool INNER1, bool ADD>
+template <int PER, bool INNER1, bool ADD, bool FULL, bool NT>
 __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, const float* in2, const float* g,
                                                            const float* b, float* out, int64_t rows,
                                                            int span, int inner, float eps) {
@@ -215,12 +221,12 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
     int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     float4 v[PER];
-    load_ln_row<PER, ADD>(v, in, in2, row * span, s4, lane);
+    load_ln_row<PER, ADD, FULL>(v, in, in2, row * span, s4, lane);
     while (true) {
         const int64_t nrow = row + wstride;
         const bool more = nrow < rows;
         float4 nx[PER];
-        if (kPrefetch<PER> && more) load_ln_row<PER, ADD>(nx, in, in2, nrow * span, s4, lane);
+        if (kPrefetch<PER> && more) load_ln_row<PER, ADD, FULL>(nx, in, in2, nrow * span, s4, lane);
         float acc = 0.f;
 #pragma unroll
         for (int q = 0; q < PER; ++q) acc += (v[q].x + v[q].y) + (v[q].z + v[q].w);
@@ -228,7 +234,7 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
         float sq = 0.f;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-            if (lane + 64 * q < s4) {
+            if (FULL || lane + 64 * q < s4) {
                 const float dx = v[q].x - mean, dy = v[q].y - mean;
                 const float dz = v[q].z - mean, dw = v[q].w - mean;
                 sq += (dx * dx + dy * dy) + (dz * dz + dw * dw);
@@ -241,7 +247,7 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             const int idx = lane + 64 * q;
-            if (idx < s4) {
+            if (FULL || idx < s4) {
                 const int e = idx * 4;
                 float r[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
                 float gv[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -265,11 +271,11 @@ __global__ void __launch_bounds__(256) layernorm_rows_v4_k(const float* in, cons
                 }
 #pragma unroll
                 for (int c = 0; c < 4; ++c) r[c] = gv[c] * ((r[c] - mean) * rsd) + bv[c];
-                y[idx] = make_float4(r[0], r[1], r[2], r[3]);
+                store_f4<NT>(reinterpret_cast<float*>(y + idx), make_float4(r[0], r[1], r[2], r[3]));
             }
         }
         if (!more) break;
-        if (!kPrefetch<PER>) load_ln_row<PER, ADD>(nx, in, in2, nrow * span, s4, lane);
+        if (!kPrefetch<PER>) load_ln_row<PER, ADD, FULL>(nx, in, in2, nrow * span, s4, lane);
 #pragma unroll
         for (int q = 0; q < PER; ++q) v[q] = nx[q];
         row = nrow;
@@ -411,22 +417,39 @@ static bool split_axis(const char* name, Tensor* in, int& axis, int64_t& outer, 
 // past the grid cap a wave walks several rows, prefetching the next
 static unsigned row_grid(int64_t rows) { return grid_for(rows, 4, 1); }
 
+template <int PER, bool FULL, bool NT>
+static void softmax_v4_at(const float* x, const float* dv, float* y, int64_t rows, int dim, const char* name) {
+    if (dv) launch(name, softmax_rows_v4_k<PER, true, FULL, NT>, dim3(row_grid(rows)), dim3(256), 0, x, dv, y, rows, dim);
+    else launch(name, softmax_rows_v4_k<PER, false, FULL, NT>, dim3(row_grid(rows)), dim3(256), 0, x, dv, y, rows, dim);
+}
 template <int PER>
 static void softmax_v4(const float* x, const float* dv, float* y, int64_t rows, int dim, const char* name) {
-    if (dv) launch(name, softmax_rows_v4_k<PER, true>, dim3(row_grid(rows)), dim3(256), 0, x, dv, y, rows, dim);
-    else launch(name, softmax_rows_v4_k<PER, false>, dim3(row_grid(rows)), dim3(256), 0, x, dv, y, rows, dim);
+    const bool full = dim == 256 * PER, nt = 4 * rows * dim >= kNtStoreBytes;
+    if (full && nt) softmax_v4_at<PER, true, true>(x, dv, y, rows, dim, name);
+    else if (full) softmax_v4_at<PER, true, false>(x, dv, y, rows, dim, name);
+    else if (nt) softmax_v4_at<PER, false, true>(x, dv, y, rows, dim, name);
+    else softmax_v4_at<PER, false, false>(x, dv, y, rows, dim, name);
 }
 
-template <int PER>
-static void layernorm_v4(const float* x, const float* x2, const float* g, const float* b, float* y, int64_t rows,
-                         int span, int inner, float eps, const char* name) {
+template <int PER, bool FULL, bool NT>
+static void layernorm_v4_at(const float* x, const float* x2, const float* g, const float* b, float* y, int64_t rows,
+                            int span, int inner, float eps, const char* name) {
     // inner == 1 with 16-byte aligned scale/bias: vector loads of those too
     const bool in1 = inner == 1 && (!g || aligned16(g)) && (!b || aligned16(b));
     const dim3 grid(row_grid(rows)), block(256);
-    if (x2 && in1) launch(name, layernorm_rows_v4_k<PER, true, true>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
-    else if (x2) launch(name, layernorm_rows_v4_k<PER, false, true>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
-    else if (in1) launch(name, layernorm_rows_v4_k<PER, true, false>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
-    else launch(name, layernorm_rows_v4_k<PER, false, false>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
+    if (x2 && in1) launch(name, layernorm_rows_v4_k<PER, true, true, FULL, NT>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
+    else if (x2) launch(name, layernorm_rows_v4_k<PER, false, true, FULL, NT>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
+    else if (in1) launch(name, layernorm_rows_v4_k<PER, true, false, FULL, NT>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
+    else launch(name, layernorm_rows_v4_k<PER, false, false, FULL, NT>, grid, block, 0, x, x2, g, b, y, rows, span, inner, eps);
+}
+template <int PER>
+static void layernorm_v4(const float* x, const float* x2, const float* g, const float* b, float* y, int64_t rows,
+                         int span, int inner, float eps, const char* name) {
+    const bool full = span == 256 * PER, nt = 4 * rows * span >= kNtStoreBytes;
+    if (full && nt) layernorm_v4_at<PER, true, true>(x, x2, g, b, y, rows, span, inner, eps, name);
+    else if (full) layernorm_v4_at<PER, true, false>(x, x2, g, b, y, rows, span, inner, eps, name);
+    else if (nt) layernorm_v4_at<PER, false, true>(x, x2, g, b, y, rows, span, inner, eps, name);
+    else layernorm_v4_at<PER, false, false>(x, x2, g, b, y, rows, span, inner, eps, name);
 }
 
 }  // namespace nnc
@@ -508,6 +531,7 @@ static void layernorm_run(Tensor* in, Tensor* in2, Tensor* scale, Tensor* bias, 
     const int sp = (int)span, inn = (int)inner;
     if (v4 && span <= 256) return layernorm_v4<1>(x, x2, g, b, y, outer, sp, inn, eps, name);
     if (v4 && span <= 512) return layernorm_v4<2>(x, x2, g, b, y, outer, sp, inn, eps, name);
+    if (v4 && span == 768) return layernorm_v4<3>(x, x2, g, b, y, outer, sp, inn, eps, name);
     if (v4 && span <= 1024) return layernorm_v4<4>(x, x2, g, b, y, outer, sp, inn, eps, name);
     if (v4 && span <= 2048) return layernorm_v4<8>(x, x2, g, b, y, outer, sp, inn, eps, name);
     if (v4 && span <= 4096) return layernorm_v4<16>(x, x2, g, b, y, outer, sp, inn, eps, name);

@@ -551,9 +551,11 @@ def test_maxpool_3x3s2_bit_exact(shape, hip, dmem, abi, oracle_lib):
 
 
 # Row kernels past the grid cap (more than 16384 rows: each wave walks
-# several rows, loading the next while it reduces the current), and a row of
-# the largest register-resident length (4096 floats, no prefetch)
-ROW_SHAPES = [(40000, 64), (20000, 260), (17, 4096)]
+# several rows, loading the next while it reduces the current), a row of
+# the largest register-resident length (4096 floats, no prefetch), and rows
+# that fill every lane exactly (1024 and 768 floats: the kernels without
+# per-lane bounds tests), past the grid cap and below it
+ROW_SHAPES = [(40000, 64), (20000, 260), (17, 4096), (20000, 1024), (333, 768), (70, 256)]
 
 
 @pytest.mark.parametrize("shape", ROW_SHAPES, ids=[str(s) for s in ROW_SHAPES])
