@@ -289,12 +289,24 @@ void gemm(const char* op, int M, int N, int K, int batches, bool a_kc, bool b_kc
     if (M <= 0 || N <= 0 || batches <= 0) return;
     const double flops = 2.0 * M * (double)N * K * batches;
     if (K <= 0) return stream_kernel(op, op, 4.0 * M * N);
+    if (batches == 1 && M == 1 && !b_kc && N % 4 == 0) {
+        // gemm.hip gemv_fin_k: one launch, its K splits finished in the
+        // kernel by the last of each column block's workgroups (a round trip
+        // for the partials when split)
+        const int col_blocks = (int)ceil_div(N, 64);
+        int splits = (int)ceil_div(4 * kCUs, col_blocks);
+        if (splits > 16) splits = 16;
+        if (splits > K) splits = K;
+        const double b = 4.0 * ((double)K * N + K + N);
+        record(op, "gemv_v4", kLaunchUs + b / (kHbm * kStreamEff) * 1e6 + (splits > 1 ? 1.0 : 0.0), flops, b);
+        return;
+    }
     if (batches == 1 && M == 1 && !b_kc) {
-        const int col_blocks = (int)ceil_div(N, N % 4 == 0 ? 1024 : 256);
+        const int col_blocks = (int)ceil_div(N, 256);
         int splits = (int)ceil_div(4 * kCUs, col_blocks);
         if (splits > ceil_div(K, 16)) splits = (int)ceil_div(K, 16);
         if (splits < 1) splits = 1;
-        record(op, N % 4 == 0 ? "gemv_xc_v4" : "gemv_xc_s1",
+        record(op, "gemv_xc_s1",
                kLaunchUs + 4.0 * ((double)K * N + K + (double)N * splits) / (kHbm * kStreamEff) * 1e6, flops,
                4.0 * K * N);
         return stream_kernel(op, "gemv_reduce", 4.0 * N * (splits + 1));

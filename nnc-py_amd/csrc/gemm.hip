@@ -593,6 +593,87 @@ __global__ void __launch_bounds__(256) gemv_reduce_k(GemmArgs g) {
         g.out[j] = gemm_finish(g, 0, j, ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]);
 }
 
+// One output row, B row-major (MatMul [1, K] x [K, N]), in one launch:
+// grid (ceil(N / 64), S), workgroup (c, s) takes columns 64c .. 64c + 63
+// over rows k_per s ..: thread t owns the four columns 64c + 4 (t % 16) on
+// row lane t / 16, i.e. rows kb + t / 16 + 16 i (a wave reads four 256-byte
+// row segments per load), with UN rows' 16-byte loads in flight; the 16 row
+// lanes' sums are added in row-lane order through LDS. S == 1: that sum is
+// the output. Otherwise the workgroup stores its 256-byte partial (device
+// scope) and the last of the column block's S workgroups to arrive
+// (finish_arrive, the stream-K protocol of mfma_tile.h) adds the S partials
+// in split order, so the sum is the same whichever workgroup finishes.
+// At most kGemvMaxSplits workgroups arrive at one counter (64 on one
+// counter measured 6 us slower than the two-launch form). Needs N % 4 == 0
+// and 16-byte aligned B rows.
+constexpr int kGemvMaxSplits = 16;
+typedef unsigned int gemv_u32x4 __attribute__((ext_vector_type(4)));
+
+template <int UN>
+__global__ void __launch_bounds__(256) gemv_fin_k(GemmArgs g, int64_t a_stride, int S, int k_per) {
+    __shared__ f32x4 red[16][16];
+    const int t = threadIdx.x, c4 = t & 15, rr = t >> 4;
+    const int c = blockIdx.x, s = blockIdx.y;
+    const int j = c * 64 + 4 * c4;
+    const int kb = s * k_per, ke = min(g.K, kb + k_per);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (j < g.N) {
+        const float* col = g.B + j;
+        int k = kb + rr;
+        for (; k + 16 * (UN - 1) < ke; k += 16 * UN) {
+            f32x4 b[UN];
+            float av[UN];
+#pragma unroll
+            for (int u = 0; u < UN; ++u) {
+                b[u] = *reinterpret_cast<const f32x4*>(col + (int64_t)(k + 16 * u) * g.ldb);
+                av[u] = g.A[(int64_t)(k + 16 * u) * a_stride];
+            }
+#pragma unroll
+            for (int u = 0; u < UN; ++u) {
+                acc.x += av[u] * b[u].x;
+                acc.y += av[u] * b[u].y;
+                acc.z += av[u] * b[u].z;
+                acc.w += av[u] * b[u].w;
+            }
+        }
+        for (; k < ke; k += 16) {
+            const f32x4 b = *reinterpret_cast<const f32x4*>(col + (int64_t)k * g.ldb);
+            const float av = g.A[(int64_t)k * a_stride];
+            acc.x += av * b.x;
+            acc.y += av * b.y;
+            acc.z += av * b.z;
+            acc.w += av * b.w;
+        }
+    }
+    red[rr][c4] = acc;
+    __syncthreads();
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (t < 16) {
+        v = red[0][t];
+#pragma unroll
+        for (int q = 1; q < 16; ++q) v += red[q][t];
+    }
+    if (S > 1) {
+        const __amdgpu_buffer_rsrc_t rws = make_rsrc(g.ws);
+        const uint32_t base = (uint32_t)c * (uint32_t)S * 256u;
+        if (t < 16)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gemv_u32x4, v), rws,
+                                                   (int)(base + (uint32_t)s * 256u + (uint32_t)t * 16u), 0, kDeviceScope);
+        if (!finish_arrive(g.cnt + c, S - 1)) return;  // uniform
+        // thread t: partial t / 16, float4 t % 16 (red was read before
+        // finish_arrive's barriers)
+        if (t < 16 * S) red[rr][c4] = load_partial4(rws, base + (uint32_t)t * 16u);
+        __syncthreads();
+        if (t < 16) {
+            v = red[0][t];
+            for (int q = 1; q < S; ++q) v += red[q][t];
+        }
+    }
+    if (t >= 16 || j >= g.N) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) g.out[j + q] = gemm_finish(g, 0, j + q, v[q]);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -1018,6 +1099,33 @@ static void gemm_run(const GemmProblem& p, const char* name) {
         // one output row, B row-major: stream B once
         const int64_t a_stride = p.a_kc ? 1 : p.lda;
         const bool vec = aligned16(p.B) && p.ldb % 4 == 0 && p.N % 4 == 0;
+        if (vec) {
+            // one launch, the K splits finished in the kernel (gemv_fin_k):
+            // about four workgroups per CU, at most kGemvMaxSplits splits
+            const int col_blocks = (int)ceil_div(p.N, 64);
+            int S = (int)ceil_div(4 * cu_count(), col_blocks);
+            if (S > kGemvMaxSplits) S = kGemvMaxSplits;
+            if (S > p.K) S = p.K;
+            if (S < 1) S = 1;
+            const int k_per = (int)ceil_div(p.K, S);
+            S = (int)ceil_div(p.K, k_per);
+            bool ok = true;
+            if (S > 1) {
+                g.ws = workspace((size_t)col_blocks * S * 256);
+                g.cnt = g.ws ? tile_counters((size_t)col_blocks) : nullptr;
+                ok = g.cnt != nullptr;
+                if (ok && ts().fixed)
+                    launch("zero_tile_counters", gemm_zero_counters_k, dim3((unsigned)ceil_div(col_blocks, 256)),
+                           dim3(256), 0, g.cnt, col_blocks);
+            }
+            if (ok) {
+                set_work(2.0 * p.K * (double)p.N, 4.0 * ((double)p.K * p.N + p.K + p.N));
+                launch("gemv_v4", gemv_fin_k<8>, dim3(col_blocks, S), dim3(256), 0, g, a_stride, S, k_per);
+                return;
+            }
+            g.ws = nullptr;
+            g.cnt = nullptr;
+        }
         const int cols_per_block = vec ? 1024 : 256;
         const int col_blocks = (int)ceil_div(p.N, cols_per_block);
         int splits = (int)ceil_div(4 * cu_count(), col_blocks);

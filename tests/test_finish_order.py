@@ -185,9 +185,9 @@ def test_finish_protocol_order_in_library(tmp_path, pkg):
     finishing = {k: v for k, v in kernels.items() if any(COUNTER_RMW.match(l) for l in v)}
     families = {re.match(r"_ZN3nnc\d+(\w+?_k)", k).group(1) for k in finishing}
     # the GEMM's and the convolution's direct-to-LDS kernels and the short
-    # products' kernels finish split tiles in-kernel, the stem's pool its
-    # range boundaries
-    assert {"gemm_dma_k", "gemm_ws_k", "conv_dma_k", "conv_ws_k", "conv_stem_pool_k"} <= families, families
+    # products' kernels finish split tiles in-kernel, the GEMV its K splits,
+    # the stem's pool its range boundaries
+    assert {"gemm_dma_k", "gemm_ws_k", "gemv_fin_k", "conv_dma_k", "conv_ws_k", "conv_stem_pool_k"} <= families, families
     for name, lines in finishing.items():
         try:
             check_finish_order(lines)

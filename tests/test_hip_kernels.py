@@ -420,6 +420,16 @@ GEMM_SHAPES = [
     (256, 256, 4096, 0, 1, True),
     (100, 70, 3000, 0, 0, False),
     (96, 160, 2500, 1, 0, True),
+    # one output row, B row-major (gemv_fin_k): 16 K splits finished in the
+    # kernel, a column block past N (1000 = 15 x 64 + 40), 13 splits of 3
+    # rows (fewer rows than row lanes), 8 splits over 128 column blocks, no
+    # split (4688 column blocks); N % 4 != 0 keeps the two-launch path
+    (1, 4096, 4096, 0, 0, True),
+    (1, 1000, 512, 0, 0, True),
+    (1, 260, 37, 0, 0, False),
+    (1, 8192, 100, 0, 0, True),
+    (1, 300000, 8, 0, 0, True),
+    (1, 333, 100, 0, 0, True),
 ]
 
 
@@ -438,11 +448,12 @@ def test_gemm_layouts_and_streamk(shape, hip, dmem, abi, oracle_lib):
 # tiles at one workgroup per CU, 192 tiles of 32 slices) and 2048x1024x256
 # (128x128 tiles, 128 tiles of 8 slices); the short-product kernels' tiles
 # split over 8 workgroups (conv 512 channels 3x3 over 7x7, GEMM
-# 256x256x4096); and the stem's fused max pool at 10 x 224x224, whose 512
+# 256x256x4096); the GEMV's 16 K splits of each 64-column block (1 x 1000
+# x 4096); and the stem's fused max pool at 10 x 224x224, whose 512
 # ranges of two or three conv rows finish the pool rows they share with
 # their neighbours in the kernel.
 IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "conv_ws_b1_512c_7", "gemm_1024x768x1024", "gemm_2048x1024x256",
-                          "gemm_ws_256x256x4096", "stem_pool_b10"]
+                          "gemm_ws_256x256x4096", "gemv_1x1000x4096", "stem_pool_b10"]
 
 
 @pytest.mark.parametrize("which", IN_KERNEL_FINISH_CASES)
@@ -460,6 +471,8 @@ def test_in_kernel_finish_alternating_inputs(which, hip, dmem, abi, oracle_lib):
             return _packed_case(rng, 1, 512, 7, 512, 3, 1, 1)
         if which == "stem_pool_b10":
             return _conv_maxpool_case(rng, 10, 224, 224, 64, True)
+        if which == "gemv_1x1000x4096":
+            return _gemm_case(rng, 1, 1000, 4096, 0, 0, True)
         m, n, k = {"gemm_1024x768x1024": (1024, 768, 1024), "gemm_2048x1024x256": (2048, 1024, 256),
                    "gemm_ws_256x256x4096": (256, 256, 4096)}[which]
         return _gemm_case(rng, m, n, k, 0, 1, True)
