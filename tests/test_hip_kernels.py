@@ -223,17 +223,35 @@ def test_conv_ws_epilogues(act, bias, res, hip, dmem, abi, oracle_lib):
         _check(got, exp, case["name"])
 
 
-@pytest.mark.parametrize("n,h", [(2, 64), (1, 224), (3, 37), (5, 224), (16, 64)])
+@pytest.mark.parametrize("n,h", [(2, 64), (1, 224), (3, 37), (2, 224), (1, 560), (5, 224), (16, 64)])
 def test_conv_packed_stem(n, h, hip, dmem, abi, oracle_lib):
     """3-channel 7x7 stride-2 stem on [Co][Kp] rows (K = 147 padded to 160):
-    64x128 tiles from 4096 output pixels, 64x64 below; from 512 output rows
-    on (5 x 224x224, 16 x 64x64) the row kernel with its input window in
-    LDS."""
+    64x64 tiles (2 x 64x64, 1 x 224x224, 3 x 37x37, 2 x 224x224), 64x128
+    tiles from 65536 output pixels (1 x 560x560: 280 rows); from 512 output
+    rows on (5 x 224x224, 16 x 64x64) the row kernel with its input window
+    in LDS."""
     rng = np.random.default_rng(23)
     case = _packed_case(rng, n, 3, h, 64, 7, 2, 3, res=False)
     w = case["tensors"]["w"]  # [Co][7][7][3]
     rows = np.zeros((64, 160), np.float32)
     rows[:, :147] = w.reshape(64, 147)
+    case["tensors"]["w"] = rows
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    _check(got, exp, case["name"])
+
+
+@pytest.mark.parametrize("n,h,co,act,bias", [(1, 224, 40, 2, False), (1, 64, 16, 1, True), (2, 96, 64, 0, True)])
+def test_conv_stem_tile_epilogues(n, h, co, act, bias, hip, dmem, abi, oracle_lib):
+    """The stem on 64x64 tiles with fewer output channels than a tile's 64
+    rows (40, 16: weight rows past Co read as zeros, their stores skipped),
+    each activation, with and without bias."""
+    rng = np.random.default_rng(31)
+    case = _packed_case(rng, n, 3, h, co, 7, 2, 3, act=act, bias=bias, res=False)
+    w = case["tensors"]["w"]
+    rows = np.zeros((co, 160), np.float32)
+    rows[:, :147] = w.reshape(co, 147)
     case["tensors"]["w"] = rows
     print(f"case {case['name']}", flush=True)
     exp = caserun.run_case(oracle_lib, case, abi)["out"]
