@@ -139,6 +139,8 @@ struct ConvGather {
     }
 };
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 // Bias (+ residual) + act for 4 consecutive output pixels p0..p0+3 of
 // channel co (one row of a tile), float4 when they are in one image and the
 // output (and residual) are 16-byte aligned. Split into the loads
@@ -223,6 +225,53 @@ __device__ void conv_finish_tile(const ConvArgs& a, int t, int g0, int g1, int f
     const __amdgpu_buffer_rsrc_t rws = make_rsrc(a.ws);
     const int mt = t % a.tiles_m, nt = t / a.tiles_m;
     const uint32_t first = slot_byte_offset<T>(g0, first_slot);
+    const int hw = a.Ho * a.Wo;
+    if (a.out32 && a.vec_out && (hw & 3) == 0) {
+        // Every float4 of a chunk inside the output (Npix is a multiple of
+        // 4 here): its bias and residual loads go out first and its partials'
+        // after them, so one wait covers the chunk's loads (they complete in
+        // order) - one memory round trip per chunk where loading the bias and
+        // residual after the sum took two. Out-of-range offsets read 0 and
+        // drop the stores. Same operations in the same order as fixup_apply.
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias), rr = make_rsrc(a.res), ro = make_rsrc(a.out);
+        for (int e0 = 0; e0 < E; e0 += CH) {
+            uint32_t off[CH];
+            float b[CH];
+            f32x4 r[CH], v[CH];
+#pragma unroll
+            for (int e = 0; e < CH; ++e) {
+                const int e4 = (e0 + e) * 256 + threadIdx.x;
+                const int co = mt * T::BM + (e4 * 4) / T::BN;
+                const int p0 = nt * T::BN + (e4 * 4) % T::BN;
+                const bool ok = co < a.Co && p0 < a.Npix;
+                const int n = p0 / hw;
+                off[e] = ok ? (uint32_t)((n * a.Co + co) * hw + (p0 - n * hw)) * 4u : kOutOfRange;
+                b[e] = load_f32(rb, a.bias && ok ? (uint32_t)co * 4u : kOutOfRange);
+                r[e] = load_f32x4(rr, a.res ? off[e] : kOutOfRange);
+            }
+#pragma unroll
+            for (int e = 0; e < CH; ++e)
+                v[e] = load_partial4(rws, first + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u);
+            for (int g = g0 + 1; g <= g1; ++g) {
+                const uint32_t base = slot_byte_offset<T>(g, 0);
+                f32x4 p[CH];
+#pragma unroll
+                for (int e = 0; e < CH; ++e)
+                    p[e] = load_partial4(rws, base + (uint32_t)((e0 + e) * 256 + threadIdx.x) * 16u);
+#pragma unroll
+                for (int e = 0; e < CH; ++e) v[e] += p[e];
+            }
+#pragma unroll
+            for (int e = 0; e < CH; ++e) {
+                f32x4 x = v[e] + b[e];
+                if (a.res) x += r[e];
+                const f32x4 y = {activate(x[0], a.act), activate(x[1], a.act), activate(x[2], a.act),
+                                 activate(x[3], a.act)};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, (int)off[e], 0, 0);
+            }
+        }
+        return;
+    }
     for (int e0 = 0; e0 < E; e0 += CH) {
         // a chunk of one partial's loads in flight at once, partial after partial
         f32x4 v[CH];
@@ -862,7 +911,6 @@ __global__ void __launch_bounds__(T::THREADS, DmaStage<T>::MIN_WAVES) conv_dma_k
 // whichever workgroup finishes: deterministic. Every shared tile is finished
 // in the launch: no fixup kernel.
 // ---------------------------------------------------------------------------
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // One 16-byte partial, stored with device-scope coherence.
 __device__ __forceinline__ void store_partial4(__amdgpu_buffer_rsrc_t ws, uint32_t byte_off, f32x4 v) {
