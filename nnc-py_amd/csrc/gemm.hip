@@ -945,6 +945,29 @@ __global__ void __launch_bounds__(256, 2) gemm_ws_k(GemmArgs g, int S, int iters
     const bool iok = i < g.M, jok = j < g.N;
     const int lda = (int)g.lda, ldb = (int)g.ldb;
 
+    // The C values of this thread's four outputs after the reduction below
+    // (tile row t / 8, columns 4 (t % 8) ..), loaded ahead of the operands,
+    // so the epilogue waits for no load (a split tile's finish for its
+    // partials only): straight-line buffer loads from C's one base, the row
+    // chosen once (C[j] or C[oi*N + j]; per element through gemm_finish,
+    // hipcc 7.2 addressed elements 1..3 of a bias row at C + oi*N, past the
+    // end of C), out-of-range offsets reading 0. A branch around per-element
+    // loads, or loads between the operands', rescheduled the operand loads.
+    // The epilogue loads C itself where its offsets would not fit 32 bits
+    // (never within this kernel's 1 GFLOP limit).
+    const int row = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
+    const int oi = i0 + row;
+    const bool has_c = g.c_mode != 0;
+    const bool pre_c = has_c && (int64_t)g.M * g.N < ((int64_t)1 << 29);
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(g.C);
+    const uint32_t crow = g.c_mode == 2 ? (uint32_t)oi * (uint32_t)g.N : 0u;
+    float cv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int oj = j0 + c4 + e;
+        cv[e] = load_f32(rc, pre_c && oi < g.M && oj < g.N ? (crow + (uint32_t)oj) * 4u : kOutOfRange);
+    }
+
     float av[NS][16], bv[NS][16];
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
@@ -996,7 +1019,6 @@ __global__ void __launch_bounds__(256, 2) gemm_ws_k(GemmArgs g, int S, int iters
         red[wave][(8 * (r >> 2) + 4 * h + (r & 3)) * 32 + l32] = x;
     }
     __syncthreads();
-    const int row = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
     f32x4 v = *reinterpret_cast<const f32x4*>(&red[0][row * 32 + c4]);
 #pragma unroll
     for (int w = 1; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(&red[w][row * 32 + c4]);
@@ -1016,20 +1038,19 @@ __global__ void __launch_bounds__(256, 2) gemm_ws_k(GemmArgs g, int S, int iters
             if (q < S) sum += q == part ? v : p[q];
         v = sum;
     }
-    const int oi = i0 + row;
     if (oi >= g.M) return;
     float* o = g.out + batch * g.so + (int64_t)oi * g.N;
-    // The C row is chosen once (C[j] or C[oi*N + j]) rather than per element
-    // through gemm_finish: with the per-element form, hipcc 7.2 addressed
-    // elements 1..3 of a bias row (c_mode 1) at C + oi*N, past the end of C.
-    const float* crow = g.C + (g.c_mode == 2 ? (int64_t)oi * g.N : (int64_t)0);
-    const bool has_c = g.c_mode != 0;
+    if (has_c && !pre_c) {
+        const float* cr = g.C + (g.c_mode == 2 ? (int64_t)oi * g.N : (int64_t)0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cv[e] = j0 + c4 + e < g.N ? cr[j0 + c4 + e] : 0.f;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int oj = j0 + c4 + e;
         if (oj < g.N) {
             float x = g.alpha * v[e];
-            if (has_c) x += g.beta * crow[oj];
+            if (has_c) x += g.beta * cv[e];
             if (g.relu) x = x > 0.0f ? x : 0.0f;
             o[oj] = x;
         }

@@ -214,8 +214,11 @@ def test_conv_ws_shapes(shape, hip, dmem, abi, oracle_lib):
 @pytest.mark.parametrize("bias,res", [(True, True), (False, True), (True, False), (False, False)])
 def test_conv_ws_epilogues(act, bias, res, hip, dmem, abi, oracle_lib):
     """Each activation, with and without bias and residual, on a whole tile
-    (S = 1) and a split one (S = 8)."""
-    for shape in ((1, 64, 12, 64, 3, 1, 1), (1, 512, 7, 512, 3, 1, 1)):
+    (S = 1) and a split one (S = 8); then on images whose pixel count is not
+    a multiple of 4 (a thread's four pixels reach into the next image: 3 x
+    7x7, 5 x 3x3) and on 1-pixel images (8 x 1x1 outputs)."""
+    for shape in ((1, 64, 12, 64, 3, 1, 1), (1, 512, 7, 512, 3, 1, 1), (3, 64, 7, 64, 3, 1, 1),
+                  (5, 32, 3, 64, 3, 1, 1), (8, 32, 3, 64, 3, 1, 0)):
         case = _packed_case(np.random.default_rng(43), *shape, act=act, bias=bias, res=res)
         print(f"case {case['name']}", flush=True)
         exp = caserun.run_case(oracle_lib, case, abi)["out"]
@@ -454,6 +457,25 @@ GEMM_SHAPES = [
 @pytest.mark.parametrize("shape", GEMM_SHAPES, ids=[str(s) for s in GEMM_SHAPES])
 def test_gemm_layouts_and_streamk(shape, hip, dmem, abi, oracle_lib):
     case = _gemm_case(np.random.default_rng(3), *shape)
+    print(f"case {case['name']}", flush=True)
+    exp = caserun.run_case(oracle_lib, case, abi)["out"]
+    got = caserun.run_case(hip, case, abi, dmem)["out"]
+    _check(got, exp, case["name"])
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 200, 777), (256, 256, 4096), (37, 45, 64)])
+@pytest.mark.parametrize("c_shape", ["row", "matrix"])
+def test_gemm_short_product_c_and_scales(m, n, k, c_shape, hip, dmem, abi, oracle_lib):
+    """alpha * A B + beta * C on the short-product kernel (gemm_ws_k: whole
+    32x32 tiles, tiles split over 8 workgroups, M and N tails), C a row of N
+    (C[j]) or a whole [M, N] matrix (C[i*N + j]), against the oracle."""
+    rng = np.random.default_rng(29)
+    case = _gemm_case(rng, m, n, k, 0, 1, True)
+    if c_shape == "matrix":
+        case["tensors"]["c"] = rng.uniform(-1, 1, (m, n)).astype(np.float32)
+    case["args"][4] = ("f", 0.5)
+    case["args"][5] = ("f", -2.0)
+    case["name"] += f"_c{c_shape}"
     print(f"case {case['name']}", flush=True)
     exp = caserun.run_case(oracle_lib, case, abi)["out"]
     got = caserun.run_case(hip, case, abi, dmem)["out"]
