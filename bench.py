@@ -188,7 +188,11 @@ class ClockSampler:
 
 
 def kernel_table(ex, runtime, steps: int) -> list[dict]:
-    """Per-kernel averages over `steps` directly launched nnc_run() calls."""
+    """Per-kernel averages over `steps` directly launched nnc_run() calls
+    (after one untimed call: the replays before it ran the same kernels from
+    a graph)."""
+    ex.run()
+    runtime.sync()
     runtime.profile_reset()
     runtime.profile_enable(True)
     for _ in range(steps):
@@ -639,7 +643,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-graph", action="store_true", help="launch each nnc_* call instead of a hipGraph")
-    ap.add_argument("--profile-steps", type=int, default=5)
+    ap.add_argument("--profile-steps", type=int, default=20)
     ap.add_argument("--latency-batches", default="1,8,16,32",
                     help="batches timed per step as the reference harness does (mean/p50/p95; '' skips)")
     ap.add_argument("--clock-seconds", type=float, default=1.0,
