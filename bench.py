@@ -670,9 +670,9 @@ def main() -> int:
         return run_suite()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU: this build runs the nnc program on a single MI355X "
+        print(f"bench.py measures one GPU: the nnc program runs on a single MI355X "
               f"(--gpus {args.gpus}, WORLD_SIZE {world} requested); multi-GPU batch sharding is "
-              f"described in DESIGN.md and not launched.", file=sys.stderr)
+              f"not launched.", file=sys.stderr)
         return 2
 
     pkg = load_package()

@@ -1,7 +1,7 @@
 """libnnc_hip.so against the reference's golden vectors, every case, through the
 C-ABI. Bar: bit-exact for data movement / integer / comparison ops and the
 ops whose arithmetic order is reproduced exactly; otherwise the reference's
-pass rule with BASELINE's bar: |got - ref| <= 1e-4 or <= 1e-3 * |ref|."""
+pass rule with the floating-point bar: |got - ref| <= 1e-4 or <= 1e-3 * |ref|."""
 
 from __future__ import annotations
 
