@@ -3,7 +3,7 @@
  * (runtime/x86/ops.c) behind the same nnc_* ABI (include/nnc_ops.h), on HOST
  * pointers.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: tests/, the smoke()
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle: tests/, the smoke()
  * hook and bench.py's cpu_baseline leg load it to produce expected values or
  * to time the CPU baseline. The product (libnnc_hip.so) never links, loads or
  * falls back to it.

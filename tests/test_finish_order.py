@@ -115,7 +115,7 @@ def test_finish_protocol_order_in_probe_kernel(tmp_path):
 
 
 def test_check_rejects_a_missing_wait():
-    """The checker fails an order with the stores' completion wait dropped
+    """check_finish_order fails an order with the stores' completion wait dropped
     or a partial load hoisted above the barrier."""
     good = ["buffer_store_dword v1, v2, s[0:3], 0 offen sc1", "s_waitcnt vmcnt(0)", "s_barrier",
             "global_atomic_add v1, v2, v3, s[4:5] sc0", "s_waitcnt vmcnt(0)", "ds_write_b32 v1, v2",
