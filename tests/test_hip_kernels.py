@@ -483,8 +483,11 @@ def test_gemm_short_product_c_and_scales(m, n, k, c_shape, hip, dmem, abi, oracl
 
 
 # Shapes whose split tiles are finished inside the kernel by the last of
-# their workgroups: 64 channels 3x3 over 8 x 56x56 (direct-to-LDS 64x128
-# tiles, 196 tiles of 18 slices), GEMM 1024x768x1024 (direct-to-LDS 64x64
+# their workgroups (no fixup launch, checked): 64 channels 3x3 with a
+# residual over 12 x 56x56 (direct-to-LDS 64x128 tiles, 294 tiles of 18
+# slices on 768 workgroups, at most 4 contributors per tile; 16-byte
+# finish) and 11 x 57x57 (images of an odd pixel count: the finish's
+# per-element path), GEMM 1024x768x1024 (direct-to-LDS 64x64
 # tiles at one workgroup per CU, 192 tiles of 32 slices) and 2048x1024x256
 # (128x128 tiles, 128 tiles of 8 slices); the short-product kernels' tiles
 # split over 8 workgroups (conv 512 channels 3x3 over 7x7, GEMM
@@ -492,7 +495,7 @@ def test_gemm_short_product_c_and_scales(m, n, k, c_shape, hip, dmem, abi, oracl
 # x 4096); and the stem's fused max pool at 10 x 224x224, whose 512
 # ranges of two or three conv rows finish the pool rows they share with
 # their neighbours in the kernel.
-IN_KERNEL_FINISH_CASES = ["conv_b8_64c_56", "conv_ws_b1_512c_7", "gemm_1024x768x1024", "gemm_2048x1024x256",
+IN_KERNEL_FINISH_CASES = ["conv_b12_64c_56", "conv_b11_64c_57", "conv_ws_b1_512c_7", "gemm_1024x768x1024", "gemm_2048x1024x256",
                           "gemm_ws_256x256x4096", "gemv_1x1000x4096", "stem_pool_b10"]
 
 
@@ -505,8 +508,10 @@ def test_in_kernel_finish_alternating_inputs(which, hip, dmem, abi, oracle_lib):
     oracle, and calls on the same input match each other to the bit."""
     def make(seed):
         rng = np.random.default_rng(seed)
-        if which == "conv_b8_64c_56":
-            return _packed_case(rng, 8, 64, 56, 64, 3, 1, 1)
+        if which == "conv_b12_64c_56":
+            return _packed_case(rng, 12, 64, 56, 64, 3, 1, 1)
+        if which == "conv_b11_64c_57":
+            return _packed_case(rng, 11, 64, 57, 64, 3, 1, 1)
         if which == "conv_ws_b1_512c_7":
             return _packed_case(rng, 1, 512, 7, 512, 3, 1, 1)
         if which == "stem_pool_b10":
@@ -516,13 +521,21 @@ def test_in_kernel_finish_alternating_inputs(which, hip, dmem, abi, oracle_lib):
         m, n, k = {"gemm_1024x768x1024": (1024, 768, 1024), "gemm_2048x1024x256": (2048, 1024, 256),
                    "gemm_ws_256x256x4096": (256, 256, 4096)}[which]
         return _gemm_case(rng, m, n, k, 0, 1, True)
+    from nnc_py_amd import runtime
     cases = [make(41), make(42)]
     exp = [caserun.run_case(oracle_lib, c, abi)["out"] for c in cases]
     first = [None, None]
     for call in range(4):
         q = call % 2
         print(f"case {which} call {call} input {q}", flush=True)
+        runtime.profile_reset()
+        runtime.profile_enable(True)
         got = caserun.run_case(hip, cases[q], abi, dmem)["out"]
+        launched = {r["name"] for r in runtime.profile_table()}
+        runtime.profile_enable(False)
+        # the case exercises the in-kernel finish only while its plan keeps
+        # every shared tile within the finish's contributor limit
+        assert not any("fixup" in name for name in launched), sorted(launched)
         _check(got, exp[q], f"{which} call {call}")
         if first[q] is None:
             first[q] = got
