@@ -2,12 +2,14 @@
 nnc_hip_conv_packed (stream-K partials and tile counters in a static device
 array instead of the grow-only workspace).
 
-Two calls in a row through the C-ABI - a ResNet-18 batch-32 layer-2 shape
-(128x128 tiles, stream-K with a fixup launch) and then a smaller batch-2
-64-channel shape (64x128 tiles whose shared tiles are finished in-kernel
-through the static tile counters) - each equal bit for bit to
-nnc_hip_conv_packed on the same inputs (same kernels, same stream-K plan)
-and within 1e-4 abs / 1e-3 rel of the oracle. A thread without library state
+Three calls in a row through the C-ABI, each on a smaller input than the
+last - a ResNet-18 batch-32 layer-2 shape (128x128 tiles, stream-K with a
+fixup launch), a 12-image 64-channel shape (64x128 tiles whose shared tiles
+are finished in-kernel through the static tile counters) and a batch-1
+512-channel 7x7 shape (short-convolution tiles split over 8 workgroups,
+finished through the static counters too) - each equal bit for bit to
+nnc_hip_conv_packed on the same inputs (same kernels, same plans) and within
+1e-4 abs / 1e-3 rel of the oracle. A thread without library state
 gets NNC_HIP_ESTATE and no launch: the entry point never creates it. Calls
 from two host threads on their own streams are ordered on the device, so
 they do not race on the shared array.
@@ -28,17 +30,26 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [
     (32, 128, 28, 128, 3, 1, 1),  # 128x128 tiles, stream-K with the fixup kernel
-    (2, 64, 56, 64, 3, 1, 1),     # smaller: 64x128 tiles, in-kernel finish on the counters
+    (12, 64, 56, 64, 3, 1, 1),    # smaller: 64x128 tiles, in-kernel finish on the counters
+    (1, 512, 7, 512, 3, 1, 1),    # smaller still: short-convolution tiles split 8 ways, on the counters
 ]
 
 
 def test_noalloc_matches_conv_packed_twice(hip, dmem, abi, oracle_lib):
     from nnc_py_amd import runtime
     for i, shape in enumerate(SHAPES):
-        case = _packed_case(np.random.default_rng(20 + i), *shape, act=1, bias=True, res=i == 0)
+        case = _packed_case(np.random.default_rng(20 + i), *shape, act=1, bias=True, res=i != 2)
         print(f"no-alloc call {i}: {case['name']}", flush=True)
+        runtime.profile_reset()
+        runtime.profile_enable(True)
         want = caserun.run_case(hip, case, abi, dmem)["out"]
+        launched = {r["name"] for r in runtime.profile_table()}
+        runtime.profile_enable(False)
         assert runtime.last_error()[0] == 0, runtime.last_error()[1]
+        # the plan both entry points share: the first shape's tiles finished
+        # by the fixup kernel, the others' in their kernels on the counters
+        # (the no-alloc calls record no launch table)
+        assert any("fixup" in n for n in launched) == (i == 0), sorted(launched)
         fixed = dict(case, op="nnc_hip_conv_packed_noalloc")
         got = caserun.run_case(hip, fixed, abi, dmem)["out"]
         assert runtime.last_error()[0] == 0, runtime.last_error()[1]
